@@ -1,0 +1,389 @@
+"""Float64 numpy restatement of the reference's jnp/XLA triangle path.
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels, never the thing
+measured or shipped. The product package does not import it.
+
+Every function restates one reference function, cited as ``path:line``
+relative to the eightmm/FoldJAX checkout. All arithmetic is float64, so the
+result stands for the reference's fp32 computation (the parity bar in fp32
+mode is max-abs 1e-4; in bf16 mode the HIP output is compared with this on the
+same bf16-valued inputs and weights, relative error 2e-2).
+
+Parameter containers are plain dicts. Boltz-2 uses its own nested dict with
+``[in, out]`` kernels; Protenix and OpenFold3 use dicts keyed by the field
+names of their NamedTuples, with PyTorch ``[out, in]`` weights. Attribute
+access (NamedTuples) is accepted too, via ``_get``.
+
+Pinning (tests/test_oracle.py): brute-force Python loops on tiny shapes, the
+torch CPU library routines ``layer_norm`` and ``scaled_dot_product_attention``
+for the special cases that reduce to them, the three ports agreeing with one
+another under the documented weight mappings, and the reference's own
+invariants (incoming == transposed outgoing with a/b swapped, ending ==
+transposed starting, row-chunk invariance, padding isolation).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+F64 = np.float64
+
+
+def _get(obj, name):
+    """Field access for dict- or NamedTuple-shaped parameter containers."""
+    if isinstance(obj, dict):
+        return obj.get(name)
+    return getattr(obj, name, None)
+
+
+def _f(x):
+    return None if x is None else np.asarray(x, dtype=F64)
+
+
+# ---------------------------------------------------------------------------
+# Leaf primitives
+# ---------------------------------------------------------------------------
+
+
+def layer_norm(x, weight, bias, eps=1e-5):
+    """LayerNorm over the last axis.
+
+    Boltz-2 ``B2P/_common.py:15-26`` (fp32 stats, ``rsqrt``), Protenix
+    ``PXP/primitives.py:57-72`` and OpenFold3 ``OF3/primitives.py:81-97``
+    (``1/sqrt``) are the same function in exact arithmetic; the optional
+    weight/bias follow the Protenix/OpenFold3 containers.
+    """
+    x = _f(x)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = np.square(x - mean).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps)
+    if weight is not None:
+        y = y * _f(weight)
+    if bias is not None:
+        y = y + _f(bias)
+    return y
+
+
+def sigmoid(x):
+    """Logistic sigmoid, evaluated stably.
+
+    ``jax.nn.sigmoid`` (Boltz-2), ``1/(1+exp(-x))`` (``PXP/primitives.py:81-84``)
+    and the branchwise form (``OF3/primitives.py:105-111``) agree in float64.
+    """
+    x = _f(x)
+    e = np.exp(-np.abs(x))
+    return np.where(x >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+
+
+def silu(x):
+    """``x * sigmoid(x)`` (``PXP/primitives.py:75-78``, ``jax.nn.silu``)."""
+    x = _f(x)
+    return x * sigmoid(x)
+
+
+def linear_torch(x, lin):
+    """PyTorch-layout linear ``x @ W.T + b`` (``PXP/primitives.py:48-54``)."""
+    y = _f(x) @ _f(_get(lin, "weight")).T
+    b = _get(lin, "bias")
+    if b is not None:
+        y = y + _f(b)
+    return y
+
+
+def _ln_params(p):
+    return _get(p, "weight"), _get(p, "bias")
+
+
+def softmax(x, axis=-1):
+    """Max-subtracted softmax, as ``jax.nn.softmax``."""
+    x = _f(x)
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / e.sum(axis=axis, keepdims=True)
+
+
+# ---------------------------------------------------------------------------
+# Triangle contraction
+# ---------------------------------------------------------------------------
+
+
+def triangle_contract(a, b, direction):
+    """Per-channel contraction of two ``[..., N, N, C]`` projections.
+
+    outgoing: ``out[i,j,c] = sum_k a[i,k,c] b[j,k,c]``
+    incoming: ``out[i,j,c] = sum_k a[k,i,c] b[k,j,c]``
+    (``B2T/triangle.py:215-254``, ``PXT/triangle.py:399-416``,
+    ``OF3/triangle.py:64-79``). Written as a batched matmul over the channel
+    axis moved to the front, which is how OpenFold3 spells it.
+    """
+    a = _f(a)
+    b = _f(b)
+    ac = np.moveaxis(a, -1, -3)  # [..., C, N, N]
+    bc = np.moveaxis(b, -1, -3)
+    if direction == "outgoing":
+        out = ac @ np.swapaxes(bc, -1, -2)
+    elif direction == "incoming":
+        out = np.swapaxes(ac, -1, -2) @ bc
+    else:
+        raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
+    return np.moveaxis(out, -3, -1)
+
+
+# ---------------------------------------------------------------------------
+# Triangle multiplicative update
+# ---------------------------------------------------------------------------
+
+
+def boltz2_triangle_multiplication(params, x, mask, direction, eps=1e-5):
+    """Boltz-2 ``triangle_multiplication_forward`` XLA path.
+
+    ``B2T/triangle.py:78-129``: LN_in; sigmoid GLU ``sigmoid(x@g_in)*(x@p_in)``
+    (``B2P/glu_backend.py:73-74``); times mask; split into a (first c_h) and b;
+    contraction; LN_out; ``@p_out``; times ``sigmoid(x_ln @ g_out)``. Kernels
+    are ``[in, out]``. Returns the update; the caller adds it.
+    """
+    x = layer_norm(x, params["norm_in"]["scale"], params["norm_in"]["bias"], eps)
+    mask = _f(mask)
+    proj = sigmoid(x @ _f(params["g_in"]["kernel"])) * (x @ _f(params["p_in"]["kernel"]))
+    proj = proj * mask[..., None]
+    a, b = np.split(proj, 2, axis=-1)
+    out = triangle_contract(a, b, direction)
+    out = layer_norm(out, params["norm_out"]["scale"], params["norm_out"]["bias"], eps)
+    out = out @ _f(params["p_out"]["kernel"])
+    gate = sigmoid(x @ _f(params["g_out"]["kernel"]))
+    return out * gate
+
+
+def protenix_triangle_multiplication(z, mask, params, direction):
+    """Protenix ``triangle_multiplication`` XLA path.
+
+    ``PXT/triangle.py:166-228``: ``b = mask*sigmoid(lin(z_ln, b_g))*lin(z_ln, b_p)``,
+    a likewise (``project_a``, :198-200), contraction in float32, cast, LN_out,
+    ``linear_z``, times ``sigmoid(linear(z_ln, linear_g))``. LN eps is 1e-5.
+    """
+    z = _f(z)
+    if mask is None:
+        mask = np.ones(z.shape[:-1])
+    m = _f(mask)[..., None]
+    zn = layer_norm(z, *_ln_params(_get(params, "layer_norm_in")))
+    b = m * sigmoid(linear_torch(zn, _get(params, "linear_b_g")))
+    b = b * linear_torch(zn, _get(params, "linear_b_p"))
+    a = m * sigmoid(linear_torch(zn, _get(params, "linear_a_g")))
+    a = a * linear_torch(zn, _get(params, "linear_a_p"))
+    out = triangle_contract(a, b, direction)
+    out = layer_norm(out, *_ln_params(_get(params, "layer_norm_out")))
+    out = linear_torch(out, _get(params, "linear_z"))
+    return out * sigmoid(linear_torch(zn, _get(params, "linear_g")))
+
+
+def openfold3_triangle_multiplication(z, params, *, outgoing, mask=None, eps=1e-5):
+    """OpenFold3 ``triangle_multiplication`` (``OF3/triangle.py:82-134``).
+
+    Same function, with ``gate_mask = 1`` when the mask is ``None``; the
+    contraction is the channel-major matmul of ``combine_projections``
+    (``OF3/triangle.py:64-79``).
+    """
+    zn = layer_norm(z, *_ln_params(_get(params, "layer_norm_in")), eps=eps)
+    gm = 1.0 if mask is None else _f(mask)[..., None]
+    a = gm * sigmoid(linear_torch(zn, _get(params, "linear_a_g"))) * linear_torch(
+        zn, _get(params, "linear_a_p")
+    )
+    b = gm * sigmoid(linear_torch(zn, _get(params, "linear_b_g"))) * linear_torch(
+        zn, _get(params, "linear_b_p")
+    )
+    x = triangle_contract(a, b, "outgoing" if outgoing else "incoming")
+    x = layer_norm(x, *_ln_params(_get(params, "layer_norm_out")), eps=eps)
+    x = linear_torch(x, _get(params, "linear_z"))
+    return x * sigmoid(linear_torch(zn, _get(params, "linear_g")))
+
+
+# ---------------------------------------------------------------------------
+# Triangle attention
+# ---------------------------------------------------------------------------
+
+
+def attention_rows(q, k, v, mask_bias, tri_bias, row_block=16):
+    """Biased softmax attention for independent rows.
+
+    ``q, k, v``: ``[..., I, H, J, D]`` with q already scaled;
+    ``mask_bias``: ``[..., I, 1, 1, J]``; ``tri_bias``: ``[..., 1, H, J, J]``.
+    ``scores = q k^T + mask_bias + tri_bias``; softmax over keys; ``p v``
+    (``B2T/triangle_attention.py:428-455``, ``PXT/triangle.py:850-860``,
+    ``OF3/attention.py:54-67``). Rows are processed in blocks of
+    ``row_block``, which the reference shows is exact
+    (``B2T/triangle_attention.py:458-493``).
+    """
+    q, k, v = _f(q), _f(k), _f(v)
+    mask_bias, tri_bias = _f(mask_bias), _f(tri_bias)
+    n_rows = q.shape[-4]
+    out = np.empty(q.shape[:-1] + (v.shape[-1],))
+    for s in range(0, n_rows, row_block):
+        e = min(n_rows, s + row_block)
+        qs, ks, vs = q[..., s:e, :, :, :], k[..., s:e, :, :, :], v[..., s:e, :, :, :]
+        mb = mask_bias[..., s:e, :, :, :] if mask_bias.shape[-4] > 1 else mask_bias
+        scores = qs @ np.swapaxes(ks, -1, -2)
+        scores = scores + mb + tri_bias
+        out[..., s:e, :, :, :] = softmax(scores, axis=-1) @ vs
+    return out
+
+
+def _split_heads_torch(x, lin, heads):
+    """``[..., J, C] -> [..., H, J, D]`` (``PXT/triangle.py:863-870``)."""
+    y = linear_torch(x, lin)
+    y = y.reshape(y.shape[:-1] + (heads, -1))
+    return np.swapaxes(y, -2, -3)
+
+
+def boltz2_triangle_attention(params, x, mask=None, starting=True, inf=1e9, eps=1e-5):
+    """Boltz-2 ``triangle_attention_forward`` XLA path.
+
+    ``B2T/triangle_attention.py:125-162`` and ``_attention`` :346-425: ending
+    node swaps the two pair axes of x and mask in and out; LN; fp32
+    ``mask_bias = inf*(mask-1)`` as ``[..., I, 1, 1, J]``; ``tri_bias = x @ W``
+    moved to ``[..., 1, H, J, J]``; q,g from ``[W_q|W_g]``, k,v from
+    ``[W_k|W_v]``; ``q /= sqrt(D)``; softmax attention; ``sigmoid(g)`` gate;
+    ``@ W_o``. Kernels are ``[in, out]``.
+    """
+    x = _f(x)
+    if mask is None:
+        mask = np.ones(x.shape[:-1])
+    mask = _f(mask)
+    if not starting:
+        x = np.swapaxes(x, -2, -3)
+        mask = np.swapaxes(mask, -1, -2)
+    x = layer_norm(x, params["layer_norm"]["scale"], params["layer_norm"]["bias"], eps)
+    mask_bias = (inf * (mask - 1.0))[..., :, None, None, :]
+    tri_bias = x @ _f(params["linear"]["kernel"])  # [..., I, J, H]
+    tri_bias = np.moveaxis(tri_bias, -1, -3)[..., None, :, :, :]
+    mha = params["mha"]
+    heads = tri_bias.shape[-3]
+    d = _f(mha["linear_g"]["kernel"]).shape[-1] // heads
+
+    def proj(name):
+        y = x @ _f(mha[name]["kernel"])
+        y = y.reshape(y.shape[:-1] + (heads, d))
+        return np.swapaxes(y, -2, -3)
+
+    q = proj("linear_q") / np.sqrt(d)
+    k = proj("linear_k")
+    v = proj("linear_v")
+    o = attention_rows(q, k, v, mask_bias, tri_bias)
+    o = np.swapaxes(o, -2, -3)  # [..., I, J, H, D]
+    gate = sigmoid(x @ _f(mha["linear_g"]["kernel"])).reshape(o.shape)
+    o = (o * gate).reshape(o.shape[:-2] + (heads * d,))
+    out = o @ _f(mha["linear_o"]["kernel"])
+    if not starting:
+        out = np.swapaxes(out, -2, -3)
+    return out
+
+
+def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, inf=1e9):
+    """Protenix ``triangle_attention`` dense path.
+
+    ``PXT/triangle.py:509-535`` and ``_triangle_attention_dense`` :732-847:
+    same math as Boltz-2 with torch-layout weights, ``scale = D**-0.5``
+    multiplied into q (:792), and an optional ``linear_g``.
+    """
+    x = _f(x)
+    if mask is None:
+        mask = np.ones(x.shape[:-1])
+    mask = _f(mask)
+    if not starting:
+        x = np.swapaxes(x, -2, -3)
+        mask = np.swapaxes(mask, -1, -2)
+    x = layer_norm(x, *_ln_params(_get(params, "layer_norm")))
+    mask_bias = (inf * (mask - 1.0))[..., :, None, None, :]
+    tri_bias = linear_torch(x, _get(params, "linear"))
+    tri_bias = np.moveaxis(tri_bias, -1, -3)[..., None, :, :, :]
+    att = _get(params, "attention")
+    d = _f(_get(_get(att, "linear_k"), "weight")).shape[0] // num_heads
+    q = _split_heads_torch(x, _get(att, "linear_q"), num_heads) * (float(d) ** -0.5)
+    k = _split_heads_torch(x, _get(att, "linear_k"), num_heads)
+    v = _split_heads_torch(x, _get(att, "linear_v"), num_heads)
+    o = np.swapaxes(attention_rows(q, k, v, mask_bias, tri_bias), -2, -3)
+    if _get(att, "linear_g") is not None:
+        o = o * sigmoid(linear_torch(x, _get(att, "linear_g"))).reshape(o.shape)
+    o = o.reshape(o.shape[:-2] + (-1,))
+    out = linear_torch(o, _get(att, "linear_o"))
+    if not starting:
+        out = np.swapaxes(out, -2, -3)
+    return out
+
+
+def openfold3_triangle_attention(x, params, *, no_heads, mask=None, starting=True, inf=1e9, eps=1e-5):
+    """OpenFold3 ``triangle_attention`` (``OF3/triangle_attention.py:159-195``).
+
+    Biases are added in the order ``(mask_bias, triangle_bias)``
+    (``OF3/attention.py:64-66``); ``query / sqrt(D)`` (``OF3/attention.py:100``);
+    the gate multiplies the ``[..., J, H, D]`` output (:106-108).
+    """
+    x = _f(x)
+    if mask is None:
+        mask = np.ones(x.shape[:-1])
+    mask = _f(mask)
+    if not starting:
+        x = np.swapaxes(x, -2, -3)
+        mask = np.swapaxes(mask, -1, -2)
+    x = layer_norm(x, *_ln_params(_get(params, "layer_norm")), eps=eps)
+    mask_bias = (inf * (mask - 1.0))[..., :, None, None, :]
+    tri_bias = np.moveaxis(linear_torch(x, _get(params, "linear_z")), -1, -3)[..., None, :, :, :]
+    mha = _get(params, "mha")
+    q = _split_heads_torch(x, _get(mha, "linear_q"), no_heads)
+    q = q / np.sqrt(q.shape[-1])
+    k = _split_heads_torch(x, _get(mha, "linear_k"), no_heads)
+    v = _split_heads_torch(x, _get(mha, "linear_v"), no_heads)
+    o = np.swapaxes(attention_rows(q, k, v, mask_bias, tri_bias), -2, -3)
+    if _get(mha, "linear_g") is not None:
+        o = o * sigmoid(linear_torch(x, _get(mha, "linear_g"))).reshape(o.shape)
+    out = linear_torch(o.reshape(o.shape[:-2] + (-1,)), _get(mha, "linear_o"))
+    if not starting:
+        out = np.swapaxes(out, -2, -3)
+    return out
+
+
+def attention_core(q, k, v, tri_bias, mask_bias, scale):
+    """The kernel-boundary core: ``cueq_attention_core`` semantics.
+
+    ``M/_cueq.py:66-121``: q/k/v ``[B, I, H, J, D]``, ``tri_bias``
+    ``[B, 1, H, J, J]``, additive ``mask_bias`` ``[B, I, 1, 1, J]``; ``scale``
+    applied inside. Returns ``[B, I, H, J, D]``.
+    """
+    return attention_rows(_f(q) * scale, k, v, mask_bias, tri_bias)
+
+
+# ---------------------------------------------------------------------------
+# Weight mappings between the three ports (test helpers)
+# ---------------------------------------------------------------------------
+
+
+def trimul_torch_to_boltz2(p):
+    """Protenix/OpenFold3 tri-mul fields -> Boltz-2 dict.
+
+    Boltz-2's fused ``p_in``/``g_in`` are ``[c_z, 2c_h]`` with the a half first
+    (``B2T/triangle.py:102``; torch layout ``[2c_h, c_z]`` per
+    ``B2T/triangle_cueq.py:94-95``).
+    """
+    w = lambda name: _f(_get(_get(p, name), "weight"))  # noqa: E731
+    lin = _get(p, "layer_norm_in")
+    lout = _get(p, "layer_norm_out")
+    return {
+        "norm_in": {"scale": _f(_get(lin, "weight")), "bias": _f(_get(lin, "bias"))},
+        "p_in": {"kernel": np.concatenate([w("linear_a_p"), w("linear_b_p")], 0).T},
+        "g_in": {"kernel": np.concatenate([w("linear_a_g"), w("linear_b_g")], 0).T},
+        "norm_out": {"scale": _f(_get(lout, "weight")), "bias": _f(_get(lout, "bias"))},
+        "p_out": {"kernel": w("linear_z").T},
+        "g_out": {"kernel": w("linear_g").T},
+    }
+
+
+def triattn_torch_to_boltz2(p, *, bias_name="linear", mha_name="attention"):
+    """Protenix (``linear``/``attention``) or OpenFold3 (``linear_z``/``mha``)
+    tri-attn fields -> Boltz-2 dict (``M/boltz2/bridge/torch_mapping.py:553-600``)."""
+    ln = _get(p, "layer_norm")
+    mha = _get(p, mha_name)
+    k = lambda lin: _f(_get(lin, "weight")).T  # noqa: E731
+    return {
+        "layer_norm": {"scale": _f(_get(ln, "weight")), "bias": _f(_get(ln, "bias"))},
+        "linear": {"kernel": k(_get(p, bias_name))},
+        "mha": {n: {"kernel": k(_get(mha, n))} for n in ("linear_q", "linear_k", "linear_v", "linear_o", "linear_g")},
+    }

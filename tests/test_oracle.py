@@ -1,0 +1,253 @@
+"""Pins for the CPU oracle (oracle/triangle.py), independent of any GPU.
+
+Each check is chosen so that a plausible mistake in the oracle fails it:
+brute-force loops (tests/_brute.py) catch transposed operands and wrong
+indices; torch's CPU ``layer_norm`` and ``scaled_dot_product_attention`` pin
+the special cases that reduce to library routines; the reference's own
+invariants (``T/models/protenix/test_triangle.py:142-166`` ending == transposed
+starting, ``T/models/openfold3/test_torch_parity_triangle.py:96-106``
+outgoing != incoming, ``T/models/protenix/test_pairformer.py:91-132`` padding
+isolation, ``T/models/boltz2/test_triangle_attention_chunk_parity.py:43-69``
+chunk invariance) pin what the loops leave open at larger sizes. The
+``planted`` tests show that mistakes planted into the oracle are caught.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from foldjax_amd import synthetic as syn
+from oracle import triangle as O
+from tests import _brute as B
+
+
+def _of3_attn(p):
+    return {"layer_norm": p["layer_norm"], "linear_z": p["linear"], "mha": p["attention"]}
+
+
+def _small(seed=0, n=3, c_z=4, c_h=5, heads=2, d=3):
+    rng = np.random.default_rng(seed)
+    z = rng.standard_normal((n, n, c_z))
+    mask = rng.integers(0, 2, size=(n, n)).astype(np.float64)
+    mask[0, :] = 1.0  # keep at least one valid key per row for the brute softmax
+    tm = syn.trimul_weights(c_z, c_h, seed=seed + 10)
+    ta = syn.triattn_weights(c_z, heads, d, seed=seed + 20)
+    return z, mask, tm, ta
+
+
+# --------------------------------------------------------------- brute force
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_matches_brute_force(direction):
+    z, mask, tm, _ = _small(seed=1)
+    want = np.array(B.trimul(z.tolist(), mask.tolist(), B.tolist(tm), direction == "outgoing"))
+    got_px = O.protenix_triangle_multiplication(z, mask, tm, direction)
+    got_of = O.openfold3_triangle_multiplication(z, tm, outgoing=direction == "outgoing", mask=mask)
+    got_b2 = O.boltz2_triangle_multiplication(O.trimul_torch_to_boltz2(tm), z, mask, direction)
+    for got in (got_px, got_of, got_b2):
+        np.testing.assert_allclose(got, want, rtol=1e-11, atol=1e-11)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_triattn_matches_brute_force(starting):
+    z, mask, _, ta = _small(seed=2, n=4, heads=2, d=3)
+    want = np.array(B.triattn(z.tolist(), mask.tolist(), B.tolist(ta), 2, starting))
+    got_px = O.protenix_triangle_attention(z, mask, ta, num_heads=2, starting=starting)
+    got_of = O.openfold3_triangle_attention(z, _of3_attn(ta), no_heads=2, mask=mask, starting=starting)
+    got_b2 = O.boltz2_triangle_attention(O.triattn_torch_to_boltz2(ta), z, mask, starting=starting)
+    for got in (got_px, got_of, got_b2):
+        np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+
+
+def test_contraction_brute_force_both_directions():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((5, 5, 2))
+    b = rng.standard_normal((5, 5, 2))
+    out = O.triangle_contract(a, b, "outgoing")
+    inc = O.triangle_contract(a, b, "incoming")
+    for i in range(5):
+        for j in range(5):
+            for c in range(2):
+                assert abs(out[i, j, c] - sum(a[i, k, c] * b[j, k, c] for k in range(5))) < 1e-12
+                assert abs(inc[i, j, c] - sum(a[k, i, c] * b[k, j, c] for k in range(5))) < 1e-12
+    with pytest.raises(ValueError, match="Unsupported triangle multiplication direction"):
+        O.triangle_contract(a, b, "sideways")
+
+
+# ----------------------------------------------------------- library routines
+
+
+def test_layer_norm_matches_torch():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((7, 33)) * 3 + 1
+    w = rng.standard_normal(33)
+    b = rng.standard_normal(33)
+    want = torch.nn.functional.layer_norm(
+        torch.from_numpy(x), (33,), torch.from_numpy(w), torch.from_numpy(b), eps=1e-5
+    ).numpy()
+    np.testing.assert_allclose(O.layer_norm(x, w, b, 1e-5), want, rtol=1e-12, atol=1e-12)
+
+
+def test_attention_rows_matches_torch_sdpa():
+    """Zero-free bias + mask reduce the row attention to textbook SDPA."""
+    rng = np.random.default_rng(5)
+    i_rows, heads, n, d = 3, 2, 9, 4
+    q = rng.standard_normal((i_rows, heads, n, d))
+    k = rng.standard_normal((i_rows, heads, n, d))
+    v = rng.standard_normal((i_rows, heads, n, d))
+    mask = (rng.random((i_rows, n)) > 0.3).astype(np.float64)
+    mask[:, 0] = 1
+    mb = (1e9 * (mask - 1.0))[:, None, None, :]
+    tb = rng.standard_normal((1, heads, n, n))
+    got = O.attention_rows(q / np.sqrt(d), k, v, mb, tb)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v),
+        attn_mask=torch.from_numpy(mb + tb),
+    ).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+
+
+def test_attention_core_scale_applied_inside():
+    rng = np.random.default_rng(6)
+    q, k, v = (rng.standard_normal((1, 2, 2, 5, 8)) for _ in range(3))
+    tb = rng.standard_normal((1, 1, 2, 5, 5))
+    mb = np.zeros((1, 2, 1, 1, 5))
+    got = O.attention_core(q, k, v, tb, mb, scale=8 ** -0.5)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        *(torch.from_numpy(t) for t in (q, k, v)), attn_mask=torch.from_numpy(tb + mb)
+    ).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+
+
+# ------------------------------------------------------------- invariants
+
+
+def _swap_ab(tm):
+    out = dict(tm)
+    out["linear_a_p"], out["linear_b_p"] = tm["linear_b_p"], tm["linear_a_p"]
+    out["linear_a_g"], out["linear_b_g"] = tm["linear_b_g"], tm["linear_a_g"]
+    return out
+
+
+def test_incoming_is_swapped_outgoing_with_a_b_exchanged():
+    """incoming(z)[i,j] = outgoing(z^T; a<->b)[j,i] (``B2T/triangle.py:112-121``)."""
+    rng = np.random.default_rng(7)
+    z = rng.standard_normal((9, 9, 8))
+    mask = (rng.random((9, 9)) > 0.2).astype(np.float64)
+    tm = syn.trimul_weights(8, 6, seed=7)
+    inc = O.protenix_triangle_multiplication(z, mask, tm, "incoming")
+    out_t = O.protenix_triangle_multiplication(
+        np.swapaxes(z, 0, 1), mask.T, _swap_ab(tm), "outgoing"
+    )
+    np.testing.assert_allclose(inc, np.swapaxes(out_t, 0, 1), rtol=1e-11, atol=1e-11)
+
+
+def test_outgoing_differs_from_incoming():
+    z, mask, tm, _ = _small(seed=8, n=6, c_z=8, c_h=8)
+    a = O.protenix_triangle_multiplication(z, mask, tm, "outgoing")
+    b = O.protenix_triangle_multiplication(z, mask, tm, "incoming")
+    assert np.max(np.abs(a - b)) > 1e-2
+
+
+def test_ending_is_transposed_starting():
+    rng = np.random.default_rng(9)
+    z = rng.standard_normal((7, 7, 8))
+    mask = (rng.random((7, 7)) > 0.2).astype(np.float64)
+    ta = syn.triattn_weights(8, 2, 4, seed=9)
+    end = O.protenix_triangle_attention(z, mask, ta, num_heads=2, starting=False)
+    start_t = O.protenix_triangle_attention(np.swapaxes(z, 0, 1), mask.T, ta, num_heads=2, starting=True)
+    np.testing.assert_allclose(end, np.swapaxes(start_t, 0, 1), rtol=1e-12, atol=1e-12)
+
+
+def test_row_block_invariance():
+    rng = np.random.default_rng(10)
+    q, k, v = (rng.standard_normal((11, 2, 6, 4)) for _ in range(3))
+    mb = (1e9 * ((rng.random((11, 6)) > 0.3) - 1.0))[:, None, None, :]
+    tb = rng.standard_normal((1, 2, 6, 6))
+    ref = O.attention_rows(q, k, v, mb, tb, row_block=11)
+    for blk in (1, 4, 10, 16):
+        np.testing.assert_allclose(O.attention_rows(q, k, v, mb, tb, row_block=blk), ref, rtol=0, atol=1e-14)
+
+
+def test_fully_masked_row_is_finite():
+    z, _, _, ta = _small(seed=11, n=5, heads=2, d=3)
+    mask = np.ones((5, 5))
+    mask[2, :] = 0.0
+    out = O.protenix_triangle_attention(z, mask, ta, num_heads=2)
+    assert np.all(np.isfinite(out))
+
+
+@pytest.mark.parametrize("op", ["trimul_out", "trimul_in", "att_start", "att_end"])
+def test_padding_isolation(op):
+    """Adversarial padded tokens leave the valid region unchanged."""
+    rng = np.random.default_rng(12)
+    n, pad = 5, 3
+    z = rng.standard_normal((n, n, 8))
+    zp = np.pad(z, ((0, pad), (0, pad), (0, 0)))
+    zp[n:, :, :] = -1.0e6
+    zp[:, n:, :] = 1.0e6
+    mask = syn.pair_mask(n + pad, n)
+    tm = syn.trimul_weights(8, 8, seed=12)
+    ta = syn.triattn_weights(8, 2, 4, seed=12)
+    if op.startswith("trimul"):
+        d = "outgoing" if op.endswith("out") else "incoming"
+        want = O.protenix_triangle_multiplication(z, np.ones((n, n)), tm, d)
+        got = O.protenix_triangle_multiplication(zp, mask, tm, d)
+    else:
+        s = op.endswith("start")
+        want = O.protenix_triangle_attention(z, np.ones((n, n)), ta, num_heads=2, starting=s)
+        got = O.protenix_triangle_attention(zp, mask, ta, num_heads=2, starting=s)
+    np.testing.assert_allclose(got[:n, :n], want, rtol=1e-9, atol=1e-9)
+
+
+def test_batch_axis_is_independent():
+    rng = np.random.default_rng(13)
+    z = rng.standard_normal((2, 6, 6, 8))
+    mask = np.ones((2, 6, 6))
+    tm = syn.trimul_weights(8, 8, seed=13)
+    ta = syn.triattn_weights(8, 2, 4, seed=13)
+    bm = O.protenix_triangle_multiplication(z, mask, tm, "incoming")
+    ba = O.protenix_triangle_attention(z, mask, ta, num_heads=2, starting=False)
+    for b in range(2):
+        np.testing.assert_allclose(bm[b], O.protenix_triangle_multiplication(z[b], mask[b], tm, "incoming"), atol=1e-12)
+        np.testing.assert_allclose(ba[b], O.protenix_triangle_attention(z[b], mask[b], ta, num_heads=2, starting=False), atol=1e-12)
+
+
+# ----------------------------------------------- planted mistakes are caught
+
+
+def test_planted_transposed_operand_is_caught(monkeypatch):
+    z, mask, tm, _ = _small(seed=14)
+    want = np.array(B.trimul(z.tolist(), mask.tolist(), B.tolist(tm), False))
+    real = O.triangle_contract
+
+    def wrong(a, b, direction):  # incoming computed as a[k,i] b[j,k]: b transposed
+        if direction == "incoming":
+            return real(a, np.swapaxes(b, -2, -3), "incoming")
+        return real(a, b, direction)
+
+    monkeypatch.setattr(O, "triangle_contract", wrong)
+    got = O.protenix_triangle_multiplication(z, mask, tm, "incoming")
+    assert np.max(np.abs(got - want)) > 1e-3
+
+
+def test_planted_dropped_bias_term_is_caught(monkeypatch):
+    z, mask, _, ta = _small(seed=15, n=4)
+    want = np.array(B.triattn(z.tolist(), mask.tolist(), B.tolist(ta), 2, True))
+    real = O.attention_rows
+    monkeypatch.setattr(O, "attention_rows", lambda q, k, v, mb, tb, row_block=16: real(q, k, v, mb, 0.0 * tb))
+    got = O.protenix_triangle_attention(z, mask, ta, num_heads=2)
+    assert np.max(np.abs(got - want)) > 1e-3
+
+
+def test_planted_wrong_bias_index_is_caught(monkeypatch):
+    """A bias read as [h, key, query] instead of [h, query, key] is caught."""
+    z, mask, _, ta = _small(seed=16, n=4)
+    want = np.array(B.triattn(z.tolist(), mask.tolist(), B.tolist(ta), 2, True))
+    real = O.attention_rows
+    monkeypatch.setattr(O, "attention_rows", lambda q, k, v, mb, tb, row_block=16: real(q, k, v, mb, np.swapaxes(tb, -1, -2)))
+    got = O.protenix_triangle_attention(z, mask, ta, num_heads=2)
+    assert np.max(np.abs(got - want)) > 1e-3
