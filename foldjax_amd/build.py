@@ -1,0 +1,75 @@
+"""Build the gfx950 HIP library ``foldjax_amd/lib/libfjx_tri.so`` in-tree.
+
+Usage: ``python -m foldjax_amd.build`` (or ``__graft_entry__.build()``).
+Every call recompiles. hipcc cross-compiles for gfx950 without a GPU present.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIBDIR = PKG / "lib"
+LIB = LIBDIR / "libfjx_tri.so"
+ARCH = os.environ.get("FJX_OFFLOAD_ARCH", "gfx950")
+
+HIP_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    # packed fp32 instructions are kept out of every kernel
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    "-Wno-pass-failed",
+    f"-I{ROOT / 'include'}",
+]
+
+
+def _hipcc() -> str:
+    cand = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    return cand
+
+
+def _compile(src: Path, obj: Path) -> tuple[Path, str]:
+    cmd = [_hipcc(), *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    log = "\n".join(line for line in (proc.stdout + proc.stderr).splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{log}")
+    return obj, log
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    LIBDIR.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
+    objs = []
+    with cf.ThreadPoolExecutor(jobs) as pool:
+        futs = [pool.submit(_compile, s, BUILD / (s.stem + ".o")) for s in sources]
+        for f in futs:
+            obj, log = f.result()
+            objs.append(obj)
+            if verbose and log.strip():
+                print(log, file=sys.stderr)
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp), *map(str, objs)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,523 @@
+// C ABI of the triangle kernels: argument checks, workspace layout, launch
+// sequence, thread-local error strings and optional per-kernel event timing.
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/fjx_tri.h"
+#include "fjx_common.hpp"
+#include "fjx_kernels.hpp"
+
+using namespace fjx;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FJX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return FJX_OK;
+}
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+int64_t round64(int64_t v) { return (v + 63) / 64 * 64; }
+size_t esize(int32_t dt) { return dt == FJX_DTYPE_BF16 ? 2 : 4; }
+
+// ------------------------------------------------------------ event timing
+enum KernelId {
+  K_TRIMUL_PROLOGUE = 0,
+  K_TRIMUL_CONTRACT,
+  K_TRIMUL_EPILOGUE,
+  K_TRIATTN_PROLOGUE,
+  K_TRIATTN_FLASH,
+  K_TRIATTN_EPILOGUE,
+  K_TRIATTN_CORE_PREP,
+  K_COUNT
+};
+const char* kKernelNames[K_COUNT] = {"trimul_prologue", "trimul_contract", "trimul_epilogue",
+                                     "triattn_prologue", "triattn_flash", "triattn_epilogue",
+                                     "triattn_core_prep"};
+
+struct Prof {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  struct Rec {
+    int id;
+    hipEvent_t a, b;
+  };
+  std::vector<Rec> pending;
+  double total_ms[K_COUNT] = {};
+  int64_t count[K_COUNT] = {};
+};
+Prof& prof() {
+  static Prof p;
+  return p;
+}
+
+hipEvent_t take_event(Prof& p) {
+  if (!p.pool.empty()) {
+    hipEvent_t e = p.pool.back();
+    p.pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+template <class F>
+int timed(int id, hipStream_t st, const char* what, F&& launch) {
+  Prof& p = prof();
+  hipEvent_t a = nullptr, b = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(p.mu);
+    if (p.on) {
+      a = take_event(p);
+      b = take_event(p);
+    }
+  }
+  if (a && b) (void)hipEventRecord(a, st);
+  launch();
+  const int rc = check_launch(what);
+  if (a && b) {
+    (void)hipEventRecord(b, st);
+    std::lock_guard<std::mutex> lk(p.mu);
+    p.pending.push_back({id, a, b});
+  }
+  return rc;
+}
+
+// --------------------------------------------------- attention-core prep
+// q/k: [B][R][H][n][32] -> [B][R][H][np][32] (q times qscale), zero padded keys
+template <typename T>
+__global__ void pad_qk_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t np,
+                              int64_t heads_rows, float mul) {
+  const int64_t total = heads_rows * np * 32;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t d = idx % 32;
+    const int64_t s = (idx / 32) % np;
+    const int64_t hr = idx / (32 * np);
+    dst[idx] = s < n ? from_f32<T>(to_f32(src[(hr * n + s) * 32 + d]) * mul) : from_f32<T>(0.f);
+  }
+}
+// v: [B][R][H][n][32] -> vt [B][R][H*32][np]
+template <typename T>
+__global__ void transpose_v_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t np,
+                                   int64_t heads_rows) {
+  const int64_t total = heads_rows * 32 * np;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t s = idx % np;
+    const int64_t d = (idx / np) % 32;
+    const int64_t hr = idx / (32 * np);
+    dst[idx] = s < n ? src[(hr * n + s) * 32 + d] : from_f32<T>(0.f);
+  }
+}
+// bias [B][H][n][n] -> [B][H][np][np], zeros outside
+template <typename T>
+__global__ void pad_bias_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t np,
+                                int64_t planes) {
+  const int64_t total = planes * np * np;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = idx % np;
+    const int64_t q = (idx / np) % np;
+    const int64_t pl = idx / (np * np);
+    dst[idx] = (q < n && k < n) ? src[(pl * n + q) * n + k] : from_f32<T>(0.f);
+  }
+}
+// mask bias [B][R][n] fp32 -> [B][R][np] times log2 e, -inf for padded keys
+__global__ void pad_mb_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n, int64_t np,
+                              int64_t rows) {
+  const int64_t total = rows * np;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = idx % np;
+    const int64_t r = idx / np;
+    dst[idx] = k < n ? (src ? src[r * n + k] * kLog2e : 0.f) : -INFINITY;
+  }
+}
+
+dim3 grid_for(int64_t total) {
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  return dim3((unsigned)blocks);
+}
+
+// --------------------------------------------------------------- layouts
+struct TriMulWs {
+  size_t a, b, o, g, total;
+};
+TriMulWs trimul_ws(int64_t batch, int64_t n, int32_t dtype) {
+  const size_t per = align_up((size_t)batch * n * n * 128 * esize(dtype));
+  TriMulWs w;
+  w.a = 0;
+  w.b = per;
+  w.o = 2 * per;
+  w.g = 3 * per;
+  w.total = 4 * per;
+  return w;
+}
+
+struct TriAttnWs {
+  size_t q, k, vt, g, bias, mb, o, total;
+};
+TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int32_t dtype, bool with_g,
+                     bool with_o) {
+  const int64_t np = round64(n);
+  const size_t es = esize(dtype);
+  const size_t qk = align_up((size_t)batch * rows * heads * np * 32 * es);
+  TriAttnWs w;
+  size_t off = 0;
+  w.q = off;
+  off += qk;
+  w.k = off;
+  off += qk;
+  w.vt = off;
+  off += qk;
+  w.g = off;
+  if (with_g) off += align_up((size_t)batch * rows * n * heads * 32 * es);
+  w.bias = off;
+  off += align_up((size_t)batch * heads * np * np * es);
+  w.mb = off;
+  off += align_up((size_t)batch * rows * np * sizeof(float));
+  w.o = off;
+  if (with_o) off += align_up((size_t)batch * rows * n * heads * 32 * es);
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+T* at(void* base, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+// ----------------------------------------------------------- tri-mul body
+template <typename T>
+int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
+  const TriMulWs ws = trimul_ws(a->batch, a->n, a->dtype);
+  T* abuf = at<T>(a->workspace, ws.a);
+  T* bbuf = at<T>(a->workspace, ws.b);
+  T* obuf = at<T>(a->workspace, ws.o);
+  T* gbuf = at<T>(a->workspace, ws.g);
+
+  TriMulPrologueParams<T> pp;
+  pp.x = static_cast<const T*>(a->x);
+  pp.mask = static_cast<const T*>(a->mask);
+  pp.ln_w = static_cast<const T*>(a->norm_in_weight);
+  pp.ln_b = static_cast<const T*>(a->norm_in_bias);
+  pp.w_p = static_cast<const T*>(a->p_in_weight);
+  pp.w_g = static_cast<const T*>(a->g_in_weight);
+  pp.w_gout = static_cast<const T*>(a->g_out_weight);
+  pp.a_cm = abuf;
+  pp.b_cm = bbuf;
+  pp.g = gbuf;
+  pp.n = a->n;
+  pp.eps = a->eps;
+  pp.transpose = a->direction == FJX_INCOMING;
+  int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] { launch_trimul_prologue<T>(pp, a->batch, st); });
+  if (rc) return rc;
+
+  ContractParams<T, T> cp;
+  cp.a = abuf;
+  cp.b = bbuf;
+  cp.out = obuf;
+  cp.n = a->n;
+  cp.batches = a->batch * 128;
+  rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] { launch_contract<T, T>(cp, st); });
+  if (rc) return rc;
+
+  EpilogueParams<T> ep;
+  ep.x = obuf;
+  ep.ln_w = static_cast<const T*>(a->norm_out_weight);
+  ep.ln_b = static_cast<const T*>(a->norm_out_bias);
+  ep.w = static_cast<const T*>(a->p_out_weight);
+  ep.gate = gbuf;
+  ep.residual = static_cast<const T*>(a->residual);
+  ep.out = static_cast<T*>(a->out);
+  ep.n = a->n;
+  ep.eps = a->eps;
+  ep.transpose = 0;
+  return timed(K_TRIMUL_EPILOGUE, st, "trimul_epilogue",
+               [&] { launch_epilogue<T>(ep, /*channel_major=*/true, /*ln=*/true, a->batch, st); });
+}
+
+// ---------------------------------------------------------- tri-attn body
+template <typename T>
+int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
+  const int64_t n = a->n;
+  const int64_t np = round64(n);
+  const bool gated = a->g_weight != nullptr;
+  const TriAttnWs ws = triattn_ws(a->batch, n, n, a->heads, a->dtype, gated, true);
+  void* W = a->workspace;
+
+  TriAttnPrologueParams<T> pp;
+  pp.x = static_cast<const T*>(a->x);
+  pp.mask = static_cast<const T*>(a->mask);
+  pp.ln_w = static_cast<const T*>(a->norm_weight);
+  pp.ln_b = static_cast<const T*>(a->norm_bias);
+  pp.w_bias = static_cast<const T*>(a->bias_weight);
+  pp.w_q = static_cast<const T*>(a->q_weight);
+  pp.w_k = static_cast<const T*>(a->k_weight);
+  pp.w_v = static_cast<const T*>(a->v_weight);
+  pp.w_g = static_cast<const T*>(a->g_weight);
+  pp.q = at<T>(W, ws.q);
+  pp.k = at<T>(W, ws.k);
+  pp.vt = at<T>(W, ws.vt);
+  pp.g = gated ? at<T>(W, ws.g) : nullptr;
+  pp.bias = at<T>(W, ws.bias);
+  pp.mb = at<float>(W, ws.mb);
+  pp.n = n;
+  pp.np = np;
+  pp.eps = a->eps;
+  pp.inf = a->inf;
+  pp.q_scale = (1.0f / sqrtf((float)a->head_dim)) * kLog2e;
+  pp.transpose = a->starting ? 0 : 1;
+  int rc = timed(K_TRIATTN_PROLOGUE, st, "triattn_prologue", [&] { launch_triattn_prologue<T>(pp, a->batch, st); });
+  if (rc) return rc;
+
+  FlashParams<T> fp;
+  fp.q = pp.q;
+  fp.k = pp.k;
+  fp.vt = pp.vt;
+  fp.bias = pp.bias;
+  fp.mb = pp.mb;
+  fp.gate = pp.g;
+  fp.out = at<T>(W, ws.o);
+  fp.n = n;
+  fp.np = np;
+  fp.heads = a->heads;
+  fp.rows = n;
+  fp.o_stride_b = n * n * 128;
+  fp.o_stride_row = n * 128;
+  fp.o_stride_head = 32;
+  fp.o_stride_q = 128;
+  fp.bias_stride_b = a->heads * np * np;
+  rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
+  if (rc) return rc;
+
+  EpilogueParams<T> ep;
+  ep.x = fp.out;
+  ep.ln_w = nullptr;
+  ep.ln_b = nullptr;
+  ep.w = static_cast<const T*>(a->o_weight);
+  ep.gate = nullptr;
+  ep.residual = static_cast<const T*>(a->residual);
+  ep.out = static_cast<T*>(a->out);
+  ep.n = n;
+  ep.eps = a->eps;
+  ep.transpose = a->starting ? 0 : 1;
+  return timed(K_TRIATTN_EPILOGUE, st, "triattn_epilogue",
+               [&] { launch_epilogue<T>(ep, /*channel_major=*/false, /*ln=*/false, a->batch, st); });
+}
+
+template <typename T>
+int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
+  const int64_t n = a->n;
+  const int64_t np = round64(n);
+  const int64_t hr = a->batch * a->rows * a->heads;
+  const TriAttnWs ws = triattn_ws(a->batch, a->rows, n, a->heads, a->dtype, false, false);
+  void* W = a->workspace;
+  T* q = at<T>(W, ws.q);
+  T* k = at<T>(W, ws.k);
+  T* vt = at<T>(W, ws.vt);
+  T* bias = at<T>(W, ws.bias);
+  float* mb = at<float>(W, ws.mb);
+  int rc = timed(K_TRIATTN_CORE_PREP, st, "triattn_core_prep", [&] {
+    hipLaunchKernelGGL(pad_qk_kernel<T>, grid_for(hr * np * 32), dim3(256), 0, st,
+                       static_cast<const T*>(a->q), q, n, np, hr, a->scale * kLog2e);
+    hipLaunchKernelGGL(pad_qk_kernel<T>, grid_for(hr * np * 32), dim3(256), 0, st,
+                       static_cast<const T*>(a->k), k, n, np, hr, 1.0f);
+    hipLaunchKernelGGL(transpose_v_kernel<T>, grid_for(hr * np * 32), dim3(256), 0, st,
+                       static_cast<const T*>(a->v), vt, n, np, hr);
+    hipLaunchKernelGGL(pad_bias_kernel<T>, grid_for(a->batch * a->heads * np * np), dim3(256), 0, st,
+                       static_cast<const T*>(a->tri_bias), bias, n, np, a->batch * a->heads);
+    hipLaunchKernelGGL(pad_mb_kernel, grid_for(a->batch * a->rows * np), dim3(256), 0, st, a->mask_bias, mb, n,
+                       np, a->batch * a->rows);
+  });
+  if (rc) return rc;
+
+  FlashParams<T> fp;
+  fp.q = q;
+  fp.k = k;
+  fp.vt = vt;
+  fp.bias = bias;
+  fp.mb = mb;
+  fp.gate = nullptr;
+  fp.out = static_cast<T*>(a->out);
+  fp.n = n;
+  fp.np = np;
+  fp.heads = a->heads;
+  fp.rows = a->rows;
+  fp.o_stride_b = a->rows * a->heads * n * 32;
+  fp.o_stride_row = a->heads * n * 32;
+  fp.o_stride_head = n * 32;
+  fp.o_stride_q = 32;
+  fp.bias_stride_b = a->heads * np * np;
+  return timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
+}
+
+bool dtype_ok(int32_t dt) { return dt == FJX_DTYPE_F32 || dt == FJX_DTYPE_BF16; }
+
+// grid dimensions are 32-bit; y/z additionally capped at 65535
+bool grid_ok(int64_t n, int64_t batch) { return n <= 65535 && batch <= 65535; }
+
+}  // namespace
+
+extern "C" {
+
+const char* fjx_last_error(void) { return g_err.c_str(); }
+int fjx_abi_version(void) { return FJX_ABI_VERSION; }
+
+size_t fjx_trimul_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype) {
+  (void)c_z;
+  (void)c_h;
+  if (batch < 1 || n < 1 || !dtype_ok(dtype)) return 0;
+  return trimul_ws(batch, n, dtype).total;
+}
+
+int fjx_trimul_fwd(const fjx_trimul_args* a, hipStream_t st) {
+  g_err.clear();
+  if (!a) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: args is NULL");
+  if (a->batch < 1 || a->n < 1) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: batch and n must be >= 1");
+  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: unknown dtype %d", a->dtype);
+  if (a->direction != FJX_OUTGOING && a->direction != FJX_INCOMING)
+    return fail(FJX_ERR_INVALID, "Unsupported triangle multiplication direction: %d", a->direction);
+  if (a->c_z != 128 || a->c_h != 128)
+    return fail(FJX_ERR_UNSUPPORTED, "fjx_trimul_fwd: this build supports c_z == c_h == 128, got c_z=%lld c_h=%lld",
+                (long long)a->c_z, (long long)a->c_h);
+  if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_trimul_fwd: n or batch too large");
+  if (!a->x || !a->out || !a->norm_in_weight || !a->norm_in_bias || !a->p_in_weight || !a->g_in_weight ||
+      !a->norm_out_weight || !a->norm_out_bias || !a->p_out_weight || !a->g_out_weight)
+    return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: a required pointer is NULL");
+  const size_t need = trimul_ws(a->batch, a->n, a->dtype).total;
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(FJX_ERR_WORKSPACE, "fjx_trimul_fwd: workspace of %zu bytes needed, %zu given", need,
+                a->workspace_bytes);
+  return a->dtype == FJX_DTYPE_BF16 ? trimul_run<bf16>(a, st) : trimul_run<float>(a, st);
+}
+
+size_t fjx_triattn_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t heads, int64_t head_dim,
+                                  int32_t dtype) {
+  (void)c_z;
+  (void)head_dim;
+  if (batch < 1 || n < 1 || heads < 1 || !dtype_ok(dtype)) return 0;
+  return triattn_ws(batch, n, n, heads, dtype, true, true).total;
+}
+
+int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
+  g_err.clear();
+  if (!a) return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: args is NULL");
+  if (a->batch < 1 || a->n < 1) return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: batch and n must be >= 1");
+  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: unknown dtype %d", a->dtype);
+  if (a->c_z != 128 || a->head_dim != 32 || a->heads * a->head_dim != 128)
+    return fail(FJX_ERR_UNSUPPORTED,
+                "fjx_triattn_fwd: this build supports c_z == 128, head_dim == 32, heads*head_dim == 128; got "
+                "c_z=%lld heads=%lld head_dim=%lld",
+                (long long)a->c_z, (long long)a->heads, (long long)a->head_dim);
+  if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_triattn_fwd: n or batch too large");
+  if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->bias_weight || !a->q_weight ||
+      !a->k_weight || !a->v_weight || !a->o_weight)
+    return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: a required pointer is NULL");
+  const size_t need = triattn_ws(a->batch, a->n, a->n, a->heads, a->dtype, a->g_weight != nullptr, true).total;
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(FJX_ERR_WORKSPACE, "fjx_triattn_fwd: workspace of %zu bytes needed, %zu given", need,
+                a->workspace_bytes);
+  return a->dtype == FJX_DTYPE_BF16 ? triattn_run<bf16>(a, st) : triattn_run<float>(a, st);
+}
+
+size_t fjx_triattn_core_workspace_size(int64_t batch, int64_t rows, int64_t heads, int64_t n, int64_t head_dim,
+                                       int32_t dtype) {
+  (void)head_dim;
+  if (batch < 1 || rows < 1 || heads < 1 || n < 1 || !dtype_ok(dtype)) return 0;
+  return triattn_ws(batch, rows, n, heads, dtype, false, false).total;
+}
+
+int fjx_triattn_core(const fjx_triattn_core_args* a, hipStream_t st) {
+  g_err.clear();
+  if (!a) return fail(FJX_ERR_INVALID, "fjx_triattn_core: args is NULL");
+  if (a->batch < 1 || a->rows < 1 || a->heads < 1 || a->n < 1)
+    return fail(FJX_ERR_INVALID, "fjx_triattn_core: batch, rows, heads and n must be >= 1");
+  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_triattn_core: unknown dtype %d", a->dtype);
+  if (a->head_dim != 32)
+    return fail(FJX_ERR_UNSUPPORTED, "fjx_triattn_core: this build supports head_dim == 32, got %lld",
+                (long long)a->head_dim);
+  if (!a->q || !a->k || !a->v || !a->tri_bias || !a->out)
+    return fail(FJX_ERR_INVALID, "fjx_triattn_core: a required pointer is NULL");
+  const size_t need = triattn_ws(a->batch, a->rows, a->n, a->heads, a->dtype, false, false).total;
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(FJX_ERR_WORKSPACE, "fjx_triattn_core: workspace of %zu bytes needed, %zu given", need,
+                a->workspace_bytes);
+  return a->dtype == FJX_DTYPE_BF16 ? core_run<bf16>(a, st) : core_run<float>(a, st);
+}
+
+int fjx_prof_enable(int on) {
+  std::lock_guard<std::mutex> lk(prof().mu);
+  prof().on = on != 0;
+  return FJX_OK;
+}
+
+int fjx_prof_reset(void) {
+  Prof& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  for (auto& r : p.pending) {
+    (void)hipEventSynchronize(r.b);
+    p.pool.push_back(r.a);
+    p.pool.push_back(r.b);
+  }
+  p.pending.clear();
+  for (int i = 0; i < K_COUNT; ++i) {
+    p.total_ms[i] = 0.0;
+    p.count[i] = 0;
+  }
+  return FJX_OK;
+}
+
+int fjx_prof_collect(void) {
+  Prof& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  for (auto& r : p.pending) {
+    if (hipEventSynchronize(r.b) != hipSuccess) return fail(FJX_ERR_HIP, "fjx_prof_collect: event sync failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess)
+      return fail(FJX_ERR_HIP, "fjx_prof_collect: elapsed time failed");
+    p.total_ms[r.id] += ms;
+    p.count[r.id] += 1;
+    p.pool.push_back(r.a);
+    p.pool.push_back(r.b);
+  }
+  p.pending.clear();
+  return FJX_OK;
+}
+
+int fjx_prof_num_kernels(void) { return K_COUNT; }
+
+const char* fjx_prof_kernel_name(int id) { return (id >= 0 && id < K_COUNT) ? kKernelNames[id] : ""; }
+
+int fjx_prof_read(int id, double* total_ms, int64_t* launches) {
+  if (id < 0 || id >= K_COUNT) return fail(FJX_ERR_INVALID, "fjx_prof_read: bad kernel id %d", id);
+  Prof& p = prof();
+  std::lock_guard<std::mutex> lk(p.mu);
+  if (total_ms) *total_ms = p.total_ms[id];
+  if (launches) *launches = p.count[id];
+  return FJX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Shared device helpers for the gfx950 triangle kernels: element types, MFMA
+// fragments, vector loads and the launch-error plumbing.
+//
+// MFMA convention used by every kernel (64-lane wavefront, lane l, g = l/16):
+//   one 16x16 output tile D[16][16] per `mma()` call, fp32 accumulators;
+//   A fragment: the 8 elements A[row = l%16][k = kbase + 8g + e], e = 0..7
+//   B fragment: the 8 elements B[k = kbase + 8g + e][col = l%16]
+//   D: lane l holds D[4g + r][l%16], r = 0..3
+// The k-slot of element e of lane group g only has to be the same in A and B,
+// so a kernel may assign any 8 distinct k values to (g, e) as long as it loads
+// both operands with that same assignment. bf16 uses one
+// v_mfma_f32_16x16x32_bf16; fp32 uses eight v_mfma_f32_16x16x4_f32, step e
+// taking element e of every lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fjx {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 8-element operand fragment per element type
+template <typename T> struct Frag;
+template <> struct Frag<bf16> { typedef bf16x8 type; };
+template <> struct Frag<float> { typedef f32x8 type; };
+
+__device__ __forceinline__ void mma(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ void mma(f32x4& acc, const f32x8& a, const f32x8& b) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return static_cast<float>(x); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float x) { return static_cast<bf16>(x); }
+
+// 8 contiguous elements <-> fragment (16 B for bf16, 32 B for fp32)
+__device__ __forceinline__ bf16x8 load8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ f32x8 load8(const float* p) {
+  f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+  f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
+  return f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+__device__ __forceinline__ void store8(bf16* p, const bf16x8& v) { *reinterpret_cast<bf16x8*>(p) = v; }
+__device__ __forceinline__ void store8(float* p, const f32x8& v) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+}
+
+// 8 elements -> fp32 and back
+__device__ __forceinline__ void to_f32x8(const bf16x8& v, float* o) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = static_cast<float>(v[e]);
+}
+__device__ __forceinline__ void to_f32x8(const f32x8& v, float* o) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = v[e];
+}
+template <typename T> __device__ __forceinline__ typename Frag<T>::type pack8(const float* f);
+template <> __device__ __forceinline__ bf16x8 pack8<bf16>(const float* f) {
+  bf16x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = static_cast<bf16>(f[e]);
+  return v;
+}
+template <> __device__ __forceinline__ f32x8 pack8<float>(const float* f) {
+  f32x8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = f[e];
+  return v;
+}
+
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  // 1 / (1 + 2^(-x log2 e)); saturates cleanly to 0 / 1 at the extremes
+  return __frcp_rn(1.0f + exp2f(-x * kLog2e));
+}
+
+// wave-wide xor shuffle of a float (64 lanes)
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+}  // namespace fjx

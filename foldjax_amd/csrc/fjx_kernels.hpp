@@ -1,0 +1,106 @@
+// Kernel parameter blocks and launchers shared between the HIP translation
+// units and the C ABI layer (fjx_capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fjx {
+
+template <typename T>
+struct TriMulPrologueParams {
+  const T* x;     // [B][N][N][128]
+  const T* mask;  // [B][N][N] or null
+  const T* ln_w;
+  const T* ln_b;
+  const T* w_p;     // [256][128]: rows 0..127 -> a, 128..255 -> b
+  const T* w_g;     // [256][128]
+  const T* w_gout;  // [128][128]
+  T* a_cm;          // [B][128][N*N] virtual grid
+  T* b_cm;
+  T* g;             // [B][N*N][128] original grid
+  int64_t n;
+  float eps;
+  int transpose;    // 1 for the incoming direction
+};
+
+template <typename T>
+struct TriAttnPrologueParams {
+  const T* x;
+  const T* mask;
+  const T* ln_w;
+  const T* ln_b;
+  const T* w_bias;  // [4][128]
+  const T* w_q;     // [128][128]
+  const T* w_k;
+  const T* w_v;
+  const T* w_g;     // or null
+  T* q;             // [B][N][4][Np][32]
+  T* k;
+  T* vt;            // [B][N][128][Np]
+  T* g;             // [B][N][N][128]
+  T* bias;          // [B][4][Np][Np]
+  float* mb;        // [B][N][Np]
+  int64_t n;
+  int64_t np;
+  float eps;
+  float inf;
+  float q_scale;    // head_dim^-0.5 * log2(e)
+  int transpose;    // 1 for the ending node
+};
+
+template <typename T>
+struct EpilogueParams {
+  const T* x;         // channel-major [B][128][N*N] or position-major [B][N*N][128]
+  const T* ln_w;      // LN over the 128 input channels (tri-mul LN_out)
+  const T* ln_b;
+  const T* w;         // [128][128]
+  const T* gate;      // [B][N*N][128] at the output position, or null
+  const T* residual;  // [B][N*N][128] or null (may alias out)
+  T* out;
+  int64_t n;
+  float eps;
+  int transpose;
+};
+
+template <typename T, typename TO>
+struct ContractParams {
+  const T* a;   // [B*C][N][N]: row i, contracted index k contiguous
+  const T* b;   // [B*C][N][N]: row j, k contiguous
+  TO* out;      // [B*C][N][N]
+  int64_t n;
+  int64_t batches;  // B*C
+};
+
+template <typename T>
+struct FlashParams {
+  const T* q;        // [B][N][H][Np][32], pre-scaled by scale*log2 e
+  const T* k;        // [B][N][H][Np][32]
+  const T* vt;       // [B][N][H*32][Np]
+  const T* bias;     // [B][H][Np][Np], raw (multiplied by log2 e in-kernel)
+  const float* mb;   // [B][N][Np], already times log2 e; -inf for padded keys
+  const T* gate;     // optional, indexed like out
+  T* out;            // out[b][i][q][h*32+d] via the strides below
+  int64_t n;
+  int64_t np;
+  int64_t heads;
+  int64_t rows;      // number of attention rows i (== n for the fused module)
+  int64_t o_stride_b;
+  int64_t o_stride_row;
+  int64_t o_stride_head;
+  int64_t o_stride_q;
+  int64_t bias_stride_b;  // 0 when one bias is shared by all batches
+};
+
+template <typename T>
+void launch_trimul_prologue(const TriMulPrologueParams<T>& p, int64_t batch, hipStream_t st);
+template <typename T>
+void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, hipStream_t st);
+template <typename T>
+void launch_epilogue(const EpilogueParams<T>& p, bool channel_major, bool ln, int64_t batch, hipStream_t st);
+template <typename T, typename TO>
+void launch_contract(const ContractParams<T, TO>& p, hipStream_t st);
+template <typename T>
+void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st);
+
+}  // namespace fjx

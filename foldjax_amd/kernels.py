@@ -1,0 +1,243 @@
+"""Tensor-level entry points of the HIP triangle kernels.
+
+Torch tensors are used only as device-memory handles: every call passes raw
+device pointers, sizes and the current HIP stream through the C ABI of
+``include/fjx_tri.h``. There is no other code path -- if the library is
+missing, the call raises.
+
+Weights are packed once into the PyTorch ``[out, in]`` layout of the ABI
+(``TriMulWeights`` / ``TriAttnWeights``); ``foldjax_amd.params`` builds them
+from each port's parameter containers.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, fields
+
+import torch
+
+from foldjax_amd import _lib
+
+_DTYPES = {torch.float32: _lib.FJX_DTYPE_F32, torch.bfloat16: _lib.FJX_DTYPE_BF16}
+
+
+def _code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise ValueError(f"the hip triangle kernels take float32 or bfloat16, got {dtype}") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _dev(x: torch.Tensor) -> None:
+    if x.device.type != "cuda":
+        raise ValueError(f"the hip backend needs device tensors, got a tensor on {x.device}")
+
+
+def _stream(x: torch.Tensor) -> int:
+    return torch.cuda.current_stream(x.device).cuda_stream
+
+
+def _prep(t: torch.Tensor | None, dtype: torch.dtype, device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    return t.to(device=device, dtype=dtype).contiguous()
+
+
+@dataclass(frozen=True)
+class TriMulWeights:
+    """Tri-mul weights in the ABI layout (PyTorch ``[out, in]``, a rows first)."""
+
+    norm_in_weight: torch.Tensor  # [c_z]
+    norm_in_bias: torch.Tensor  # [c_z]
+    p_in_weight: torch.Tensor  # [2 c_h, c_z]
+    g_in_weight: torch.Tensor  # [2 c_h, c_z]
+    norm_out_weight: torch.Tensor  # [c_h]
+    norm_out_bias: torch.Tensor  # [c_h]
+    p_out_weight: torch.Tensor  # [c_z, c_h]
+    g_out_weight: torch.Tensor  # [c_z, c_z]
+
+    def to(self, dtype: torch.dtype, device) -> "TriMulWeights":
+        return TriMulWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+
+
+@dataclass(frozen=True)
+class TriAttnWeights:
+    """Tri-attn weights in the ABI layout (PyTorch ``[out, in]``)."""
+
+    norm_weight: torch.Tensor  # [c_z]
+    norm_bias: torch.Tensor  # [c_z]
+    bias_weight: torch.Tensor  # [H, c_z]
+    q_weight: torch.Tensor  # [H D, c_z]
+    k_weight: torch.Tensor
+    v_weight: torch.Tensor
+    g_weight: torch.Tensor | None  # [H D, c_z] or None (ungated)
+    o_weight: torch.Tensor  # [c_z, H D]
+
+    @property
+    def heads(self) -> int:
+        return int(self.bias_weight.shape[0])
+
+    def to(self, dtype: torch.dtype, device) -> "TriAttnWeights":
+        return TriAttnWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+
+
+def _flatten_pair(x: torch.Tensor, mask: torch.Tensor | None):
+    if x.dim() < 3:
+        raise ValueError(f"pair tensor must be [..., N, N, C], got shape {tuple(x.shape)}")
+    n, n2, c = x.shape[-3:]
+    if n != n2:
+        raise ValueError(f"pair tensor must be square in its two pair axes, got {tuple(x.shape)}")
+    lead = x.shape[:-3]
+    batch = 1
+    for s in lead:
+        batch *= int(s)
+    xf = x.contiguous().reshape(batch, n, n, c)
+    mf = None
+    if mask is not None:
+        if tuple(mask.shape[-2:]) != (n, n):
+            raise ValueError(f"mask must be [..., {n}, {n}], got {tuple(mask.shape)}")
+        mf = torch.broadcast_to(mask, tuple(lead) + (n, n)).to(dtype=x.dtype).contiguous().reshape(batch, n, n)
+    return xf, mf, lead, batch, n, c
+
+
+def trimul(
+    x: torch.Tensor,
+    mask: torch.Tensor | None,
+    w: TriMulWeights,
+    direction: str,
+    eps: float = 1e-5,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Triangle multiplicative update (``fjx_trimul_fwd``); returns the update,
+    or ``residual + update`` when ``residual`` is given."""
+    _dev(x)
+    if direction not in ("outgoing", "incoming"):
+        raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
+    xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
+    c_h = int(w.norm_out_weight.shape[0])
+    lib = _lib.load()
+    code = _code(x.dtype)
+    out = torch.empty_like(xf)
+    res = None if residual is None else residual.to(dtype=x.dtype).contiguous().reshape(batch, n, n, c)
+    ws_bytes = lib.fjx_trimul_workspace_size(batch, n, c, c_h, code)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    a = _lib.TriMulArgs(
+        batch=batch, n=n, c_z=c, c_h=c_h,
+        direction=_lib.FJX_OUTGOING if direction == "outgoing" else _lib.FJX_INCOMING,
+        dtype=code, eps=float(eps),
+        x=_ptr(xf), mask=_ptr(mf),
+        norm_in_weight=_ptr(w.norm_in_weight), norm_in_bias=_ptr(w.norm_in_bias),
+        p_in_weight=_ptr(w.p_in_weight), g_in_weight=_ptr(w.g_in_weight),
+        norm_out_weight=_ptr(w.norm_out_weight), norm_out_bias=_ptr(w.norm_out_bias),
+        p_out_weight=_ptr(w.p_out_weight), g_out_weight=_ptr(w.g_out_weight),
+        residual=_ptr(res), out=_ptr(out),
+        workspace=_ptr(ws), workspace_bytes=ws_bytes,
+    )
+    _check_weights(x, w)
+    _lib.check(lib.fjx_trimul_fwd(ctypes.byref(a), _stream(x)))
+    return out.reshape(tuple(lead) + (n, n, c))
+
+
+def triattn(
+    x: torch.Tensor,
+    mask: torch.Tensor | None,
+    w: TriAttnWeights,
+    starting: bool = True,
+    inf: float = 1e9,
+    eps: float = 1e-5,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Triangle attention, starting or ending node (``fjx_triattn_fwd``)."""
+    _dev(x)
+    xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
+    heads = w.heads
+    hd = int(w.q_weight.shape[0])
+    if hd % heads:
+        raise ValueError(f"q projection width {hd} is not divisible by {heads} heads")
+    lib = _lib.load()
+    code = _code(x.dtype)
+    out = torch.empty_like(xf)
+    res = None if residual is None else residual.to(dtype=x.dtype).contiguous().reshape(batch, n, n, c)
+    ws_bytes = lib.fjx_triattn_workspace_size(batch, n, c, heads, hd // heads, code)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    a = _lib.TriAttnArgs(
+        batch=batch, n=n, c_z=c, heads=heads, head_dim=hd // heads,
+        starting=1 if starting else 0, dtype=code, eps=float(eps), inf=float(inf),
+        x=_ptr(xf), mask=_ptr(mf),
+        norm_weight=_ptr(w.norm_weight), norm_bias=_ptr(w.norm_bias), bias_weight=_ptr(w.bias_weight),
+        q_weight=_ptr(w.q_weight), k_weight=_ptr(w.k_weight), v_weight=_ptr(w.v_weight),
+        g_weight=_ptr(w.g_weight), o_weight=_ptr(w.o_weight),
+        residual=_ptr(res), out=_ptr(out),
+        workspace=_ptr(ws), workspace_bytes=ws_bytes,
+    )
+    _check_weights(x, w)
+    _lib.check(lib.fjx_triattn_fwd(ctypes.byref(a), _stream(x)))
+    return out.reshape(tuple(lead) + (n, n, c))
+
+
+def triattn_core(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    tri_bias: torch.Tensor,
+    mask_bias: torch.Tensor | None,
+    *,
+    scale: float,
+) -> torch.Tensor:
+    """``cueq_attention_core`` semantics (``src/foldjax/models/_cueq.py:66-121``).
+
+    q/k/v ``[..., I, H, J, D]``; ``tri_bias`` ``[..., 1, H, J, J]``; additive
+    ``mask_bias`` ``[..., I, 1, 1, J]`` (or None); ``scale`` applied inside.
+    Leading axes are broadcast and folded into one batch axis.
+    """
+    _dev(q)
+    lead = torch.broadcast_shapes(q.shape[:-4], tri_bias.shape[:-4],
+                                  () if mask_bias is None else mask_bias.shape[:-4])
+    rows, heads, n, d = q.shape[-4:]
+    batch = 1
+    for s in lead:
+        batch *= int(s)
+    dt = q.dtype
+
+    def fold(t, shape):
+        return torch.broadcast_to(t, tuple(lead) + tuple(shape)).to(dtype=dt).contiguous().reshape((batch,) + tuple(shape))
+
+    qf = fold(q, (rows, heads, n, d))
+    kf = fold(k, (rows, heads, n, d))
+    vf = fold(v, (rows, heads, n, d))
+    if tri_bias.shape[-4] != 1:
+        raise ValueError("tri_bias must be [..., 1, H, J, J]: the kernel shares one bias across rows")
+    bf = fold(tri_bias, (1, heads, n, n)).reshape(batch, heads, n, n)
+    mb = None
+    if mask_bias is not None:
+        mb = torch.broadcast_to(mask_bias, tuple(lead) + (rows, 1, 1, n)).to(torch.float32).contiguous()
+        mb = mb.reshape(batch, rows, n)
+    lib = _lib.load()
+    code = _code(dt)
+    out = torch.empty_like(qf)
+    ws_bytes = lib.fjx_triattn_core_workspace_size(batch, rows, heads, n, d, code)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+    a = _lib.TriAttnCoreArgs(
+        batch=batch, rows=rows, heads=heads, n=n, head_dim=d, dtype=code, scale=float(scale),
+        q=_ptr(qf), k=_ptr(kf), v=_ptr(vf), tri_bias=_ptr(bf), mask_bias=_ptr(mb),
+        out=_ptr(out), workspace=_ptr(ws), workspace_bytes=ws_bytes,
+    )
+    _lib.check(lib.fjx_triattn_core(ctypes.byref(a), _stream(q)))
+    return out.reshape(tuple(lead) + (rows, heads, n, d))
+
+
+def _check_weights(x: torch.Tensor, w) -> None:
+    for f in fields(w):
+        t = getattr(w, f.name)
+        if t is None:
+            continue
+        if t.dtype != x.dtype or t.device != x.device or not t.is_contiguous():
+            raise ValueError(
+                f"weight {f.name} must be a contiguous {x.dtype} tensor on {x.device}; "
+                "pack weights with .to(dtype, device) first"
+            )

@@ -1,0 +1,69 @@
+"""OpenFold3 triangle entry points with the reference's call signatures.
+
+Mirrors ``src/foldjax/models/openfold3/models/triangle.py:82``
+(``triangle_multiplication``, which has no backend switch upstream) and
+``triangle_attention.py:95`` (``triangle_attention``). The attention selector
+``OPENFOLD3_TRIANGLE_BACKEND`` / ``backend`` keeps its values {xla, cueq},
+case-insensitive (reference ``triangle_attention.py:80,154-157``), and gains
+``"hip"``, the default here.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from foldjax_amd import kernels
+from foldjax_amd.kernels import TriAttnWeights, TriMulWeights
+from foldjax_amd.params import pack_triattn_openfold3, pack_trimul_torch
+
+DEFAULT_BACKEND = "hip"
+
+
+def _default_backend() -> str:
+    return os.environ.get("OPENFOLD3_TRIANGLE_BACKEND", DEFAULT_BACKEND).lower()
+
+
+def triangle_multiplication(
+    z: torch.Tensor,
+    params,
+    *,
+    outgoing: bool,
+    mask: torch.Tensor | None = None,
+    eps: float = 1e-5,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """OpenFold3 triangle multiplication; ``mask=None`` means all ones."""
+    w = params if isinstance(params, TriMulWeights) else pack_trimul_torch(params, z.dtype, z.device)
+    return kernels.trimul(z, mask, w, "outgoing" if outgoing else "incoming", eps=eps, residual=residual)
+
+
+def triangle_attention(
+    x: torch.Tensor,
+    params,
+    *,
+    no_heads: int,
+    mask: torch.Tensor | None = None,
+    starting: bool = True,
+    inf: float = 1e9,
+    eps: float = 1e-5,
+    chunk_size: int | None = None,
+    backend: str | None = None,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """OpenFold3 triangle attention; ``chunk_size`` is accepted and unused."""
+    if backend is None:
+        backend = _default_backend()
+    backend = backend.lower()
+    if backend not in {"xla", "cueq", "hip"}:
+        raise ValueError(f"unsupported triangle attention backend: {backend!r}")
+    if backend != "hip":
+        raise RuntimeError(
+            f"the triangle attention backend {backend!r} is a JAX backend of the reference; "
+            "this package provides 'hip'"
+        )
+    w = params if isinstance(params, TriAttnWeights) else pack_triattn_openfold3(params, x.dtype, x.device)
+    if w.heads != no_heads:
+        raise ValueError(f"no_heads={no_heads} but the bias projection has {w.heads} heads")
+    return kernels.triattn(x, mask, w, starting=starting, inf=inf, eps=eps, residual=residual)

@@ -1,0 +1,273 @@
+"""Parameter containers of the three ports and their packing into ABI weights.
+
+The containers mirror the reference's own types so that mapped checkpoints
+drop in unchanged:
+
+* Boltz-2 uses nested dicts with ``[in, out]`` kernels
+  (``src/foldjax/models/boltz2/bridge/torch_mapping.py:513-600``).
+* Protenix uses NamedTuples with PyTorch ``[out, in]`` weights
+  (``src/foldjax/models/protenix/models/primitives/primitives.py:11-28``,
+  ``.../triangle/triangle.py:77-95``, ``.../primitives/attention.py:21-29``).
+* OpenFold3 uses its own NamedTuples (``src/foldjax/models/openfold3/models/
+  triangle.py:40-54``, ``triangle_attention.py:83-92``, ``attention.py``).
+
+Every triangle projection is bias-free upstream; a container carrying a
+projection bias is rejected rather than silently ignored.
+"""
+
+from __future__ import annotations
+
+from typing import Any, NamedTuple
+
+import numpy as np
+import torch
+
+from foldjax_amd.kernels import TriAttnWeights, TriMulWeights
+
+
+class LinearParams(NamedTuple):
+    """PyTorch-layout linear: ``weight [out, in]``, optional ``bias [out]``."""
+
+    weight: Any
+    bias: Any = None
+
+
+class LayerNormParams(NamedTuple):
+    weight: Any = None
+    bias: Any = None
+
+
+class AttentionParams(NamedTuple):
+    """Protenix/OpenFold3 ``Attention`` projections."""
+
+    linear_q: LinearParams
+    linear_k: LinearParams
+    linear_v: LinearParams
+    linear_o: LinearParams
+    linear_g: LinearParams | None
+
+
+class ProtenixTriangleMultiplicationParams(NamedTuple):
+    layer_norm_in: LayerNormParams
+    layer_norm_out: LayerNormParams
+    linear_a_p: LinearParams
+    linear_a_g: LinearParams
+    linear_b_p: LinearParams
+    linear_b_g: LinearParams
+    linear_z: LinearParams
+    linear_g: LinearParams
+
+
+class ProtenixTriangleAttentionParams(NamedTuple):
+    layer_norm: LayerNormParams
+    linear: LinearParams
+    attention: AttentionParams
+
+
+class OpenFold3TriangleMultiplicationParams(NamedTuple):
+    layer_norm_in: LayerNormParams
+    layer_norm_out: LayerNormParams
+    linear_a_p: LinearParams
+    linear_a_g: LinearParams
+    linear_b_p: LinearParams
+    linear_b_g: LinearParams
+    linear_g: LinearParams
+    linear_z: LinearParams
+
+
+class OpenFold3TriangleAttentionParams(NamedTuple):
+    layer_norm: LayerNormParams
+    linear_z: LinearParams
+    mha: AttentionParams
+
+
+def _t(x) -> torch.Tensor:
+    if isinstance(x, torch.Tensor):
+        return x
+    return torch.as_tensor(np.asarray(x))
+
+
+def _get(obj, name):
+    if isinstance(obj, dict):
+        return obj.get(name)
+    return getattr(obj, name, None)
+
+
+def _weight(lin, what: str) -> torch.Tensor:
+    if lin is None:
+        raise ValueError(f"missing linear {what}")
+    if _get(lin, "bias") is not None:
+        raise ValueError(f"{what} carries a bias; the triangle projections are bias-free")
+    return _t(_get(lin, "weight"))
+
+
+def _ln(p, c: int):
+    w = _get(p, "weight") if p is not None else None
+    b = _get(p, "bias") if p is not None else None
+    w = torch.ones(c) if w is None else _t(w)
+    b = torch.zeros(c) if b is None else _t(b)
+    return w, b
+
+
+# ----------------------------------------------------------------- tri-mul
+
+
+def pack_trimul_boltz2(params, dtype: torch.dtype, device) -> TriMulWeights:
+    """Boltz-2 dict (kernels ``[in, out]``) -> ABI weights: every projection is
+    transposed, as the reference's cuEquivariance adapter does
+    (``B2T/triangle_cueq.py:92-99``)."""
+    k = lambda name: _t(params[name]["kernel"]).T  # noqa: E731
+    w = TriMulWeights(
+        norm_in_weight=_t(params["norm_in"]["scale"]),
+        norm_in_bias=_t(params["norm_in"]["bias"]),
+        p_in_weight=k("p_in"),
+        g_in_weight=k("g_in"),
+        norm_out_weight=_t(params["norm_out"]["scale"]),
+        norm_out_bias=_t(params["norm_out"]["bias"]),
+        p_out_weight=k("p_out"),
+        g_out_weight=k("g_out"),
+    )
+    return w.to(dtype, device)
+
+
+def pack_trimul_torch(params, dtype: torch.dtype, device) -> TriMulWeights:
+    """Protenix/OpenFold3 tri-mul fields -> ABI weights: a and b projections
+    are stacked a-first, as ``PXT/triangle_cueq.py:28-47`` does for cuEq."""
+    a_p = _weight(_get(params, "linear_a_p"), "linear_a_p")
+    c_h, c_z = a_p.shape
+    ln_in = _ln(_get(params, "layer_norm_in"), c_z)
+    ln_out = _ln(_get(params, "layer_norm_out"), c_h)
+    w = TriMulWeights(
+        norm_in_weight=ln_in[0],
+        norm_in_bias=ln_in[1],
+        p_in_weight=torch.cat([a_p, _weight(_get(params, "linear_b_p"), "linear_b_p")], 0),
+        g_in_weight=torch.cat(
+            [_weight(_get(params, "linear_a_g"), "linear_a_g"), _weight(_get(params, "linear_b_g"), "linear_b_g")], 0
+        ),
+        norm_out_weight=ln_out[0],
+        norm_out_bias=ln_out[1],
+        p_out_weight=_weight(_get(params, "linear_z"), "linear_z"),
+        g_out_weight=_weight(_get(params, "linear_g"), "linear_g"),
+    )
+    return w.to(dtype, device)
+
+
+# ---------------------------------------------------------------- tri-attn
+
+
+def pack_triattn_boltz2(params, dtype: torch.dtype, device) -> TriAttnWeights:
+    """Boltz-2 tri-attn dict -> ABI weights (all kernels transposed)."""
+    mha = params["mha"]
+    k = lambda p: _t(p["kernel"]).T  # noqa: E731
+    w = TriAttnWeights(
+        norm_weight=_t(params["layer_norm"]["scale"]),
+        norm_bias=_t(params["layer_norm"]["bias"]),
+        bias_weight=k(params["linear"]),
+        q_weight=k(mha["linear_q"]),
+        k_weight=k(mha["linear_k"]),
+        v_weight=k(mha["linear_v"]),
+        g_weight=k(mha["linear_g"]),
+        o_weight=k(mha["linear_o"]),
+    )
+    return w.to(dtype, device)
+
+
+def _pack_triattn_torch(ln, bias_lin, att, dtype, device) -> TriAttnWeights:
+    q = _weight(_get(att, "linear_q"), "linear_q")
+    c_z = q.shape[1]
+    lw, lb = _ln(ln, c_z)
+    g = _get(att, "linear_g")
+    w = TriAttnWeights(
+        norm_weight=lw,
+        norm_bias=lb,
+        bias_weight=_weight(bias_lin, "triangle bias linear"),
+        q_weight=q,
+        k_weight=_weight(_get(att, "linear_k"), "linear_k"),
+        v_weight=_weight(_get(att, "linear_v"), "linear_v"),
+        g_weight=None if g is None else _weight(g, "linear_g"),
+        o_weight=_weight(_get(att, "linear_o"), "linear_o"),
+    )
+    return w.to(dtype, device)
+
+
+def pack_triattn_protenix(params, dtype: torch.dtype, device) -> TriAttnWeights:
+    """Protenix ``TriangleAttentionParams(layer_norm, linear, attention)``."""
+    return _pack_triattn_torch(_get(params, "layer_norm"), _get(params, "linear"), _get(params, "attention"), dtype, device)
+
+
+def pack_triattn_openfold3(params, dtype: torch.dtype, device) -> TriAttnWeights:
+    """OpenFold3 ``TriangleAttentionParams(layer_norm, linear_z, mha)``."""
+    return _pack_triattn_torch(_get(params, "layer_norm"), _get(params, "linear_z"), _get(params, "mha"), dtype, device)
+
+
+# ------------------------------------------------ synthetic-weight adapters
+
+
+def _lin(d):
+    return LinearParams(weight=d["weight"], bias=d.get("bias"))
+
+
+def _lnp(d):
+    return LayerNormParams(weight=d.get("weight"), bias=d.get("bias"))
+
+
+def trimul_to_protenix(w: dict) -> ProtenixTriangleMultiplicationParams:
+    """Field dict (``foldjax_amd.synthetic.trimul_weights``) -> Protenix container."""
+    return ProtenixTriangleMultiplicationParams(
+        layer_norm_in=_lnp(w["layer_norm_in"]), layer_norm_out=_lnp(w["layer_norm_out"]),
+        linear_a_p=_lin(w["linear_a_p"]), linear_a_g=_lin(w["linear_a_g"]),
+        linear_b_p=_lin(w["linear_b_p"]), linear_b_g=_lin(w["linear_b_g"]),
+        linear_z=_lin(w["linear_z"]), linear_g=_lin(w["linear_g"]),
+    )
+
+
+def trimul_to_openfold3(w: dict) -> OpenFold3TriangleMultiplicationParams:
+    return OpenFold3TriangleMultiplicationParams(
+        layer_norm_in=_lnp(w["layer_norm_in"]), layer_norm_out=_lnp(w["layer_norm_out"]),
+        linear_a_p=_lin(w["linear_a_p"]), linear_a_g=_lin(w["linear_a_g"]),
+        linear_b_p=_lin(w["linear_b_p"]), linear_b_g=_lin(w["linear_b_g"]),
+        linear_g=_lin(w["linear_g"]), linear_z=_lin(w["linear_z"]),
+    )
+
+
+def trimul_to_boltz2(w: dict) -> dict:
+    """Field dict -> Boltz-2 dict (``p_in``/``g_in`` ``[c_z, 2c_h]``, a first)."""
+    cat = lambda a, b: np.concatenate([np.asarray(w[a]["weight"]), np.asarray(w[b]["weight"])], 0).T  # noqa: E731
+    return {
+        "norm_in": {"scale": w["layer_norm_in"]["weight"], "bias": w["layer_norm_in"]["bias"]},
+        "p_in": {"kernel": cat("linear_a_p", "linear_b_p")},
+        "g_in": {"kernel": cat("linear_a_g", "linear_b_g")},
+        "norm_out": {"scale": w["layer_norm_out"]["weight"], "bias": w["layer_norm_out"]["bias"]},
+        "p_out": {"kernel": np.asarray(w["linear_z"]["weight"]).T},
+        "g_out": {"kernel": np.asarray(w["linear_g"]["weight"]).T},
+    }
+
+
+def _attn(d) -> AttentionParams:
+    g = d.get("linear_g")
+    return AttentionParams(
+        linear_q=_lin(d["linear_q"]), linear_k=_lin(d["linear_k"]), linear_v=_lin(d["linear_v"]),
+        linear_o=_lin(d["linear_o"]), linear_g=None if g is None else _lin(g),
+    )
+
+
+def triattn_to_protenix(w: dict) -> ProtenixTriangleAttentionParams:
+    """Field dict (``foldjax_amd.synthetic.triattn_weights``) -> Protenix container."""
+    return ProtenixTriangleAttentionParams(
+        layer_norm=_lnp(w["layer_norm"]), linear=_lin(w["linear"]), attention=_attn(w["attention"])
+    )
+
+
+def triattn_to_openfold3(w: dict) -> OpenFold3TriangleAttentionParams:
+    return OpenFold3TriangleAttentionParams(
+        layer_norm=_lnp(w["layer_norm"]), linear_z=_lin(w["linear"]), mha=_attn(w["attention"])
+    )
+
+
+def triattn_to_boltz2(w: dict) -> dict:
+    att = w["attention"]
+    return {
+        "layer_norm": {"scale": w["layer_norm"]["weight"], "bias": w["layer_norm"]["bias"]},
+        "linear": {"kernel": np.asarray(w["linear"]["weight"]).T},
+        "mha": {n: {"kernel": np.asarray(att[n]["weight"]).T} for n in ("linear_q", "linear_k", "linear_v", "linear_o", "linear_g")},
+    }

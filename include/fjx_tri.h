@@ -1,0 +1,201 @@
+/*
+ * fjx_tri.h -- C ABI of the MI355X (gfx950) Pairformer triangle kernels.
+ *
+ * Plain C: device pointers, sizes, enums and a hipStream_t. No C++ or torch
+ * types cross this boundary. Every entry point enqueues its kernels on the
+ * given stream and returns without synchronising; buffers are owned by the
+ * caller (inputs, weights, outputs and the workspace). Nothing is retained
+ * between calls except read-only launch configuration and, when enabled, the
+ * per-kernel timing events of fjx_prof_*.
+ *
+ * Errors: every int-returning call returns FJX_OK (0) or an FJX_ERR_* code;
+ * fjx_last_error() then gives a message for the calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the eightmm/FoldJAX tree):
+ *   fjx_trimul_fwd     cuex.triangle_multiplicative_update as called from
+ *                      src/foldjax/models/boltz2/models/triangle/triangle_cueq.py:88-102
+ *                      and src/foldjax/models/protenix/models/triangle/triangle_cueq.py:28-47;
+ *                      numerically the XLA path of
+ *                      src/foldjax/models/boltz2/models/triangle/triangle.py:78-129.
+ *   fjx_triattn_fwd    the fused XLA module of
+ *                      src/foldjax/models/boltz2/models/triangle/triangle_attention.py:125-162
+ *                      (LN, mask bias, triangle bias, q/k/v/g projections,
+ *                      attention, gate, output projection; ending node by
+ *                      transposed addressing).
+ *   fjx_triattn_core   cueq_attention_core, src/foldjax/models/_cueq.py:66-121
+ *                      (cuex.triangle_attention with an additive mask).
+ */
+#ifndef FJX_TRI_H
+#define FJX_TRI_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FJX_ABI_VERSION 1
+
+/* element types of activations, masks and weights */
+enum { FJX_DTYPE_F32 = 0, FJX_DTYPE_BF16 = 1 };
+
+/* triangle multiplication direction (AF3 Algorithms 12 / 13) */
+enum { FJX_OUTGOING = 0, FJX_INCOMING = 1 };
+
+/* return codes */
+enum {
+  FJX_OK = 0,
+  FJX_ERR_INVALID = 1,     /* null pointer, bad enum, negative size */
+  FJX_ERR_UNSUPPORTED = 2, /* a shape this build has no kernel for */
+  FJX_ERR_WORKSPACE = 3,   /* workspace missing or smaller than required */
+  FJX_ERR_HIP = 4          /* a HIP runtime call failed */
+};
+
+/*
+ * Triangle multiplicative update, returning the update (or residual+update).
+ *
+ *   x_ln = LN_in(x)
+ *   a    = mask * sigmoid(x_ln g_in[:c_h]^T)  * (x_ln p_in[:c_h]^T)
+ *   b    = mask * sigmoid(x_ln g_in[c_h:]^T) * (x_ln p_in[c_h:]^T)
+ *   o    = outgoing: o[i,j,c] = sum_k a[i,k,c] b[j,k,c]
+ *          incoming: o[i,j,c] = sum_k a[k,i,c] b[k,j,c]
+ *   out  = (LN_out(o) p_out^T) * sigmoid(x_ln g_out^T)   (+ residual)
+ *
+ * Weights use the PyTorch [out, in] layout of the cuEquivariance call:
+ * p_in/g_in are [2*c_h, c_z] with the a rows first. In BF16 mode the
+ * contraction runs on bf16 MFMA with fp32 accumulation (the reference's
+ * fp32-upcast contraction of bf16 values, B2T/triangle.py:95-97) and o is
+ * rounded to bf16 before LN_out (B2T/triangle.py:124). Supported here:
+ * c_z == c_h == 128.
+ */
+typedef struct fjx_trimul_args {
+  int64_t batch;
+  int64_t n;
+  int64_t c_z;
+  int64_t c_h;
+  int32_t direction; /* FJX_OUTGOING or FJX_INCOMING */
+  int32_t dtype;     /* of x, mask, weights, residual and out */
+  float eps;         /* LayerNorm epsilon, 1e-5 in every port */
+  const void* x;     /* [batch, n, n, c_z] */
+  const void* mask;  /* [batch, n, n], or NULL for all ones */
+  const void* norm_in_weight;  /* [c_z] */
+  const void* norm_in_bias;    /* [c_z] */
+  const void* p_in_weight;     /* [2*c_h, c_z] */
+  const void* g_in_weight;     /* [2*c_h, c_z] */
+  const void* norm_out_weight; /* [c_h] */
+  const void* norm_out_bias;   /* [c_h] */
+  const void* p_out_weight;    /* [c_z, c_h] */
+  const void* g_out_weight;    /* [c_z, c_z] */
+  const void* residual;        /* NULL, or [batch, n, n, c_z] added to the update; may equal out */
+  void* out;                   /* [batch, n, n, c_z] */
+  void* workspace;
+  size_t workspace_bytes;
+} fjx_trimul_args;
+
+size_t fjx_trimul_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype);
+int fjx_trimul_fwd(const fjx_trimul_args* args, hipStream_t stream);
+
+/*
+ * Triangle attention around the starting (Algorithm 14) or ending
+ * (Algorithm 15) node, returning the update (or residual+update).
+ *
+ *   ending node: x and mask are read with their two pair axes swapped and the
+ *   result is written back swapped, without materialising a transpose.
+ *   x_ln      = LN(x)
+ *   mask_bias = inf * (mask[b,i,k] - 1)                 (fp32)
+ *   tri_bias  = x_ln w_bias^T, as [b, h, q, k]
+ *   q,k,v,g   = x_ln w_{q,k,v,g}^T, heads of width d
+ *   o[b,i,q]  = softmax_k( q.k / sqrt(d) + mask_bias[b,i,k] + tri_bias[b,h,q,k] ) v
+ *   out       = (sigmoid(g) * o) w_o^T                 (+ residual)
+ *
+ * Weights are PyTorch [out, in]. The softmax runs in fp32 with exp2 and the
+ * log2(e) factor folded into q and the biases. Supported here: c_z == 128,
+ * heads * head_dim == 128, head_dim == 32.
+ */
+typedef struct fjx_triattn_args {
+  int64_t batch;
+  int64_t n;
+  int64_t c_z;
+  int64_t heads;
+  int64_t head_dim;
+  int32_t starting; /* 1 = starting node, 0 = ending node */
+  int32_t dtype;
+  float eps;
+  float inf;        /* masking constant, 1e9 in every port */
+  const void* x;    /* [batch, n, n, c_z] */
+  const void* mask; /* [batch, n, n], or NULL for all ones */
+  const void* norm_weight;  /* [c_z] */
+  const void* norm_bias;    /* [c_z] */
+  const void* bias_weight;  /* [heads, c_z]   (Boltz-2 `linear`, OpenFold3 `linear_z`) */
+  const void* q_weight;     /* [heads*head_dim, c_z] */
+  const void* k_weight;     /* [heads*head_dim, c_z] */
+  const void* v_weight;     /* [heads*head_dim, c_z] */
+  const void* g_weight;     /* [heads*head_dim, c_z], or NULL for an ungated module */
+  const void* o_weight;     /* [c_z, heads*head_dim] */
+  const void* residual;     /* NULL, or [batch, n, n, c_z]; may equal out */
+  void* out;                /* [batch, n, n, c_z] */
+  void* workspace;
+  size_t workspace_bytes;
+} fjx_triattn_args;
+
+size_t fjx_triattn_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t heads,
+                                  int64_t head_dim, int32_t dtype);
+int fjx_triattn_fwd(const fjx_triattn_args* args, hipStream_t stream);
+
+/*
+ * Attention core with the cuEquivariance layouts (src/foldjax/models/_cueq.py:77-87):
+ *   q, k, v   [batch, rows, heads, n, head_dim]
+ *   tri_bias  [batch, heads, n, n]      (the row axis of [B,1,H,N,N] dropped)
+ *   mask_bias [batch, rows, n] fp32 additive, or NULL for zeros
+ *   out       [batch, rows, heads, n, head_dim]
+ * out = softmax(scale * q k^T + mask_bias + tri_bias) v per (batch, row, head).
+ * q/k/v/tri_bias/out share `dtype`. Supported here: head_dim == 32.
+ */
+typedef struct fjx_triattn_core_args {
+  int64_t batch;
+  int64_t rows;
+  int64_t heads;
+  int64_t n;
+  int64_t head_dim;
+  int32_t dtype;
+  float scale;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* tri_bias;
+  const float* mask_bias;
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+} fjx_triattn_core_args;
+
+size_t fjx_triattn_core_workspace_size(int64_t batch, int64_t rows, int64_t heads, int64_t n,
+                                       int64_t head_dim, int32_t dtype);
+int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
+
+/* Message for the last error on the calling thread ("" if none). */
+const char* fjx_last_error(void);
+
+/* FJX_ABI_VERSION of the loaded library. */
+int fjx_abi_version(void);
+
+/*
+ * Per-kernel timing with HIP events recorded on the launch stream around
+ * every kernel the library enqueues. Off by default. fjx_prof_collect waits
+ * for the recorded events, adds each kernel's elapsed time to its running
+ * total and count, and recycles the events; fjx_prof_read copies the totals.
+ */
+int fjx_prof_enable(int on);
+int fjx_prof_reset(void);
+int fjx_prof_collect(void);
+int fjx_prof_num_kernels(void);
+const char* fjx_prof_kernel_name(int id);
+int fjx_prof_read(int id, double* total_ms, int64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FJX_TRI_H */

@@ -1,0 +1,245 @@
+"""GPU parity of the HIP triangle kernels against the CPU oracle.
+
+Every test calls the HIP library through its C ABI (via ``foldjax_amd``) on
+seeded inputs and compares with ``oracle/triangle.py`` on the same values:
+max-abs <= 1e-4 in fp32 mode, relative (Frobenius) error <= 2e-2 in bf16 mode
+against the float64 oracle on the bf16-rounded inputs and weights.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from foldjax_amd import boltz2, kernels, openfold3, protenix
+from foldjax_amd import params as P
+from foldjax_amd import synthetic as syn
+from oracle import triangle as O
+from tests.gpu_util import assert_parity, device_tensor, mask_case, prep, prep_tree, say, to_np
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _trimul_case(n, dt, direction, mask_kind, seed=0):
+    dtype = DTYPES[dt]
+    say(f"trimul n={n} {dt} {direction} mask={mask_kind} seed={seed}")
+    z = syn.pair_input(n, 128, seed=seed)
+    m = mask_case(mask_kind, n)
+    w = syn.trimul_weights(128, 128, seed=seed + 2)
+    got = protenix.triangle_multiplication(
+        device_tensor(z, dtype), device_tensor(m, dtype), P.trimul_to_protenix(w), direction
+    )
+    torch.cuda.synchronize()
+    want = O.protenix_triangle_multiplication(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), direction)
+    return to_np(got), want, dtype
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("n,mask_kind", [(5, "random"), (17, "ones"), (33, "tail"), (64, "random"), (100, "row0"), (130, "tail")])
+def test_trimul_parity(dt, direction, n, mask_kind):
+    got, want, dtype = _trimul_case(n, dt, direction, mask_kind)
+    assert got.shape == want.shape
+    assert_parity(got, want, dtype, f"trimul {direction} n={n}")
+
+
+def _valid_rows(m: np.ndarray, starting: bool) -> np.ndarray:
+    mv = m if starting else m.T
+    return mv.max(axis=1) > 0
+
+
+def _triattn_case(n, dt, starting, mask_kind, seed=0, heads=4):
+    dtype = DTYPES[dt]
+    say(f"triattn n={n} {dt} starting={starting} mask={mask_kind} seed={seed}")
+    z = syn.pair_input(n, 128, seed=seed)
+    m = mask_case(mask_kind, n)
+    w = syn.triattn_weights(128, heads, 128 // heads, seed=seed + 2)
+    got = protenix.triangle_attention(
+        device_tensor(z, dtype), device_tensor(m, dtype), P.triattn_to_protenix(w), num_heads=heads, starting=starting
+    )
+    torch.cuda.synchronize()
+    want = O.protenix_triangle_attention(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), num_heads=heads,
+                                         starting=starting)
+    return to_np(got), want, dtype, m
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("n,mask_kind", [(5, "random"), (17, "ones"), (33, "tail"), (64, "random"), (100, "row0"), (130, "tail")])
+def test_triattn_parity(dt, starting, n, mask_kind):
+    got, want, dtype, m = _triattn_case(n, dt, starting, mask_kind)
+    assert np.all(np.isfinite(got)), "non-finite output (fully masked rows must stay finite)"
+    rows = _valid_rows(m, starting)
+    if starting:
+        g, w_ = got[rows], want[rows]
+    else:
+        g, w_ = got[:, rows], want[:, rows]
+    assert_parity(g, w_, dtype, f"triattn starting={starting} n={n}")
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+def test_triattn_core_matches_oracle(dt):
+    dtype = DTYPES[dt]
+    say(f"triattn_core {dt}")
+    rng = np.random.default_rng(4)
+    b, i, h, n, d = 2, 3, 4, 70, 32
+    q, k, v = (rng.standard_normal((b, i, h, n, d)).astype(np.float32) for _ in range(3))
+    tb = rng.standard_normal((b, 1, h, n, n)).astype(np.float32)
+    mask = (rng.random((b, i, n)) > 0.2).astype(np.float32)
+    mask[..., 0] = 1
+    mb = (1e9 * (mask - 1.0))[:, :, None, None, :].astype(np.float32)
+    scale = d ** -0.5
+    got = boltz2.hip_attention_core(device_tensor(q, dtype), device_tensor(k, dtype), device_tensor(v, dtype),
+                                    device_tensor(tb, dtype), torch.from_numpy(mb).cuda(), scale=scale)
+    torch.cuda.synchronize()
+    want = O.attention_core(prep(q, dtype), prep(k, dtype), prep(v, dtype), prep(tb, dtype), mb.astype(np.float64), scale)
+    assert_parity(to_np(got), want, dtype, "triattn_core")
+
+
+def test_ports_agree_on_device():
+    """Boltz-2, Protenix and OpenFold3 entry points run the same kernels on
+    the same weights and agree to the last bit."""
+    say("ports agree n=48 bf16")
+    n, dtype = 48, torch.bfloat16
+    z = device_tensor(syn.pair_input(n, 128, seed=5), dtype)
+    m = device_tensor(mask_case("tail", n), dtype)
+    tm = syn.trimul_weights(seed=6)
+    ta = syn.triattn_weights(seed=7)
+    a = protenix.triangle_multiplication(z, m, P.trimul_to_protenix(tm), "incoming")
+    b = openfold3.triangle_multiplication(z, P.trimul_to_openfold3(tm), outgoing=False, mask=m)
+    c = boltz2.triangle_multiplication_forward(P.trimul_to_boltz2(tm), z, m, "incoming")
+    assert torch.equal(a, b) and torch.equal(a, c)
+    a = protenix.triangle_attention(z, m, P.triattn_to_protenix(ta), num_heads=4, starting=False)
+    b = openfold3.triangle_attention(z, P.triattn_to_openfold3(ta), no_heads=4, mask=m, starting=False)
+    c = boltz2.triangle_attention_forward(P.triattn_to_boltz2(ta), z, m, starting=False)
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_residual_fused_equals_added():
+    say("residual fused n=40")
+    n, dtype = 40, torch.float32
+    z = device_tensor(syn.pair_input(n, seed=8), dtype)
+    m = device_tensor(mask_case("random", n), dtype)
+    w = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(seed=9)), dtype, "cuda")
+    upd = kernels.trimul(z, m, w, "outgoing")
+    fused = kernels.trimul(z, m, w, "outgoing", residual=z)
+    torch.testing.assert_close(fused, z + upd, rtol=1e-6, atol=1e-6)
+    wa = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(seed=10)), dtype, "cuda")
+    upd = kernels.triattn(z, m, wa, starting=False)
+    fused = kernels.triattn(z, m, wa, starting=False, residual=z)
+    torch.testing.assert_close(fused, z + upd, rtol=1e-6, atol=1e-6)
+
+
+def test_batch_axis_matches_per_item():
+    say("batch axis n=24 B=3")
+    n, dtype = 24, torch.float32
+    zb = device_tensor(syn.pair_input(n, seed=11, batch=3), dtype)
+    mb = device_tensor(np.stack([mask_case(k, n) for k in ("ones", "tail", "random")]), dtype)
+    w = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(seed=12)), dtype, "cuda")
+    wa = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(seed=13)), dtype, "cuda")
+    out = kernels.trimul(zb, mb, w, "incoming")
+    att = kernels.triattn(zb, mb, wa, starting=True)
+    for i in range(3):
+        torch.testing.assert_close(out[i], kernels.trimul(zb[i], mb[i], w, "incoming"), rtol=0, atol=0)
+        torch.testing.assert_close(att[i], kernels.triattn(zb[i], mb[i], wa, starting=True), rtol=0, atol=0)
+
+
+def test_mask_none_equals_all_ones():
+    say("mask None n=20")
+    n, dtype = 20, torch.bfloat16
+    z = device_tensor(syn.pair_input(n, seed=14), dtype)
+    ones = torch.ones(n, n, dtype=dtype, device="cuda")
+    w = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(seed=15)), dtype, "cuda")
+    wa = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(seed=16)), dtype, "cuda")
+    assert torch.equal(kernels.trimul(z, None, w, "outgoing"), kernels.trimul(z, ones, w, "outgoing"))
+    assert torch.equal(kernels.triattn(z, None, wa), kernels.triattn(z, ones, wa))
+
+
+def test_config1_trimul_out_then_in_fp32_n256():
+    """outgoing then incoming update, fp32, all-ones mask."""
+    say("config1 trimul out+in n=256 fp32")
+    n, dtype = 256, torch.float32
+    z = syn.pair_input(n, 128, seed=0)
+    m = np.ones((n, n), np.float32)
+    w_out = syn.trimul_weights(seed=2)
+    w_in = syn.trimul_weights(seed=3)
+    zt = device_tensor(z, dtype)
+    mt = device_tensor(m, dtype)
+    zt = protenix.triangle_multiplication(zt, mt, P.trimul_to_protenix(w_out), "outgoing", residual=zt)
+    zt = protenix.triangle_multiplication(zt, mt, P.trimul_to_protenix(w_in), "incoming", residual=zt)
+    torch.cuda.synchronize()
+    ref = z.astype(np.float64)
+    ref = ref + O.protenix_triangle_multiplication(ref, m, w_out, "outgoing")
+    ref = ref + O.protenix_triangle_multiplication(ref, m, w_in, "incoming")
+    assert_parity(to_np(zt), ref, dtype, "config1")
+
+
+def test_config2_triattn_start_end_bf16_n384():
+    """starting then ending node, bf16, N=384, last 10% padded."""
+    say("config2 triattn start+end n=384 bf16")
+    n, dtype = 384, torch.bfloat16
+    n_real = n - 38
+    z = syn.pair_input(n, 128, seed=0)
+    m = syn.pair_mask(n, n_real)
+    w_s = syn.triattn_weights(seed=2)
+    w_e = syn.triattn_weights(seed=3)
+    zt = device_tensor(z, dtype)
+    mt = device_tensor(m, dtype)
+    zt = protenix.triangle_attention(zt, mt, P.triattn_to_protenix(w_s), num_heads=4, starting=True, residual=zt)
+    zt = protenix.triangle_attention(zt, mt, P.triattn_to_protenix(w_e), num_heads=4, starting=False, residual=zt)
+    torch.cuda.synchronize()
+    got = to_np(zt)
+    assert np.all(np.isfinite(got))
+    # the fp32 reference sees the bf16 input, runs in float64 between the two
+    # sublayers (the GPU rounds z to bf16 there: inside the 2e-2 budget)
+    ref = prep(z, dtype)
+    ref = ref + O.protenix_triangle_attention(ref, m, prep_tree(w_s, dtype), num_heads=4, starting=True)
+    ref = ref + O.protenix_triangle_attention(ref, m, prep_tree(w_e, dtype), num_heads=4, starting=False)
+    v = slice(0, n_real)
+    assert_parity(got[v, v], ref[v, v], dtype, "config2 valid region")
+
+
+def test_ending_is_transposed_starting_bitexact_n1024():
+    """Size-independent property at the headline size: the ending node on z
+    equals the starting node on z^T, transposed back, bit for bit."""
+    say("ending == transposed starting n=1024 bf16")
+    n, dtype = 1024, torch.bfloat16
+    z = device_tensor(syn.pair_input(n, 128, seed=21), dtype)
+    m = device_tensor(syn.pair_mask(n, n - 51), dtype)
+    wa = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(seed=22)), dtype, "cuda")
+    end = kernels.triattn(z, m, wa, starting=False)
+    start_t = kernels.triattn(z.transpose(0, 1).contiguous(), m.t().contiguous(), wa, starting=True)
+    assert torch.equal(end, start_t.transpose(0, 1))
+
+
+def test_triattn_sampled_rows_n1024_bf16():
+    """Full-size parity on sampled rows: attention rows are independent, so the
+    oracle evaluates a handful of rows of the N=1024 problem exactly."""
+    say("triattn sampled rows n=1024 bf16")
+    n, dtype = 1024, torch.bfloat16
+    n_real = n - 51
+    z = syn.pair_input(n, 128, seed=31)
+    m = syn.pair_mask(n, n_real)
+    w = syn.triattn_weights(seed=32)
+    got = to_np(protenix.triangle_attention(device_tensor(z, dtype), device_tensor(m, dtype), P.triattn_to_protenix(w),
+                                            num_heads=4, starting=True))
+    zq, wq = prep(z, dtype), prep_tree(w, dtype)
+    rows = [0, 1, 500, n_real - 1]
+    # LN/projections are per position; attention for row i needs row i only,
+    # except the bias which needs all positions: compute it once.
+    xl = O.layer_norm(zq, wq["layer_norm"]["weight"], wq["layer_norm"]["bias"])
+    bias = np.moveaxis(xl @ np.asarray(wq["linear"]["weight"]).T, -1, 0)  # [H, N, N]
+    att = wq["attention"]
+    for i in rows:
+        x = xl[i]  # [J, C]
+        proj = lambda name: (x @ np.asarray(att[name]["weight"]).T).reshape(n, 4, 32).transpose(1, 0, 2)  # noqa: E731
+        q = proj("linear_q") / np.sqrt(32)
+        k, v = proj("linear_k"), proj("linear_v")
+        s = q @ k.transpose(0, 2, 1) + (1e9 * (m[i] - 1.0))[None, None, :] + bias
+        o = O.softmax(s) @ v  # [H, J, D]
+        o = o.transpose(1, 0, 2) * O.sigmoid(x @ np.asarray(att["linear_g"]["weight"]).T).reshape(n, 4, 32)
+        want = o.reshape(n, 128) @ np.asarray(att["linear_o"]["weight"]).T
+        assert_parity(got[i], want, dtype, f"row {i}")
