@@ -81,9 +81,17 @@ def silu(x):
     return x * sigmoid(x)
 
 
+def _mm(x, w_in_out):
+    """``x @ W`` over the last axis, as one contiguous 2-D BLAS call."""
+    x = _f(x)
+    w = np.ascontiguousarray(_f(w_in_out))
+    y = np.ascontiguousarray(x).reshape(-1, x.shape[-1]) @ w
+    return y.reshape(x.shape[:-1] + (w.shape[-1],))
+
+
 def linear_torch(x, lin):
     """PyTorch-layout linear ``x @ W.T + b`` (``PXP/primitives.py:48-54``)."""
-    y = _f(x) @ _f(_get(lin, "weight")).T
+    y = _mm(x, _f(_get(lin, "weight")).T)
     b = _get(lin, "bias")
     if b is not None:
         y = y + _f(b)
@@ -121,9 +129,9 @@ def triangle_contract(a, b, direction):
     ac = np.moveaxis(a, -1, -3)  # [..., C, N, N]
     bc = np.moveaxis(b, -1, -3)
     if direction == "outgoing":
-        out = ac @ np.swapaxes(bc, -1, -2)
+        out = np.ascontiguousarray(ac) @ np.ascontiguousarray(np.swapaxes(bc, -1, -2))
     elif direction == "incoming":
-        out = np.swapaxes(ac, -1, -2) @ bc
+        out = np.ascontiguousarray(np.swapaxes(ac, -1, -2)) @ np.ascontiguousarray(bc)
     else:
         raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
     return np.moveaxis(out, -3, -1)
@@ -144,13 +152,13 @@ def boltz2_triangle_multiplication(params, x, mask, direction, eps=1e-5):
     """
     x = layer_norm(x, params["norm_in"]["scale"], params["norm_in"]["bias"], eps)
     mask = _f(mask)
-    proj = sigmoid(x @ _f(params["g_in"]["kernel"])) * (x @ _f(params["p_in"]["kernel"]))
+    proj = sigmoid(_mm(x, params["g_in"]["kernel"])) * _mm(x, params["p_in"]["kernel"])
     proj = proj * mask[..., None]
     a, b = np.split(proj, 2, axis=-1)
     out = triangle_contract(a, b, direction)
     out = layer_norm(out, params["norm_out"]["scale"], params["norm_out"]["bias"], eps)
-    out = out @ _f(params["p_out"]["kernel"])
-    gate = sigmoid(x @ _f(params["g_out"]["kernel"]))
+    out = _mm(out, params["p_out"]["kernel"])
+    gate = sigmoid(_mm(x, params["g_out"]["kernel"]))
     return out * gate
 
 
@@ -221,9 +229,9 @@ def attention_rows(q, k, v, mask_bias, tri_bias, row_block=16):
         e = min(n_rows, s + row_block)
         qs, ks, vs = q[..., s:e, :, :, :], k[..., s:e, :, :, :], v[..., s:e, :, :, :]
         mb = mask_bias[..., s:e, :, :, :] if mask_bias.shape[-4] > 1 else mask_bias
-        scores = qs @ np.swapaxes(ks, -1, -2)
+        scores = np.ascontiguousarray(qs) @ np.ascontiguousarray(np.swapaxes(ks, -1, -2))
         scores = scores + mb + tri_bias
-        out[..., s:e, :, :, :] = softmax(scores, axis=-1) @ vs
+        out[..., s:e, :, :, :] = softmax(scores, axis=-1) @ np.ascontiguousarray(vs)
     return out
 
 
@@ -253,14 +261,14 @@ def boltz2_triangle_attention(params, x, mask=None, starting=True, inf=1e9, eps=
         mask = np.swapaxes(mask, -1, -2)
     x = layer_norm(x, params["layer_norm"]["scale"], params["layer_norm"]["bias"], eps)
     mask_bias = (inf * (mask - 1.0))[..., :, None, None, :]
-    tri_bias = x @ _f(params["linear"]["kernel"])  # [..., I, J, H]
+    tri_bias = _mm(x, params["linear"]["kernel"])  # [..., I, J, H]
     tri_bias = np.moveaxis(tri_bias, -1, -3)[..., None, :, :, :]
     mha = params["mha"]
     heads = tri_bias.shape[-3]
     d = _f(mha["linear_g"]["kernel"]).shape[-1] // heads
 
     def proj(name):
-        y = x @ _f(mha[name]["kernel"])
+        y = _mm(x, mha[name]["kernel"])
         y = y.reshape(y.shape[:-1] + (heads, d))
         return np.swapaxes(y, -2, -3)
 
@@ -269,9 +277,9 @@ def boltz2_triangle_attention(params, x, mask=None, starting=True, inf=1e9, eps=
     v = proj("linear_v")
     o = attention_rows(q, k, v, mask_bias, tri_bias)
     o = np.swapaxes(o, -2, -3)  # [..., I, J, H, D]
-    gate = sigmoid(x @ _f(mha["linear_g"]["kernel"])).reshape(o.shape)
+    gate = sigmoid(_mm(x, mha["linear_g"]["kernel"])).reshape(o.shape)
     o = (o * gate).reshape(o.shape[:-2] + (heads * d,))
-    out = o @ _f(mha["linear_o"]["kernel"])
+    out = _mm(o, mha["linear_o"]["kernel"])
     if not starting:
         out = np.swapaxes(out, -2, -3)
     return out
