@@ -6,7 +6,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/fjx_tri.h"
+#include "fjx_tri.h"
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
 
@@ -129,7 +129,7 @@ __global__ void transpose_v_kernel(const T* __restrict__ src, T* __restrict__ ds
     dst[idx] = s < n ? src[(hr * n + s) * 32 + d] : from_f32<T>(0.f);
   }
 }
-// bias [B][H][n][n] -> [B][H][np][np], zeros outside
+// bias [B][H][n][n] -> [B][H][np][np] times log2 e, zeros outside
 template <typename T>
 __global__ void pad_bias_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t np,
                                 int64_t planes) {
@@ -139,7 +139,7 @@ __global__ void pad_bias_kernel(const T* __restrict__ src, T* __restrict__ dst, 
     const int64_t k = idx % np;
     const int64_t q = (idx / np) % np;
     const int64_t pl = idx / (np * np);
-    dst[idx] = (q < n && k < n) ? src[(pl * n + q) * n + k] : from_f32<T>(0.f);
+    dst[idx] = (q < n && k < n) ? from_f32<T>(to_f32(src[(pl * n + q) * n + k]) * kLog2e) : from_f32<T>(0.f);
   }
 }
 // mask bias [B][R][n] fp32 -> [B][R][np] times log2 e, -inf for padded keys

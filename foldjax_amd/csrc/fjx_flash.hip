@@ -3,20 +3,29 @@
 // One wave owns one attention row i of the pair grid and 64 queries of one
 // head; the ROWS waves of a workgroup own ROWS consecutive rows with the same
 // head and query tile, so the [64 x 64] tile of the triangle bias -- shared by
-// every row -- is staged once in LDS per key block and read by all of them.
+// every row -- is staged once in LDS per key block (double-buffered, the next
+// tile prefetched into registers while the current one is consumed) and read
+// by all of them.
 //
 // Everything is computed transposed so that each lane keeps one query:
 //   S^T[key][q] = K[key][:] . Q[q][:]   (A = K fragment, B = Q fragment)
 //   lane l holds S^T[16kt + 4g + r][16qt + l%16], g = l/16
-// The online-softmax state (running max m, partial sum l) therefore lives in
-// the lane of its query; only the block max needs a 4-lane reduction. The
-// probabilities then feed the second product directly as the B operand,
+// with the accumulator initialised to the bias tile (plus the mask bias when
+// the block holds masked keys). The online-softmax max lives in the lane of
+// its query; the block max needs one reduction over the 4 lane groups
+// (v_permlane16/32_swap). The probabilities feed the second product directly
+// as the B operand,
 //   O^T[d][q] += V^T[d][keys] . P^T[keys][q]
 // with the 8 keys of lane group g in a 32-key chunk c taken as
-// {32c + 4g + 0..3, 32c + 16 + 4g + 0..3} -- the keys that lane already holds
-// -- and the V^T fragment loaded with the same key assignment.
-// Scores are in log2 units: q carries scale*log2(e), the bias and mask bias
-// are multiplied by log2(e), and exp2 is used.
+// {32c + 4g + 0..3, 32c + 16 + 4g + 0..3} -- the keys that lane already holds --
+// and the V^T fragment loaded with the same key assignment. The softmax
+// denominator is a third product with an all-ones A operand, so the running
+// sums cost MFMA cycles instead of VALU adds. Rescaling of O and of the sums
+// is skipped when no query's running max moved (a wave-uniform test).
+// Scores are in log2 units: q carries scale*log2(e), and the bias and mask
+// bias arrive multiplied by log2(e).
+#include <type_traits>
+
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
 
@@ -26,6 +35,8 @@ constexpr int kQT = 64;   // queries per wave
 constexpr int kKB = 64;   // keys per block
 constexpr int kD = 32;    // head dim
 constexpr int kNumXcdF = 8;
+constexpr int kBiasLd = kKB + 4;  // padded LDS row (floats)
+constexpr int kMaxBlocks = 1024;  // key blocks per row: N <= 65536
 
 __device__ __forceinline__ int64_t xcd_remap_f(int64_t w, int64_t total) {
   const int64_t per = total / kNumXcdF;
@@ -33,7 +44,7 @@ __device__ __forceinline__ int64_t xcd_remap_f(int64_t w, int64_t total) {
   return (w % kNumXcdF) * per + w / kNumXcdF;
 }
 
-// 4 contiguous elements -> 4 fp32 / half of an 8-element fragment
+// 4 contiguous elements into half of an 8-element fragment
 __device__ __forceinline__ void load4_into(const bf16* p, bf16x8& f, int half) {
   const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
 #pragma unroll
@@ -45,9 +56,27 @@ __device__ __forceinline__ void load4_into(const float* p, f32x8& f, int half) {
   for (int e = 0; e < 4; ++e) f[4 * half + e] = v[e];
 }
 
+// max over the 4 lanes {l%16 + 16g}
+__device__ __forceinline__ float max_over_groups(float x) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+template <typename T> __device__ __forceinline__ typename Frag<T>::type ones8();
+template <> __device__ __forceinline__ bf16x8 ones8<bf16>() {
+  const bf16 o = static_cast<bf16>(1.0f);
+  return bf16x8{o, o, o, o, o, o, o, o};
+}
+template <> __device__ __forceinline__ f32x8 ones8<float>() { return f32x8{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f}; }
+
 template <typename T, int ROWS>
-__global__ __launch_bounds__(64 * ROWS) void flash_tri_kernel(FlashParams<T> P) {
-  __shared__ __attribute__((aligned(16))) float bias_s[kQT][kKB + 4];
+__device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
+  __shared__ __attribute__((aligned(16))) float bias_s[2][kQT][kBiasLd];
+  __shared__ unsigned char blk_masked[ROWS][kMaxBlocks];
 
   const int64_t n = P.n;
   const int64_t np = P.np;
@@ -80,107 +109,137 @@ __global__ __launch_bounds__(64 * ROWS) void flash_tri_kernel(FlashParams<T> P) 
   const float* MB = P.mb + (b * P.rows + i) * np;
   const T* BIAS = P.bias + b * P.bias_stride_b + h * np * np;
 
+  // which key blocks of this row hold a non-zero mask bias (masked or padded keys)
+  const int64_t nblk = np / kKB;
+  for (int64_t blk0 = 0; blk0 < nblk; blk0 += 8) {
+    float mv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mv[u] = blk0 + u < nblk ? MB[(blk0 + u) * kKB + lane] : 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool any = __builtin_amdgcn_ballot_w64(mv[u] != 0.f) != 0;
+      if (lane == 0 && blk0 + u < nblk) blk_masked[wave][blk0 + u] = any ? 1 : 0;
+    }
+  }
+
   typedef typename Frag<T>::type FragT;
   FragT qf[4];
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) qf[qt] = load8(Q + (q0 + 16 * qt + li) * kD + 8 * lg);
+  const FragT ones = ones8<T>();
 
-  float m[4], l[4];
-  f32x4 o[2][4];
+  float m[4];
+  f32x4 o[2][4], lsum[4];
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
     m[qt] = -1.0e30f;
-    l[qt] = 0.f;
+    lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     o[0][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     o[1][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // bias tile fill: each thread moves PER consecutive elements of one row
   constexpr int NT = 64 * ROWS;
-  constexpr int PER = kQT * kKB / NT;  // bias elements per thread per block
-
-  for (int64_t k0 = 0; k0 < np; k0 += kKB) {
-    __syncthreads();
-    {
-      const int e0 = t * PER;
-      const int br = e0 / kKB;
-      const int bc = e0 % kKB;
-      const T* src = BIAS + (q0 + br) * np + k0 + bc;
+  constexpr int PER = kQT * kKB / NT;
+  const int e0 = t * PER;
+  const int br = e0 / kKB;
+  const int bc = e0 % kKB;
+  const T* bsrc = BIAS + (q0 + br) * np + bc;
+  typename Frag<T>::type breg[PER / 8];
 #pragma unroll
-      for (int c = 0; c < PER; c += 8) {
-        float f[8];
-        to_f32x8(load8(src + c), f);
-        f32x4 lo = {f[0] * kLog2e, f[1] * kLog2e, f[2] * kLog2e, f[3] * kLog2e};
-        f32x4 hi = {f[4] * kLog2e, f[5] * kLog2e, f[6] * kLog2e, f[7] * kLog2e};
-        *reinterpret_cast<f32x4*>(&bias_s[br][bc + c]) = lo;
-        *reinterpret_cast<f32x4*>(&bias_s[br][bc + c + 4]) = hi;
-      }
+  for (int c = 0; c < PER / 8; ++c) breg[c] = load8(bsrc + 8 * c);
+  auto put_bias = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < PER / 8; ++c) {
+      float f[8];
+      to_f32x8(breg[c], f);
+      *reinterpret_cast<f32x4*>(&bias_s[buf][br][bc + 8 * c]) = f32x4{f[0], f[1], f[2], f[3]};
+      *reinterpret_cast<f32x4*>(&bias_s[buf][br][bc + 8 * c + 4]) = f32x4{f[4], f[5], f[6], f[7]};
     }
-    __syncthreads();
+  };
+  put_bias(0);
 
-    f32x4 s[4][4];  // [kt][qt]
+  FragT kf[4];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const FragT kf = load8(K + (k0 + 16 * kt + li) * kD + 8 * lg);
-      const f32x4 mbv = *reinterpret_cast<const f32x4*>(MB + k0 + 16 * kt + 4 * lg);
+  for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (16 * kt + li) * kD + 8 * lg);
+  __syncthreads();
+
+  for (int64_t blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    const int64_t k0 = blk * kKB;
+    const bool more = blk + 1 < nblk;
+    if (more) {
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
-        f32x4 init = *reinterpret_cast<const f32x4*>(&bias_s[16 * qt + li][16 * kt + 4 * lg]);
-        init += mbv;
-        mma(init, kf, qf[qt]);
-        s[kt][qt] = init;
-      }
+      for (int c = 0; c < PER / 8; ++c) breg[c] = load8(bsrc + k0 + kKB + 8 * c);
     }
+    const bool masked_blk = blk_masked[wave][blk] != 0;
+    FragT vf[2][2];  // [dt][c]
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const T* vrow = VT + (int64_t)(16 * dt + li) * np + k0 + 32 * c + 4 * lg;
+        load4_into(vrow, vf[dt][c], 0);
+        load4_into(vrow + 16, vf[dt][c], 1);
+      }
 
-    // online softmax per query (one query per lane per qt)
+    // the two instantiations differ only in adding the mask bias; branching
+    // here keeps the common all-valid block free of those adds
+    auto block_body = [&](auto masked_tag) {
+      constexpr bool kMasked = decltype(masked_tag)::value;
+      f32x4 mbv[4];
+      if (kMasked) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) mbv[kt] = *reinterpret_cast<const f32x4*>(MB + k0 + 16 * kt + 4 * lg);
+      }
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
-      float mx = s[0][qt][0];
+      f32x4 s[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+      for (int kt = 0; kt < 4; ++kt) {
+        s[kt] = *reinterpret_cast<const f32x4*>(&bias_s[buf][16 * qt + li][16 * kt + 4 * lg]);
+        if (kMasked) s[kt] += mbv[kt];
+        mma(s[kt], kf[kt], qf[qt]);
+      }
+      if (qt == 3 && more) {
+        // K of this block is consumed: fetch the next block's into the same registers
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][qt][r]);
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float mnew = fmaxf(m[qt], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
+        for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (k0 + kKB + 16 * kt + li) * kD + 8 * lg);
+      }
+      float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+      for (int kt = 1; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
+      mx = max_over_groups(mx);
+      const float mold = m[qt];
+      const float mnew = fmaxf(mold, mx);
+      if (__builtin_amdgcn_ballot_w64(mnew > mold) != 0) {
+        const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
+        o[0][qt] *= alpha;
+        o[1][qt] *= alpha;
+        lsum[qt] *= alpha;
+      }
       m[qt] = mnew;
-      float ls = 0.f;
+      float pv[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(s[kt][qt][r] - mnew);
-          s[kt][qt][r] = p;
-          ls += p;
-        }
-      l[qt] = l[qt] * alpha + ls;
-      o[0][qt] *= alpha;
-      o[1][qt] *= alpha;
+        for (int r = 0; r < 4; ++r) pv[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] - mnew);
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const float f[8] = {pv[2 * c][0], pv[2 * c][1], pv[2 * c][2], pv[2 * c][3],
+                            pv[2 * c + 1][0], pv[2 * c + 1][1], pv[2 * c + 1][2], pv[2 * c + 1][3]};
+        const FragT pf = pack8<T>(f);
+        mma(o[0][qt], vf[0][c], pf);
+        mma(o[1][qt], vf[1][c], pf);
+        mma(lsum[qt], ones, pf);
+      }
     }
+    };
+    if (masked_blk) block_body(std::true_type{});
+    else block_body(std::false_type{});
 
-    // O^T += V^T P^T over two 32-key chunks
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      FragT vf[2];
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const T* vrow = VT + (int64_t)(16 * dt + li) * np + k0 + 32 * c + 4 * lg;
-        load4_into(vrow, vf[dt], 0);
-        load4_into(vrow + 16, vf[dt], 1);
-      }
-#pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
-        float pv[8];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          pv[r] = s[2 * c][qt][r];
-          pv[4 + r] = s[2 * c + 1][qt][r];
-        }
-        const FragT pf = pack8<T>(pv);
-#pragma unroll
-        for (int dt = 0; dt < 2; ++dt) mma(o[dt][qt], vf[dt], pf);
-      }
-    }
+    if (more) put_bias(buf ^ 1);
+    __syncthreads();
   }
 
   if (!row_ok) return;
@@ -188,31 +247,45 @@ __global__ __launch_bounds__(64 * ROWS) void flash_tri_kernel(FlashParams<T> P) 
   const T* G = P.gate ? P.gate + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head : nullptr;
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
-    float lt = l[qt];
-    lt += shfl_xor(lt, 16);
-    lt += shfl_xor(lt, 32);
-    const float inv = 1.0f / lt;
+    const float inv = 1.0f / lsum[qt][0];
     const int64_t q = q0 + 16 * qt + li;
     if (q >= n) continue;
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt) {
       const int64_t off = q * P.o_stride_q + 16 * dt + 4 * lg;
+      float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float v = o[dt][qt][r] * inv;
-        if (G) v *= to_f32(G[off + r]);
-        OUT[off + r] = from_f32<T>(v);
+      for (int r = 0; r < 4; ++r) v[r] = o[dt][qt][r] * inv;
+      if (G) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] *= to_f32(G[off + r]);
       }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) OUT[off + r] = from_f32<T>(v[r]);
     }
   }
 }
 
+constexpr int kRows = 4;
+
+// bf16: 3 waves per SIMD (168 VGPRs) measured faster than 2 without spills;
+// the fp32 variant would spill heavily under that cap and keeps 2.
+__global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void flash_tri_kernel_bf16(FlashParams<bf16> P) {
+  flash_tri_body<bf16, kRows>(P);
+}
+__global__ __launch_bounds__(64 * kRows) void flash_tri_kernel_f32(FlashParams<float> P) {
+  flash_tri_body<float, kRows>(P);
+}
+
 template <typename T>
 void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st) {
-  constexpr int ROWS = 4;
-  const int64_t rg = (p.rows + ROWS - 1) / ROWS;
+  const int64_t rg = (p.rows + kRows - 1) / kRows;
   const int64_t total = batch * p.heads * rg * (p.np / kQT);
-  hipLaunchKernelGGL((flash_tri_kernel<T, ROWS>), dim3((unsigned)total), dim3(64 * ROWS), 0, st, p);
+  if constexpr (std::is_same<T, bf16>::value)
+    hipLaunchKernelGGL(flash_tri_kernel_bf16, dim3((unsigned)total), dim3(64 * kRows), 0, st, p);
+  else
+    hipLaunchKernelGGL(flash_tri_kernel_f32, dim3((unsigned)total), dim3(64 * kRows), 0, st, p);
 }
 
 template void launch_flash<bf16>(const FlashParams<bf16>&, int64_t, hipStream_t);

@@ -77,7 +77,7 @@ struct FlashParams {
   const T* q;        // [B][N][H][Np][32], pre-scaled by scale*log2 e
   const T* k;        // [B][N][H][Np][32]
   const T* vt;       // [B][N][H*32][Np]
-  const T* bias;     // [B][H][Np][Np], raw (multiplied by log2 e in-kernel)
+  const T* bias;     // [B][H][Np][Np], already times log2 e
   const float* mb;   // [B][N][Np], already times log2 e; -inf for padded keys
   const T* gate;     // optional, indexed like out
   T* out;            // out[b][i][q][h*32+d] via the strides below

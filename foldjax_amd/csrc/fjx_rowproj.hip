@@ -224,7 +224,7 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(TriMulProloguePara
 //   k  [B][N][H][Np][D]
 //   vt [B][N][H*D][Np]   v transposed so that keys are contiguous
 //   g  [B][N][N][H*D]    sigmoid(x_ln w_g^T), or absent
-//   bias [B][H][Np][Np]  x_ln w_bias^T (raw value, in T)
+//   bias [B][H][Np][Np]  x_ln w_bias^T times log2 e (in T)
 //   mb [B][N][Np] fp32   inf*(mask-1)*log2 e, -inf for keys >= N
 // Np = N rounded up to 64; padded key slots of q/k/vt are written as zeros.
 // ---------------------------------------------------------------------------
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(TriAttnProloguePa
           for (int e = 0; e < 8; ++e) acc += xv[e] * wv[e];
         }
       }
-      P.bias[(((int64_t)b * H + h) * np + r) * np + s] = from_f32<T>(acc);
+      P.bias[(((int64_t)b * H + h) * np + r) * np + s] = from_f32<T>(acc * kLog2e);
     }
   }
 
