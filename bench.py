@@ -1,9 +1,11 @@
-"""Benchmark of the Pairformer triangle hot path on one MI355X.
+"""Benchmark of one Pairformer block on one MI355X.
 
-One step = one pass of the pair-track triangle sublayers of a Pairformer
-block (tri-mul outgoing, incoming, tri-attn starting, ending; residuals
-fused) at N=1024, c_z=128, 4 heads x 32, bf16, on a synthetic z ~ N(0,1) with
-a 5% padded tail (973 real tokens) and random-init weights.
+One step = one Boltz-2-form Pairformer layer at N=1024, c_z=128, c_s=384,
+bf16: tri-mul outgoing and incoming, tri-attn starting and ending node
+(4 heads x 32), the pair transition (4x SwiGLU), the single attention with
+pair bias (16 heads) and the single transition, every residual fused. Inputs
+are synthetic (z, s ~ N(0,1), PCG64 seeds 0/1) with a 5% padded tail (973 real
+tokens) and random-init weights (seed 2).
 
 Prints one JSON line. Per-kernel durations come from HIP events that the
 library records on its launch stream around every kernel during the timed
@@ -44,12 +46,12 @@ def _args():
 
 
 def cpu_baseline(n_target: int, n_sample: int, budget_s: float = 25.0) -> dict:
-    """Time the float64 oracle on one triangle block at ``n_sample`` and scale
-    to ``n_target`` by the ratio of algorithmic flops."""
+    """Time the float64 oracle on one Pairformer layer at ``n_sample`` and
+    scale to ``n_target`` by the ratio of algorithmic flops."""
     import numpy as np
 
     from foldjax_amd import synthetic as syn
-    from foldjax_amd.pairformer import flops_triangle
+    from foldjax_amd.pairformer import flops_block
     from oracle import triangle as O
 
     try:
@@ -60,38 +62,32 @@ def cpu_baseline(n_target: int, n_sample: int, budget_s: float = 25.0) -> dict:
         threads = len(os.sched_getaffinity(0))
     n = n_sample
     n_real = n - int(round(0.05 * n))
-    z = syn.bf16_round(syn.pair_input(n, 128, seed=0)).astype(np.float64)
-    m = syn.pair_mask(n, n_real).astype(np.float64)
-    ws = [syn.trimul_weights(seed=2), syn.trimul_weights(seed=3)]
-    wa = [syn.triattn_weights(seed=4), syn.triattn_weights(seed=5)]
-
-    def block(z):
-        z = z + O.protenix_triangle_multiplication(z, m, ws[0], "outgoing")
-        z = z + O.protenix_triangle_multiplication(z, m, ws[1], "incoming")
-        z = z + O.protenix_triangle_attention(z, m, wa[0], num_heads=4, starting=True)
-        z = z + O.protenix_triangle_attention(z, m, wa[1], num_heads=4, starting=False)
-        return z
+    r = lambda a: syn.bf16_round(a).astype(np.float64)  # noqa: E731
+    z = r(syn.pair_input(n, 128, seed=0, batch=1))
+    s = r(syn.single_input(n, 384, seed=1, batch=1))
+    tm = syn.token_mask(n, n_real)[None].astype(np.float64)
+    pm = syn.pair_mask(n, n_real)[None].astype(np.float64)
+    w = syn.pairformer_layer_weights(seed=2)
 
     times = []
     t_start = time.perf_counter()
     while True:
         t0 = time.perf_counter()
-        block(z)
+        O.boltz2_pairformer_layer(w, s, z, tm, pm)
         times.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > budget_s / 2 or len(times) >= 5:
             break
     t = float(np.median(times))
-    f = lambda nn: sum(2 * v for k, v in flops_triangle(nn).items() if k in ("trimul", "triattn"))  # noqa: E731
-    scale = f(n_target) / f(n)
+    scale = sum(flops_block(n_target).values()) / sum(flops_block(n).values())
     return {
         "value": t * scale * 1e3,
         "unit": "ms",
         "cores": threads,
         "kind": "port",
         "sample": (
-            f"float64 numpy oracle, one triangle block (tri-mul out+in, tri-attn start+end) at N={n} "
-            f"({n_real} real tokens), median of {len(times)} run(s) = {t * 1e3:.1f} ms, scaled to N={n_target} "
-            f"by the algorithmic-flop ratio {scale:.1f}"
+            f"float64 numpy oracle, one Pairformer layer (tri-mul out+in, tri-attn start+end, pair transition, "
+            f"single attention with pair bias, single transition) at N={n} ({n_real} real tokens), median of "
+            f"{len(times)} run(s) = {t * 1e3:.1f} ms, scaled to N={n_target} by the algorithmic-flop ratio {scale:.1f}"
         ),
     }
 
@@ -110,32 +106,34 @@ def main() -> int:
 
     from foldjax_amd import _lib
     from foldjax_amd import synthetic as syn
-    from foldjax_amd.pairformer import TriangleSublayers, flops_triangle
+    from foldjax_amd.pairformer import PairformerLayerWeights, flops_block, flops_triangle
 
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
     n = a.n
     n_real = n - int(round(a.pad_frac * n))
-    z0 = torch.from_numpy(syn.pair_input(n, 128, seed=0)).to(dev, dtype)
-    mask = torch.from_numpy(syn.pair_mask(n, n_real)).to(dev, dtype)
-    block = TriangleSublayers.random(dtype, dev, seed=2)
+    z0 = torch.from_numpy(syn.pair_input(n, 128, seed=0, batch=1)).to(dev, dtype)
+    s0 = torch.from_numpy(syn.single_input(n, 384, seed=1, batch=1)).to(dev, dtype)
+    tmask = torch.from_numpy(syn.token_mask(n, n_real)[None]).to(dev, dtype)
+    pmask = torch.from_numpy(syn.pair_mask(n, n_real)[None]).to(dev, dtype)
+    layer = PairformerLayerWeights.random(dtype, dev, seed=2)
 
     for _ in range(a.warmup):
-        block.forward(z0, mask)
+        layer.forward(s0, z0, tmask, pmask)
     torch.cuda.synchronize(dev)
 
     _lib.prof_reset()
     _lib.prof_enable(True)
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
-    z = z0
+    s, z = s0, z0
     for _ in range(a.steps):
-        z = block.forward(z0, mask)
+        s, z = layer.forward(s0, z0, tmask, pmask)
     torch.cuda.synchronize(dev)
     elapsed = time.perf_counter() - t0
     _lib.prof_enable(False)
     stats = _lib.prof_read()
-    if not torch.isfinite(z.float()).all():
+    if not (torch.isfinite(z.float()).all() and torch.isfinite(s.float()).all()):
         print("non-finite output", file=sys.stderr)
         return 1
 
@@ -159,8 +157,11 @@ def main() -> int:
     t_contract = kern["trimul_contract"]["avg_ms"] * 2
     t_flash = kern["triattn_flash"]["avg_ms"] * 2
     primary = (2 * fl["contraction"] + 2 * fl["attn_core"]) / ((t_contract + t_flash) * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
-    sub_t = sum(v["avg_ms"] * v["launches"] for v in kern.values()) / a.steps
+    tri_kernels = ("trimul_prologue", "trimul_contract", "trimul_epilogue", "triattn_prologue", "triattn_flash",
+                   "triattn_epilogue")
+    sub_t = sum(kern[k]["avg_ms"] * kern[k]["launches"] for k in tri_kernels if k in kern) / a.steps
     secondary = (2 * fl["trimul"] + 2 * fl["triattn"]) / (sub_t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
+    block_tflops = sum(flops_block(n).values()) / (ms_step * 1e-3) / 1e12
     dom_flops = per_launch.get(dominant)
     if dom_flops is not None:
         ach = dom_flops / (kern[dominant]["avg_ms"] * 1e-3) / 1e12
@@ -186,11 +187,14 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: z~N(0,1) (PCG64 seed 0), Glorot-uniform random-init weights, 5% padded tail mask",
+        "data": "synthetic: z, s ~ N(0,1) (PCG64 seeds 0, 1), Glorot-uniform random-init weights, 5% padded tail mask",
         "config": {
-            "workload": "pairformer block triangle sublayers (tri-mul out+in, tri-attn start+end, fused residuals)",
-            "n": n, "n_real": n_real, "c_z": 128, "c_hidden": 128, "heads": 4, "head_dim": 32,
+            "workload": "one Pairformer block (Boltz-2 layer): tri-mul out+in, tri-attn start+end, pair transition "
+                        "4x SwiGLU, single attention with pair bias, single transition; residuals fused",
+            "n": n, "n_real": n_real, "c_z": 128, "c_hidden": 128, "c_s": 384, "tri_heads": 4, "tri_head_dim": 32,
+            "single_heads": 16,
         },
+        "block_tflops": round(block_tflops, 1),
         "roofline": roof,
         "cpu_baseline": cpu,
         "mfma_frac": {"primary": round(primary, 4), "secondary": round(secondary, 4)},

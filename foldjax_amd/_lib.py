@@ -69,6 +69,29 @@ class TriAttnCoreArgs(ctypes.Structure):
     ]
 
 
+class TransitionArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _i64), ("c", _i64), ("dtype", _i32), ("eps", _f32),
+        ("x", _vp), ("norm_weight", _vp), ("norm_bias", _vp),
+        ("w_a", _vp), ("w_b", _vp), ("w_o", _vp),
+        ("row_mask", _vp), ("residual", _vp), ("out", _vp),
+    ]
+
+
+class SingleAttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("n", _i64), ("c_s", _i64), ("c_z", _i64), ("heads", _i64),
+        ("dtype", _i32), ("eps", _f32), ("inf", _f32),
+        ("s", _vp), ("z", _vp), ("mask", _vp),
+        ("pre_norm_weight", _vp), ("pre_norm_bias", _vp),
+        ("z_norm_weight", _vp), ("z_norm_bias", _vp), ("z_weight", _vp),
+        ("q_weight", _vp), ("q_bias", _vp), ("k_weight", _vp), ("v_weight", _vp),
+        ("g_weight", _vp), ("o_weight", _vp),
+        ("residual", _vp), ("out", _vp),
+        ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
 # every symbol the header declares, with its ctypes signature
 SYMBOLS = {
     "fjx_trimul_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
@@ -77,6 +100,9 @@ SYMBOLS = {
     "fjx_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), _vp]),
     "fjx_triattn_core_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "fjx_triattn_core": (ctypes.c_int, [ctypes.POINTER(TriAttnCoreArgs), _vp]),
+    "fjx_transition_fwd": (ctypes.c_int, [ctypes.POINTER(TransitionArgs), _vp]),
+    "fjx_single_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
+    "fjx_single_attention_fwd": (ctypes.c_int, [ctypes.POINTER(SingleAttentionArgs), _vp]),
     "fjx_last_error": (ctypes.c_char_p, []),
     "fjx_abi_version": (ctypes.c_int, []),
     "fjx_prof_enable": (ctypes.c_int, [ctypes.c_int]),

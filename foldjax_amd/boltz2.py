@@ -23,8 +23,13 @@ import os
 import torch
 
 from foldjax_amd import kernels
-from foldjax_amd.kernels import TriAttnWeights, TriMulWeights
-from foldjax_amd.params import pack_triattn_boltz2, pack_trimul_boltz2
+from foldjax_amd.kernels import SingleAttentionWeights, TransitionWeights, TriAttnWeights, TriMulWeights
+from foldjax_amd.params import (
+    pack_single_attention_boltz2,
+    pack_transition_boltz2,
+    pack_triattn_boltz2,
+    pack_trimul_boltz2,
+)
 
 DEFAULT_BACKEND = "hip"
 _REFERENCE_ONLY = "the {kind} backend {name!r} is a JAX backend of the reference; this package provides 'hip'"
@@ -107,3 +112,82 @@ def hip_triangle_multiplication_forward(params, x, mask, direction, eps: float =
     """Drop-in for ``cueq_triangle_multiplication_forward`` (``triangle_cueq.py:72-102``)."""
     w = params if isinstance(params, TriMulWeights) else pack_trimul_boltz2(params, x.dtype, x.device)
     return kernels.trimul(x, mask, w, direction, eps=eps)
+
+
+def transition_forward(
+    params,
+    x: torch.Tensor,
+    chunk_size: int | None = None,
+    eps: float = 1e-5,
+    row_chunk_size: int | None = None,
+    glu_backend: str = "xla",
+    *,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Boltz-2 ``transition_forward`` (``B2P/transition.py:39-122``): the fused
+    kernel never forms the widened hidden tensor, so both chunk sizes are
+    accepted and unused (a non-positive ``chunk_size`` still raises, as there)."""
+    if chunk_size is not None and chunk_size <= 0:
+        raise ValueError(f"chunk_size must be positive, got {chunk_size}")
+    if glu_backend not in ("xla", "tokamax"):
+        raise ValueError(f"Unsupported glu backend: {glu_backend!r}")
+    w = params if isinstance(params, TransitionWeights) else pack_transition_boltz2(params, x.dtype, x.device)
+    return kernels.transition(x, w, residual=residual, eps=eps)
+
+
+def attention_pair_bias_forward(
+    params,
+    s: torch.Tensor,
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    k_in: torch.Tensor | None = None,
+    multiplicity: int = 1,
+    inf: float = 1e6,
+    eps: float = 1e-5,
+    chunk_size: int | None = None,
+    attention_backend: str = "xla",
+    *,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Boltz-2 ``attention_pair_bias_forward`` (``B2P/attention.py:19-115``) in
+    the self-attention form the Pairformer layer uses (``k_in`` is ``s``).
+    ``s`` is the normalised single representation; returns the update."""
+    if k_in is not None and k_in is not s:
+        raise ValueError("the hip attention with pair bias supports k_in=None or k_in=s only")
+    if multiplicity != 1:
+        raise ValueError("the hip attention with pair bias supports multiplicity=1 only")
+    if attention_backend not in ("xla", "tokamax", "flash", "hip"):
+        raise ValueError(f"Unsupported attention backend: {attention_backend!r}")
+    w = params if isinstance(params, SingleAttentionWeights) else pack_single_attention_boltz2(params, s.dtype, s.device)
+    return kernels.single_attention(s, z, mask, w, inf=inf, eps=eps, residual=residual)
+
+
+def pairformer_layer_forward(
+    params,
+    s: torch.Tensor,
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    pair_mask: torch.Tensor,
+    eps: float = 1e-5,
+    chunk_size: int = 128,
+    triangle_attention_chunk: int | None = None,
+    triangle_attention_q_chunk: int | None = None,
+    transition_hidden_chunk: int | None = None,
+    matmul_precision: str = "highest",
+    attention_backend: str = "xla",
+    triangle_backend: str = DEFAULT_BACKEND,
+    glu_backend: str = "xla",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:100-206``):
+    every residual is fused into the producing kernel. ``params`` is the
+    Boltz-2 layer dict, or a ``foldjax_amd.pairformer.PairformerLayerWeights``."""
+    from foldjax_amd.pairformer import PairformerLayerWeights
+
+    w = params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_boltz2(params, z.dtype, z.device)
+    # selector validation as the reference's entry points do it
+    resolve_matmul_precision(matmul_precision)
+    if triangle_backend not in ("xla", "pallas", "tokamax", "cueq", "hip"):
+        raise ValueError(f"Unsupported triangle_backend: {triangle_backend!r}")
+    if triangle_backend != "hip":
+        raise RuntimeError(_REFERENCE_ONLY.format(kind="triangle attention", name=triangle_backend))
+    return w.forward(s, z, mask, pair_mask, eps=eps)

@@ -46,11 +46,17 @@ enum KernelId {
   K_TRIATTN_FLASH,
   K_TRIATTN_EPILOGUE,
   K_TRIATTN_CORE_PREP,
+  K_TRANSITION,
+  K_SINGLE_PROJ,
+  K_SINGLE_PAIR_BIAS,
+  K_SINGLE_FLASH,
+  K_SINGLE_OUT,
   K_COUNT
 };
 const char* kKernelNames[K_COUNT] = {"trimul_prologue", "trimul_contract", "trimul_epilogue",
                                      "triattn_prologue", "triattn_flash", "triattn_epilogue",
-                                     "triattn_core_prep"};
+                                     "triattn_core_prep", "transition",     "single_proj",
+                                     "single_pair_bias", "single_flash",   "single_out"};
 
 struct Prof {
   std::mutex mu;
@@ -235,13 +241,15 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] { launch_trimul_prologue<T>(pp, a->batch, st); });
   if (rc) return rc;
 
-  ContractParams<T, T> cp;
+  GemmParams<T, T> cp = {};
   cp.a = abuf;
   cp.b = bbuf;
-  cp.out = obuf;
-  cp.n = a->n;
+  cp.c = obuf;
+  cp.m = cp.n = cp.k = a->n;
+  cp.lda = cp.ldb = cp.ldc = a->n;
+  cp.sa = cp.sb = cp.sc = a->n * a->n;
   cp.batches = a->batch * 128;
-  rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] { launch_contract<T, T>(cp, st); });
+  rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] { launch_gemm<T, T>(cp, st); });
   if (rc) return rc;
 
   EpilogueParams<T> ep;
@@ -374,6 +382,134 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   return timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
 }
 
+// -------------------------------------------------------- transition body
+template <typename T>
+int transition_run(const fjx_transition_args* a, hipStream_t st) {
+  TransitionParams<T> p;
+  p.x = static_cast<const T*>(a->x);
+  p.ln_w = static_cast<const T*>(a->norm_weight);
+  p.ln_b = static_cast<const T*>(a->norm_bias);
+  p.w_a = static_cast<const T*>(a->w_a);
+  p.w_b = static_cast<const T*>(a->w_b);
+  p.w_o = static_cast<const T*>(a->w_o);
+  p.row_mask = static_cast<const T*>(a->row_mask);
+  p.residual = static_cast<const T*>(a->residual);
+  p.out = static_cast<T*>(a->out);
+  p.rows = a->rows;
+  p.eps = a->eps;
+  return timed(K_TRANSITION, st, "transition", [&] { launch_transition<T>(p, (int)a->c, st); });
+}
+
+// ------------------------------------------------ single-track attention
+struct SingleWs {
+  size_t s_ln, qkvg, q, k, vt, bias, mb, o, go, total;
+};
+SingleWs single_ws(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype) {
+  const int64_t np = round64(n);
+  const size_t es = esize(dtype);
+  SingleWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  w.s_ln = take((size_t)batch * n * c_s * es);
+  w.qkvg = take((size_t)batch * n * 4 * c_s * es);
+  w.q = take((size_t)batch * heads * np * 32 * es);
+  w.k = take((size_t)batch * heads * np * 32 * es);
+  w.vt = take((size_t)batch * heads * np * 32 * es);
+  w.bias = take((size_t)batch * heads * np * np * es);
+  w.mb = take((size_t)batch * np * sizeof(float));
+  w.o = take((size_t)batch * n * heads * 32 * es);
+  w.go = take((size_t)batch * n * c_s * es);
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+int single_run(const fjx_single_attention_args* a, hipStream_t st) {
+  const int64_t B = a->batch, n = a->n, cs = a->c_s, H = a->heads;
+  const int64_t np = round64(n);
+  const int dh = (int)(cs / H);
+  const SingleWs ws = single_ws(B, n, cs, H, a->dtype);
+  void* W = a->workspace;
+  T* s_ln = at<T>(W, ws.s_ln);
+  T* qkvg = at<T>(W, ws.qkvg);
+  const T* s_in = static_cast<const T*>(a->s);
+
+  int rc = timed(K_SINGLE_PROJ, st, "single_proj", [&] {
+    if (a->pre_norm_weight)
+      launch_layernorm_rows<T>(s_in, static_cast<const T*>(a->pre_norm_weight),
+                               static_cast<const T*>(a->pre_norm_bias), s_ln, B * n, (int)cs, a->eps, st);
+    const void* ws_[4] = {a->q_weight, a->k_weight, a->v_weight, a->g_weight};
+    for (int j = 0; j < 4; ++j) {
+      GemmParams<T, T> g = {};
+      g.a = a->pre_norm_weight ? s_ln : s_in;
+      g.b = static_cast<const T*>(ws_[j]);
+      g.c = qkvg + j * cs;
+      g.m = B * n;
+      g.n = cs;
+      g.k = cs;
+      g.lda = cs;
+      g.ldb = cs;
+      g.ldc = 4 * cs;
+      g.batches = 1;
+      g.bias = j == 0 ? static_cast<const T*>(a->q_bias) : nullptr;
+      g.act = j == 3 ? 1 : 0;
+      launch_gemm<T, T>(g, st);
+    }
+    launch_split_heads<T>(qkvg, 4 * cs, B, n, np, (int)H, dh, (1.0f / sqrtf((float)dh)) * kLog2e,
+                          at<T>(W, ws.q), at<T>(W, ws.k), at<T>(W, ws.vt), st);
+    launch_key_mask<T>(static_cast<const T*>(a->mask), at<float>(W, ws.mb), B, n, np, a->inf, st);
+  });
+  if (rc) return rc;
+  rc = timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
+    launch_pair_bias<T>(static_cast<const T*>(a->z), static_cast<const T*>(a->z_norm_weight),
+                        static_cast<const T*>(a->z_norm_bias), static_cast<const T*>(a->z_weight), at<T>(W, ws.bias),
+                        B, n, np, (int)H, a->eps, st);
+  });
+  if (rc) return rc;
+
+  FlashParams<T> fp;
+  fp.q = at<T>(W, ws.q);
+  fp.k = at<T>(W, ws.k);
+  fp.vt = at<T>(W, ws.vt);
+  fp.bias = at<T>(W, ws.bias);
+  fp.mb = at<float>(W, ws.mb);
+  fp.gate = nullptr;
+  fp.out = at<T>(W, ws.o);
+  fp.n = n;
+  fp.np = np;
+  fp.heads = H;
+  fp.rows = 1;
+  fp.o_stride_b = n * H * 32;
+  fp.o_stride_row = 0;
+  fp.o_stride_head = 32;
+  fp.o_stride_q = H * 32;
+  fp.bias_stride_b = H * np * np;
+  rc = timed(K_SINGLE_FLASH, st, "single_flash", [&] { launch_flash<T>(fp, B, st); });
+  if (rc) return rc;
+
+  return timed(K_SINGLE_OUT, st, "single_out", [&] {
+    T* go = at<T>(W, ws.go);
+    launch_gate_unpad<T>(fp.out, qkvg + 3 * cs, 4 * cs, go, B * n, (int)H, dh, st);
+    GemmParams<T, T> g = {};
+    g.a = go;
+    g.b = static_cast<const T*>(a->o_weight);
+    g.c = static_cast<T*>(a->out);
+    g.m = B * n;
+    g.n = cs;
+    g.k = cs;
+    g.lda = cs;
+    g.ldb = cs;
+    g.ldc = cs;
+    g.batches = 1;
+    g.residual = static_cast<const T*>(a->residual);
+    launch_gemm<T, T>(g, st);
+  });
+}
+
 bool dtype_ok(int32_t dt) { return dt == FJX_DTYPE_F32 || dt == FJX_DTYPE_BF16; }
 
 // grid dimensions are 32-bit; y/z additionally capped at 65535
@@ -466,6 +602,50 @@ int fjx_triattn_core(const fjx_triattn_core_args* a, hipStream_t st) {
     return fail(FJX_ERR_WORKSPACE, "fjx_triattn_core: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);
   return a->dtype == FJX_DTYPE_BF16 ? core_run<bf16>(a, st) : core_run<float>(a, st);
+}
+
+int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
+  g_err.clear();
+  if (!a) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: args is NULL");
+  if (a->rows < 1) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: rows must be >= 1");
+  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: unknown dtype %d", a->dtype);
+  if (a->c != 128 && a->c != 384)
+    return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: this build supports c in {128, 384}, got %lld",
+                (long long)a->c);
+  if ((a->rows + 63) / 64 > 0x7fffffffLL) return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: too many rows");
+  if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->w_a || !a->w_b || !a->w_o)
+    return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a required pointer is NULL");
+  return a->dtype == FJX_DTYPE_BF16 ? transition_run<bf16>(a, st) : transition_run<float>(a, st);
+}
+
+size_t fjx_single_attention_workspace_size(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype) {
+  if (batch < 1 || n < 1 || c_s < 1 || heads < 1 || !dtype_ok(dtype)) return 0;
+  return single_ws(batch, n, c_s, heads, dtype).total;
+}
+
+int fjx_single_attention_fwd(const fjx_single_attention_args* a, hipStream_t st) {
+  g_err.clear();
+  if (!a) return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: args is NULL");
+  if (a->batch < 1 || a->n < 1 || a->heads < 1)
+    return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: batch, n and heads must be >= 1");
+  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: unknown dtype %d", a->dtype);
+  if (a->c_z != 128 || a->c_s % a->heads != 0 || a->c_s / a->heads > 32 || a->c_s > 1024)
+    return fail(FJX_ERR_UNSUPPORTED,
+                "fjx_single_attention_fwd: this build supports c_z == 128, heads dividing c_s <= 1024 with "
+                "head_dim <= 32; got c_s=%lld c_z=%lld heads=%lld",
+                (long long)a->c_s, (long long)a->c_z, (long long)a->heads);
+  if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_single_attention_fwd: n or batch too large");
+  if ((a->pre_norm_weight == nullptr) != (a->pre_norm_bias == nullptr))
+    return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: pre_norm weight and bias must both be given or both NULL");
+  if (!a->s || !a->z || !a->out || !a->z_norm_weight ||
+      !a->z_norm_bias || !a->z_weight || !a->q_weight || !a->k_weight || !a->v_weight || !a->g_weight ||
+      !a->o_weight)
+    return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: a required pointer is NULL");
+  const size_t need = single_ws(a->batch, a->n, a->c_s, a->heads, a->dtype).total;
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(FJX_ERR_WORKSPACE, "fjx_single_attention_fwd: workspace of %zu bytes needed, %zu given", need,
+                a->workspace_bytes);
+  return a->dtype == FJX_DTYPE_BF16 ? single_run<bf16>(a, st) : single_run<float>(a, st);
 }
 
 int fjx_prof_enable(int on) {

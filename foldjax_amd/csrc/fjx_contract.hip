@@ -1,15 +1,18 @@
-// Triangle contraction: for every (batch, channel) an independent N x N x N
-// product with both operands k-contiguous,
-//     out[i][j] = sum_k a[i][k] * b[j][k]
-// The prologue lays a and b out channel-major with the contracted index
-// innermost (the incoming direction is prepared in the transposed grid), so
-// one "NT" kernel serves both directions.
+// Batched "NT" GEMM on MFMA: for every batch b
+//     C[i][j] = epilogue( sum_k A[i][k] * B[j][k] )
+// with both operands k-contiguous. It is the triangle contraction (one batch
+// per (batch, channel), M = N = K = N_tok, a and b laid out channel-major with
+// the contracted index innermost; the incoming direction is prepared in the
+// transposed grid, so one kernel serves both directions) and the plain
+// x W^T projections of the single track (B = a PyTorch [out, in] weight).
+//
+// Epilogue, in order: + bias[j], sigmoid, * gate[i][j], + residual[i][j].
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, 2 x 2 waves of
 // 64 x 64 (4 x 4 MFMA tiles of 16 x 16), k-tiles of BK staged through LDS with
 // a register prefetch of the next k-tile. Blocks are numbered so that all
-// tiles of one channel land on one XCD (workgroups are dealt round-robin over
-// the 8 XCDs), keeping that channel's a and b in the XCD's L2.
+// tiles of one batch land on one XCD (workgroups are dealt round-robin over
+// the 8 XCDs), keeping that batch's operands in the XCD's L2.
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
 
@@ -18,9 +21,9 @@ namespace fjx {
 constexpr int kBM = 128;
 constexpr int kNumXcd = 8;
 
-template <typename T> struct ContractCfg;
-template <> struct ContractCfg<bf16> { static constexpr int BK = 64; };
-template <> struct ContractCfg<float> { static constexpr int BK = 32; };
+template <typename T> struct GemmCfg;
+template <> struct GemmCfg<bf16> { static constexpr int BK = 64; };
+template <> struct GemmCfg<float> { static constexpr int BK = 32; };
 
 // Map hardware block id -> logical tile id so that consecutive logical ids run
 // on the same XCD. Bijective on [0, total).
@@ -31,27 +34,28 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t w, int64_t total) {
 }
 
 template <typename T, typename TO>
-__global__ __launch_bounds__(256) void contract_nt_kernel(ContractParams<T, TO> P) {
-  constexpr int BK = ContractCfg<T>::BK;
+__global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
+  constexpr int BK = GemmCfg<T>::BK;
   constexpr int LD = BK + 8;                  // padded LDS row (elements)
   constexpr int CHUNKS = kBM * BK / 8;        // 8-element chunks per operand tile
   constexpr int PER_T = CHUNKS / 256;         // chunks per thread per operand
   __shared__ __attribute__((aligned(16))) T As[2][kBM][LD];
   __shared__ __attribute__((aligned(16))) T Bs[2][kBM][LD];
 
-  const int64_t n = P.n;
-  const int64_t tiles = (n + kBM - 1) / kBM;
-  const int64_t total = P.batches * tiles * tiles;
+  const int64_t M = P.m, N = P.n, K = P.k;
+  const int64_t tm = (M + kBM - 1) / kBM;
+  const int64_t tn = (N + kBM - 1) / kBM;
+  const int64_t total = P.batches * tm * tn;
   const int64_t lid = xcd_remap(blockIdx.x, total);
-  const int64_t bc = lid / (tiles * tiles);
-  const int64_t tile = lid % (tiles * tiles);
-  const int64_t m0 = (tile / tiles) * kBM;
-  const int64_t n0 = (tile % tiles) * kBM;
+  const int64_t bat = lid / (tm * tn);
+  const int64_t tile = lid % (tm * tn);
+  const int64_t m0 = (tile / tn) * kBM;
+  const int64_t n0 = (tile % tn) * kBM;
 
-  const T* A = P.a + bc * n * n;
-  const T* B = P.b + bc * n * n;
+  const T* A = P.a + bat * P.sa;
+  const T* B = P.b + bat * P.sb;
   const int t = threadIdx.x;
-  const bool aligned = (n % 8) == 0;
+  const bool aligned = (K % 8) == 0 && (P.lda % 8) == 0 && (P.ldb % 8) == 0;
 
   typename Frag<T>::type ra[PER_T], rb[PER_T];
 
@@ -64,18 +68,18 @@ __global__ __launch_bounds__(256) void contract_nt_kernel(ContractParams<T, TO> 
       const int64_t gk = k0 + kc;
       const int64_t ga = m0 + row;
       const int64_t gb = n0 + row;
-      if (aligned && gk + 8 <= n) {
-        if (ga < n) ra[it] = load8(A + ga * n + gk);
+      if (aligned && gk + 8 <= K) {
+        if (ga < M) ra[it] = load8(A + ga * P.lda + gk);
         else ra[it] = typename Frag<T>::type{};
-        if (gb < n) rb[it] = load8(B + gb * n + gk);
+        if (gb < N) rb[it] = load8(B + gb * P.ldb + gk);
         else rb[it] = typename Frag<T>::type{};
       } else {
         float fa[8], fb[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const bool kin = gk + e < n;
-          fa[e] = (kin && ga < n) ? to_f32(A[ga * n + gk + e]) : 0.f;
-          fb[e] = (kin && gb < n) ? to_f32(B[gb * n + gk + e]) : 0.f;
+          const bool kin = gk + e < K;
+          fa[e] = (kin && ga < M) ? to_f32(A[ga * P.lda + gk + e]) : 0.f;
+          fb[e] = (kin && gb < N) ? to_f32(B[gb * P.ldb + gk + e]) : 0.f;
         }
         ra[it] = pack8<T>(fa);
         rb[it] = pack8<T>(fb);
@@ -106,7 +110,7 @@ __global__ __launch_bounds__(256) void contract_nt_kernel(ContractParams<T, TO> 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t ktiles = (n + BK - 1) / BK;
+  const int64_t ktiles = (K + BK - 1) / BK;
   load_tile(0);
   store_tile(0);
   __syncthreads();
@@ -130,28 +134,39 @@ __global__ __launch_bounds__(256) void contract_nt_kernel(ContractParams<T, TO> 
     __syncthreads();
   }
 
-  TO* O = P.out + bc * n * n;
+  TO* O = P.c + bat * P.sc;
+  const TO* G = P.gate ? P.gate + bat * P.sc : nullptr;
+  const TO* R = P.residual ? P.residual + bat * P.sc : nullptr;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t col = n0 + wn + 16 * j + li;
+      if (col >= N) continue;
+      const float bias = P.bias ? to_f32(P.bias[col]) : 0.f;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t row = m0 + wm + 16 * i + 4 * lg + q;
-        if (row < n && col < n) O[row * n + col] = from_f32<TO>(acc[i][j][q]);
+        if (row >= M) continue;
+        float v = acc[i][j][q] + bias;
+        if (P.act == 1) v = fast_sigmoid(v);
+        const int64_t off = row * P.ldc + col;
+        if (G) v *= to_f32(G[off]);
+        if (R) v += to_f32(R[off]);
+        O[off] = from_f32<TO>(v);
       }
     }
 }
 
 template <typename T, typename TO>
-void launch_contract(const ContractParams<T, TO>& p, hipStream_t st) {
-  const int64_t tiles = (p.n + kBM - 1) / kBM;
-  const int64_t total = p.batches * tiles * tiles;
-  hipLaunchKernelGGL((contract_nt_kernel<T, TO>), dim3((unsigned)total), dim3(256), 0, st, p);
+void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st) {
+  const int64_t tm = (p.m + kBM - 1) / kBM;
+  const int64_t tn = (p.n + kBM - 1) / kBM;
+  const int64_t total = p.batches * tm * tn;
+  hipLaunchKernelGGL((gemm_nt_kernel<T, TO>), dim3((unsigned)total), dim3(256), 0, st, p);
 }
 
-template void launch_contract<bf16, bf16>(const ContractParams<bf16, bf16>&, hipStream_t);
-template void launch_contract<float, float>(const ContractParams<float, float>&, hipStream_t);
+template void launch_gemm<bf16, bf16>(const GemmParams<bf16, bf16>&, hipStream_t);
+template void launch_gemm<float, float>(const GemmParams<float, float>&, hipStream_t);
 
 }  // namespace fjx

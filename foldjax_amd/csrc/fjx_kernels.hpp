@@ -64,12 +64,33 @@ struct EpilogueParams {
 };
 
 template <typename T, typename TO>
-struct ContractParams {
-  const T* a;   // [B*C][N][N]: row i, contracted index k contiguous
-  const T* b;   // [B*C][N][N]: row j, k contiguous
-  TO* out;      // [B*C][N][N]
-  int64_t n;
-  int64_t batches;  // B*C
+struct GemmParams {
+  const T* a;       // [batches][m][lda], k-contiguous rows
+  const T* b;       // [batches][n][ldb], k-contiguous rows (a PyTorch [out, in] weight)
+  TO* c;            // [batches][m][ldc]
+  int64_t m, n, k;
+  int64_t lda, ldb, ldc;
+  int64_t sa, sb, sc;  // batch strides in elements (0 = shared)
+  int64_t batches;
+  const T* bias;       // [n] or null
+  int act;             // 0 none, 1 sigmoid
+  const TO* gate;      // indexed like c, or null
+  const TO* residual;  // indexed like c, or null (may alias c)
+};
+
+template <typename T>
+struct TransitionParams {
+  const T* x;         // [rows][C]
+  const T* ln_w;
+  const T* ln_b;
+  const T* w_a;       // [4C][C] (silu branch)
+  const T* w_b;       // [4C][C]
+  const T* w_o;       // [C][4C]
+  const T* row_mask;  // [rows] or null
+  const T* residual;  // [rows][C] or null (may alias out)
+  T* out;             // [rows][C]
+  int64_t rows;
+  float eps;
 };
 
 template <typename T>
@@ -99,7 +120,24 @@ void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, h
 template <typename T>
 void launch_epilogue(const EpilogueParams<T>& p, bool channel_major, bool ln, int64_t batch, hipStream_t st);
 template <typename T, typename TO>
-void launch_contract(const ContractParams<T, TO>& p, hipStream_t st);
+void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st);
+template <typename T>
+void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st);
+
+// single-track helpers (fjx_single.hip)
+template <typename T>
+void launch_layernorm_rows(const T* x, const T* w, const T* b, T* y, int64_t rows, int c, float eps, hipStream_t st);
+template <typename T>
+void launch_split_heads(const T* qkv, int64_t ld, int64_t batch, int64_t n, int64_t np, int heads, int dh,
+                        float q_mul, T* q, T* k, T* vt, hipStream_t st);
+template <typename T>
+void launch_pair_bias(const T* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
+                      int64_t np, int heads, float eps, hipStream_t st);
+template <typename T>
+void launch_key_mask(const T* mask, float* mb, int64_t batch, int64_t n, int64_t np, float inf, hipStream_t st);
+template <typename T>
+void launch_gate_unpad(const T* o, const T* g, int64_t ldg, T* out, int64_t rows, int heads, int dh,
+                       hipStream_t st);
 template <typename T>
 void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st);
 

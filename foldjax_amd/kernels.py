@@ -86,6 +86,125 @@ class TriAttnWeights:
         return TriAttnWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
 
 
+@dataclass(frozen=True)
+class TransitionWeights:
+    """Transition weights, PyTorch ``[out, in]``: ``w_a``/``w_b`` ``[4c, c]`` (silu
+    and linear branches), ``w_o`` ``[c, 4c]``."""
+
+    norm_weight: torch.Tensor
+    norm_bias: torch.Tensor
+    w_a: torch.Tensor
+    w_b: torch.Tensor
+    w_o: torch.Tensor
+
+    def to(self, dtype: torch.dtype, device) -> "TransitionWeights":
+        return TransitionWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+
+
+@dataclass(frozen=True)
+class SingleAttentionWeights:
+    """Boltz-2 ``AttentionPairBias`` weights (PyTorch ``[out, in]``) plus the
+    layer's ``pre_norm_s`` (None when the caller passes a normalised s)."""
+
+    pre_norm_weight: torch.Tensor | None
+    pre_norm_bias: torch.Tensor | None
+    z_norm_weight: torch.Tensor  # [c_z]
+    z_norm_bias: torch.Tensor
+    z_weight: torch.Tensor  # [H, c_z]
+    q_weight: torch.Tensor  # [c_s, c_s]
+    q_bias: torch.Tensor | None  # [c_s]
+    k_weight: torch.Tensor
+    v_weight: torch.Tensor
+    g_weight: torch.Tensor
+    o_weight: torch.Tensor
+
+    @property
+    def heads(self) -> int:
+        return int(self.z_weight.shape[0])
+
+    def to(self, dtype: torch.dtype, device) -> "SingleAttentionWeights":
+        return SingleAttentionWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+
+
+def transition(
+    x: torch.Tensor,
+    w: TransitionWeights,
+    *,
+    row_mask: torch.Tensor | None = None,
+    residual: torch.Tensor | None = None,
+    eps: float = 1e-5,
+) -> torch.Tensor:
+    """``(silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T [* row_mask] [+ residual]``
+    over the last axis (``fjx_transition_fwd``)."""
+    _dev(x)
+    c = int(x.shape[-1])
+    rows = x.numel() // max(c, 1)
+    xf = x.contiguous()
+    lib = _lib.load()
+    out = torch.empty_like(xf)
+    rm = None
+    if row_mask is not None:
+        rm = torch.broadcast_to(row_mask, x.shape[:-1]).to(dtype=x.dtype).contiguous()
+    res = None if residual is None else residual.to(dtype=x.dtype).contiguous()
+    a = _lib.TransitionArgs(
+        rows=rows, c=c, dtype=_code(x.dtype), eps=float(eps),
+        x=_ptr(xf), norm_weight=_ptr(w.norm_weight), norm_bias=_ptr(w.norm_bias),
+        w_a=_ptr(w.w_a), w_b=_ptr(w.w_b), w_o=_ptr(w.w_o),
+        row_mask=_ptr(rm), residual=_ptr(res), out=_ptr(out),
+    )
+    _check_weights(x, w)
+    _lib.check(lib.fjx_transition_fwd(ctypes.byref(a), _stream(x)))
+    return out
+
+
+def single_attention(
+    s: torch.Tensor,
+    z: torch.Tensor,
+    mask: torch.Tensor | None,
+    w: SingleAttentionWeights,
+    *,
+    inf: float = 1e6,
+    eps: float = 1e-5,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Single-track attention with pair bias (``fjx_single_attention_fwd``).
+    ``s`` ``[B, N, c_s]`` (or ``[N, c_s]``), ``z`` ``[B, N, N, c_z]``, ``mask``
+    ``[B, N]`` token mask. Returns the update, or ``residual + update``."""
+    _dev(s)
+    squeeze = s.dim() == 2
+    sb = s.unsqueeze(0) if squeeze else s
+    zb = z.unsqueeze(0) if z.dim() == 3 else z
+    batch, n, c_s = (int(v) for v in sb.shape)
+    c_z = int(zb.shape[-1])
+    if tuple(zb.shape[:3]) != (batch, n, n):
+        raise ValueError(f"z must be [{batch}, {n}, {n}, c_z], got {tuple(z.shape)}")
+    sb = sb.contiguous()
+    zb = zb.to(dtype=s.dtype).contiguous()
+    mb = None
+    if mask is not None:
+        mb = torch.broadcast_to(mask, (batch, n)).to(dtype=s.dtype).contiguous()
+    res = None
+    if residual is not None:
+        res = (residual.unsqueeze(0) if squeeze else residual).to(dtype=s.dtype).contiguous()
+    lib = _lib.load()
+    code = _code(s.dtype)
+    out = torch.empty_like(sb)
+    ws_bytes = lib.fjx_single_attention_workspace_size(batch, n, c_s, w.heads, code)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=s.device)
+    a = _lib.SingleAttentionArgs(
+        batch=batch, n=n, c_s=c_s, c_z=c_z, heads=w.heads, dtype=code, eps=float(eps), inf=float(inf),
+        s=_ptr(sb), z=_ptr(zb), mask=_ptr(mb),
+        pre_norm_weight=_ptr(w.pre_norm_weight), pre_norm_bias=_ptr(w.pre_norm_bias),
+        z_norm_weight=_ptr(w.z_norm_weight), z_norm_bias=_ptr(w.z_norm_bias), z_weight=_ptr(w.z_weight),
+        q_weight=_ptr(w.q_weight), q_bias=_ptr(w.q_bias), k_weight=_ptr(w.k_weight), v_weight=_ptr(w.v_weight),
+        g_weight=_ptr(w.g_weight), o_weight=_ptr(w.o_weight),
+        residual=_ptr(res), out=_ptr(out), workspace=_ptr(ws), workspace_bytes=ws_bytes,
+    )
+    _check_weights(s, w)
+    _lib.check(lib.fjx_single_attention_fwd(ctypes.byref(a), _stream(s)))
+    return out[0] if squeeze else out
+
+
 def _flatten_pair(x: torch.Tensor, mask: torch.Tensor | None):
     if x.dim() < 3:
         raise ValueError(f"pair tensor must be [..., N, N, C], got shape {tuple(x.shape)}")

@@ -15,8 +15,8 @@ import os
 import torch
 
 from foldjax_amd import kernels
-from foldjax_amd.kernels import TriAttnWeights, TriMulWeights
-from foldjax_amd.params import pack_triattn_openfold3, pack_trimul_torch
+from foldjax_amd.kernels import TransitionWeights, TriAttnWeights, TriMulWeights
+from foldjax_amd.params import pack_transition_openfold3, pack_triattn_openfold3, pack_trimul_torch
 
 DEFAULT_BACKEND = "hip"
 
@@ -67,3 +67,17 @@ def triangle_attention(
     if w.heads != no_heads:
         raise ValueError(f"no_heads={no_heads} but the bias projection has {w.heads} heads")
     return kernels.triattn(x, mask, w, starting=starting, inf=inf, eps=eps, residual=residual)
+
+
+def swiglu_transition(
+    x: torch.Tensor,
+    params,
+    *,
+    mask: torch.Tensor | None = None,
+    eps: float = 1e-5,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """OpenFold3 ``swiglu_transition`` (``OF3/primitives.py:133-150``): the
+    output is multiplied by ``mask`` over the last axis when given."""
+    w = params if isinstance(params, TransitionWeights) else pack_transition_openfold3(params, x.dtype, x.device)
+    return kernels.transition(x, w, row_mask=mask, residual=residual, eps=eps)

@@ -22,7 +22,7 @@ from typing import Any, NamedTuple
 import numpy as np
 import torch
 
-from foldjax_amd.kernels import TriAttnWeights, TriMulWeights
+from foldjax_amd.kernels import SingleAttentionWeights, TransitionWeights, TriAttnWeights, TriMulWeights
 
 
 class LinearParams(NamedTuple):
@@ -270,4 +270,103 @@ def triattn_to_boltz2(w: dict) -> dict:
         "layer_norm": {"scale": w["layer_norm"]["weight"], "bias": w["layer_norm"]["bias"]},
         "linear": {"kernel": np.asarray(w["linear"]["weight"]).T},
         "mha": {n: {"kernel": np.asarray(att[n]["weight"]).T} for n in ("linear_q", "linear_k", "linear_v", "linear_o", "linear_g")},
+    }
+
+
+# -------------------------------------------------------------- transition
+
+
+def pack_transition_torch(params, dtype: torch.dtype, device) -> TransitionWeights:
+    """Protenix ``TransitionParams(layer_norm, linear_a, linear_b, linear_out)``
+    (``PXP/primitives.py:30-36``); ``linear_a`` is the silu branch."""
+    a = _weight(_get(params, "linear_a"), "linear_a")
+    lw, lb = _ln(_get(params, "layer_norm"), a.shape[1])
+    w = TransitionWeights(
+        norm_weight=lw, norm_bias=lb, w_a=a,
+        w_b=_weight(_get(params, "linear_b"), "linear_b"),
+        w_o=_weight(_get(params, "linear_out"), "linear_out"),
+    )
+    return w.to(dtype, device)
+
+
+def pack_transition_openfold3(params, dtype: torch.dtype, device) -> TransitionWeights:
+    """OpenFold3 ``SwiGLUTransitionParams(layer_norm, swiglu, linear_out)``
+    (``OF3/primitives.py:67-72``)."""
+    sw = _get(params, "swiglu")
+    a = _weight(_get(sw, "linear_a"), "swiglu.linear_a")
+    lw, lb = _ln(_get(params, "layer_norm"), a.shape[1])
+    w = TransitionWeights(
+        norm_weight=lw, norm_bias=lb, w_a=a,
+        w_b=_weight(_get(sw, "linear_b"), "swiglu.linear_b"),
+        w_o=_weight(_get(params, "linear_out"), "linear_out"),
+    )
+    return w.to(dtype, device)
+
+
+def pack_transition_boltz2(params, dtype: torch.dtype, device) -> TransitionWeights:
+    """Boltz-2 ``{norm, fc1, fc2, fc3}`` with ``[in, out]`` kernels
+    (``M/boltz2/bridge/torch_mapping.py:63-71``)."""
+    k = lambda name: _t(params[name]["kernel"]).T  # noqa: E731
+    w = TransitionWeights(
+        norm_weight=_t(params["norm"]["scale"]), norm_bias=_t(params["norm"]["bias"]),
+        w_a=k("fc1"), w_b=k("fc2"), w_o=k("fc3"),
+    )
+    return w.to(dtype, device)
+
+
+def pack_single_attention_boltz2(params, dtype: torch.dtype, device, pre_norm=None) -> SingleAttentionWeights:
+    """Boltz-2 ``AttentionPairBias`` dict (``M/boltz2/bridge/torch_mapping.py:
+    74-113``, kernels ``[in, out]``) plus an optional ``pre_norm_s`` dict."""
+    k = lambda name: _t(params[name]["kernel"]).T  # noqa: E731
+    qb = params["proj_q"].get("bias")
+    w = SingleAttentionWeights(
+        pre_norm_weight=None if pre_norm is None else _t(pre_norm["scale"]),
+        pre_norm_bias=None if pre_norm is None else _t(pre_norm["bias"]),
+        z_norm_weight=_t(params["proj_z_norm"]["scale"]),
+        z_norm_bias=_t(params["proj_z_norm"]["bias"]),
+        z_weight=k("proj_z"),
+        q_weight=k("proj_q"),
+        q_bias=None if qb is None else _t(qb),
+        k_weight=k("proj_k"), v_weight=k("proj_v"), g_weight=k("proj_g"), o_weight=k("proj_o"),
+    )
+    return w.to(dtype, device)
+
+
+def transition_to_boltz2(w: dict) -> dict:
+    """Field dict (``foldjax_amd.synthetic.transition_weights``) -> Boltz-2 dict."""
+    return {
+        "norm": {"scale": w["layer_norm"]["weight"], "bias": w["layer_norm"]["bias"]},
+        "fc1": {"kernel": np.asarray(w["linear_a"]["weight"]).T},
+        "fc2": {"kernel": np.asarray(w["linear_b"]["weight"]).T},
+        "fc3": {"kernel": np.asarray(w["linear_out"]["weight"]).T},
+    }
+
+
+def single_attention_to_boltz2(w: dict) -> tuple[dict, dict]:
+    """Torch-layout dict (``foldjax_amd.synthetic.single_attention_weights``) ->
+    (Boltz-2 ``attention`` dict, ``pre_norm_s`` dict)."""
+    k = lambda name: {"kernel": np.asarray(w[name]["weight"]).T}  # noqa: E731
+    att = {
+        "proj_q": {"kernel": np.asarray(w["proj_q"]["weight"]).T, "bias": w["proj_q"]["bias"]},
+        "proj_k": k("proj_k"), "proj_v": k("proj_v"), "proj_g": k("proj_g"), "proj_o": k("proj_o"),
+        "proj_z_norm": {"scale": w["proj_z_norm"]["weight"], "bias": w["proj_z_norm"]["bias"]},
+        "proj_z": k("proj_z"),
+    }
+    pre = {"scale": w["pre_norm_s"]["weight"], "bias": w["pre_norm_s"]["bias"]}
+    return att, pre
+
+
+def pairformer_layer_to_boltz2(w: dict) -> dict:
+    """Field dicts of one layer -> Boltz-2 ``PairformerLayerParams`` dict
+    (``M/boltz2/bridge/torch_mapping.py:603-650`` key names)."""
+    att, pre = single_attention_to_boltz2(w["attention"])
+    return {
+        "tri_mul_out": trimul_to_boltz2(w["tri_mul_out"]),
+        "tri_mul_in": trimul_to_boltz2(w["tri_mul_in"]),
+        "tri_att_start": triattn_to_boltz2(w["tri_att_start"]),
+        "tri_att_end": triattn_to_boltz2(w["tri_att_end"]),
+        "transition_z": transition_to_boltz2(w["transition_z"]),
+        "pre_norm_s": pre,
+        "attention": att,
+        "transition_s": transition_to_boltz2(w["transition_s"]),
     }

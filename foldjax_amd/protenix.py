@@ -22,8 +22,8 @@ import os
 import torch
 
 from foldjax_amd import kernels
-from foldjax_amd.kernels import TriAttnWeights, TriMulWeights
-from foldjax_amd.params import pack_triattn_protenix, pack_trimul_torch
+from foldjax_amd.kernels import TransitionWeights, TriAttnWeights, TriMulWeights
+from foldjax_amd.params import pack_transition_torch, pack_triattn_protenix, pack_trimul_torch
 
 DEFAULT_BACKEND = "hip"
 _REFERENCE_ONLY = "the {kind} backend {name!r} is a JAX backend of the reference; this package provides 'hip'"
@@ -84,3 +84,16 @@ def hip_attention_core(q, k, v, triangle_bias, mask_bias, *, scale: float) -> to
     """Drop-in for ``PXT/triangle_cueq.py``'s ``cueq_attention_core`` (via
     ``src/foldjax/models/_cueq.py:66``)."""
     return kernels.triattn_core(q, k, v, triangle_bias, mask_bias, scale=scale)
+
+
+def transition(
+    x: torch.Tensor,
+    params,
+    *,
+    chunk_size: int | None = None,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Protenix ``transition`` (``PXP/primitives.py:96-114``); ``chunk_size`` is
+    accepted and unused (the widened form never leaves the chip)."""
+    w = params if isinstance(params, TransitionWeights) else pack_transition_torch(params, x.dtype, x.device)
+    return kernels.transition(x, w, residual=residual)

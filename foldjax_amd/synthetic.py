@@ -71,6 +71,42 @@ def triattn_weights(c_z: int = 128, heads: int = 4, head_dim: int = 32, seed: in
     }
 
 
+def transition_weights(c: int = 128, expansion: int = 4, seed: int = 2) -> dict:
+    """Transition weights under the Protenix field names (``linear_a`` is the
+    silu branch), torch layout."""
+    rng = np.random.default_rng(seed)
+    h = expansion * c
+    return {
+        "layer_norm": _ln(rng, c),
+        "linear_a": {"weight": _glorot(rng, h, c)},
+        "linear_b": {"weight": _glorot(rng, h, c)},
+        "linear_out": {"weight": _glorot(rng, c, h)},
+    }
+
+
+def single_attention_weights(c_s: int = 384, c_z: int = 128, heads: int = 16, seed: int = 2) -> dict:
+    """Boltz-2 ``AttentionPairBias`` weights plus the layer's ``pre_norm_s``,
+    torch layout, Boltz-2 module names."""
+    rng = np.random.default_rng(seed)
+    return {
+        "pre_norm_s": _ln(rng, c_s),
+        "proj_q": {"weight": _glorot(rng, c_s, c_s), "bias": (0.1 * rng.standard_normal(c_s)).astype(np.float32)},
+        "proj_k": {"weight": _glorot(rng, c_s, c_s)},
+        "proj_v": {"weight": _glorot(rng, c_s, c_s)},
+        "proj_g": {"weight": _glorot(rng, c_s, c_s)},
+        "proj_o": {"weight": _glorot(rng, c_s, c_s)},
+        "proj_z_norm": _ln(rng, c_z),
+        "proj_z": {"weight": _glorot(rng, heads, c_z)},
+    }
+
+
+def single_input(n: int, c_s: int = 384, seed: int = 1, batch: int | None = None) -> np.ndarray:
+    """``s ~ N(0,1)`` of shape ``[N, c_s]`` (or ``[B, N, c_s]``), float32."""
+    rng = np.random.default_rng(seed)
+    shape = (n, c_s) if batch is None else (batch, n, c_s)
+    return rng.standard_normal(shape, dtype=np.float32)
+
+
 def pair_input(n: int, c_z: int = 128, seed: int = 0, batch: int | None = None) -> np.ndarray:
     """``z ~ N(0,1)`` of shape ``[N, N, c_z]`` (or ``[B, N, N, c_z]``), float32."""
     rng = np.random.default_rng(seed)
@@ -98,3 +134,18 @@ def cast_tree(tree, fn):
     if tree is None:
         return None
     return fn(tree)
+
+
+def pairformer_layer_weights(c_s: int = 384, c_z: int = 128, heads_pair: int = 4, heads_single: int = 16,
+                             seed: int = 2) -> dict:
+    """All weights of one Pairformer layer as torch-layout field dicts, each
+    sublayer from its own seed (``seed``, ``seed + 1``, ...)."""
+    return {
+        "tri_mul_out": trimul_weights(c_z, c_z, seed=seed),
+        "tri_mul_in": trimul_weights(c_z, c_z, seed=seed + 1),
+        "tri_att_start": triattn_weights(c_z, heads_pair, c_z // heads_pair, seed=seed + 2),
+        "tri_att_end": triattn_weights(c_z, heads_pair, c_z // heads_pair, seed=seed + 3),
+        "transition_z": transition_weights(c_z, seed=seed + 4),
+        "attention": single_attention_weights(c_s, c_z, heads_single, seed=seed + 5),
+        "transition_s": transition_weights(c_s, seed=seed + 6),
+    }

@@ -175,6 +175,77 @@ size_t fjx_triattn_core_workspace_size(int64_t batch, int64_t rows, int64_t head
                                        int64_t head_dim, int32_t dtype);
 int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
 
+/*
+ * Transition (pair or single track): for every row of c channels
+ *   out = (silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T  [* row_mask]  [+ residual]
+ * with a 4c hidden width that never leaves the chip. Replaces
+ * src/foldjax/models/boltz2/models/primitives/transition.py:39-122
+ * (fc1 = w_a, fc2 = w_b, fc3 = w_o), protenix/models/primitives/primitives.py:117-146
+ * and openfold3/models/primitives.py:133-150 (row_mask = the OpenFold3 mask).
+ * Weights PyTorch [out, in]: w_a, w_b [4c, c]; w_o [c, 4c]. Supported: c in {128, 384}.
+ */
+typedef struct fjx_transition_args {
+  int64_t rows;
+  int64_t c;
+  int32_t dtype;
+  float eps;
+  const void* x;         /* [rows, c] */
+  const void* norm_weight;
+  const void* norm_bias;
+  const void* w_a;
+  const void* w_b;
+  const void* w_o;
+  const void* row_mask;  /* [rows] or NULL */
+  const void* residual;  /* [rows, c] or NULL; may equal out */
+  void* out;             /* [rows, c] */
+} fjx_transition_args;
+
+int fjx_transition_fwd(const fjx_transition_args* args, hipStream_t stream);
+
+/*
+ * Single-track attention with pair bias of a Pairformer layer, Boltz-2 form
+ * (src/foldjax/models/boltz2/models/primitives/attention.py:19-115 called from
+ * trunk_blocks/pairformer.py:182-201):
+ *   s_ln = LN_pre(s)            (s itself when pre_norm_weight is NULL)
+ *   q = s_ln w_q^T + b_q, k = s_ln w_k^T, v = s_ln w_v^T, g = sigmoid(s_ln w_g^T)
+ *   bias[b,h,i,j] = LN_z(z[b,i,j]) w_z[h]^T
+ *   o = softmax(q k^T / sqrt(d) + bias + (1 - mask[b,j]) * (-inf)) v
+ *   out = (g * o) w_o^T  (+ residual)
+ * Weights PyTorch [out, in]. Supported: c_z == 128, heads * head_dim == c_s,
+ * head_dim <= 32.
+ */
+typedef struct fjx_single_attention_args {
+  int64_t batch;
+  int64_t n;
+  int64_t c_s;
+  int64_t c_z;
+  int64_t heads;
+  int32_t dtype;
+  float eps;
+  float inf;            /* 1e6 in Boltz-2 */
+  const void* s;        /* [batch, n, c_s] */
+  const void* z;        /* [batch, n, n, c_z] */
+  const void* mask;     /* [batch, n] token mask, or NULL */
+  const void* pre_norm_weight;  /* [c_s], or NULL: s is already normalised */
+  const void* pre_norm_bias;
+  const void* z_norm_weight;    /* [c_z] */
+  const void* z_norm_bias;
+  const void* z_weight;         /* [heads, c_z] */
+  const void* q_weight;         /* [c_s, c_s] */
+  const void* q_bias;           /* [c_s] or NULL */
+  const void* k_weight;
+  const void* v_weight;
+  const void* g_weight;
+  const void* o_weight;
+  const void* residual; /* [batch, n, c_s] or NULL; may equal out */
+  void* out;            /* [batch, n, c_s]; may equal s when residual == s */
+  void* workspace;
+  size_t workspace_bytes;
+} fjx_single_attention_args;
+
+size_t fjx_single_attention_workspace_size(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype);
+int fjx_single_attention_fwd(const fjx_single_attention_args* args, hipStream_t stream);
+
 /* Message for the last error on the calling thread ("" if none). */
 const char* fjx_last_error(void);
 

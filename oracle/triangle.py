@@ -395,3 +395,79 @@ def triattn_torch_to_boltz2(p, *, bias_name="linear", mha_name="attention"):
         "linear": {"kernel": k(_get(p, bias_name))},
         "mha": {n: {"kernel": k(_get(mha, n))} for n in ("linear_q", "linear_k", "linear_v", "linear_o", "linear_g")},
     }
+
+
+# ---------------------------------------------------------------------------
+# The rest of a Pairformer block: transition and single-track attention
+# ---------------------------------------------------------------------------
+
+
+def transition(x, p, *, mask=None, eps=1e-5):
+    """SwiGLU transition: ``(silu(LN(x) Wa^T) * (LN(x) Wb^T)) Wo^T [* mask]``.
+
+    Protenix ``_transition_block`` (``PXP/primitives.py:88-93``), Boltz-2
+    ``transition_forward`` (``B2P/transition.py:112-116``: fc1 = a, fc2 = b,
+    fc3 = out), OpenFold3 ``swiglu_transition`` (``OF3/primitives.py:133-150``,
+    optional mask over the last axis).
+    """
+    y = layer_norm(x, *_ln_params(_get(p, "layer_norm")), eps=eps)
+    h = silu(linear_torch(y, _get(p, "linear_a"))) * linear_torch(y, _get(p, "linear_b"))
+    out = linear_torch(h, _get(p, "linear_out"))
+    if mask is not None:
+        out = out * _f(mask)[..., None]
+    return out
+
+
+def boltz2_attention_pair_bias(p, s, z, mask, *, inf=1e6, eps=1e-5):
+    """Boltz-2 ``attention_pair_bias_forward`` XLA path with ``k_in = s``.
+
+    ``B2P/attention.py:44-115``: q/g from ``s`` (q with bias), k/v from ``s``;
+    ``bias = LN_z(z) W_z^T`` as ``[B, H, N, N]``; scores
+    ``q k^T / sqrt(d) + bias + (1 - mask[b, key]) * (-inf)``; softmax; gate
+    ``sigmoid(g)``; ``@ W_o``. ``s`` is the already normalised single
+    representation; weights are torch-layout under the Boltz-2 module names.
+    """
+    s = _f(s)
+    z = _f(z)
+    mask = _f(mask)
+    b, n, c_s = s.shape
+    heads = _f(p["proj_z"]["weight"]).shape[0]
+    d = c_s // heads
+    q = linear_torch(s, p["proj_q"]).reshape(b, n, heads, d)
+    g = sigmoid(linear_torch(s, {"weight": p["proj_g"]["weight"]}))
+    k = linear_torch(s, {"weight": p["proj_k"]["weight"]}).reshape(b, n, heads, d)
+    v = linear_torch(s, {"weight": p["proj_v"]["weight"]}).reshape(b, n, heads, d)
+    bias = linear_torch(layer_norm(z, p["proj_z_norm"]["weight"], p["proj_z_norm"]["bias"], eps), {"weight": p["proj_z"]["weight"]})
+    bias = np.transpose(bias, (0, 3, 1, 2))  # [B, H, N, N]
+    mask_bias = (1.0 - mask[:, None, None, :]) * -inf
+    qh = np.ascontiguousarray(np.transpose(q, (0, 2, 1, 3)))
+    kh = np.ascontiguousarray(np.transpose(k, (0, 2, 3, 1)))
+    vh = np.ascontiguousarray(np.transpose(v, (0, 2, 1, 3)))
+    attn = qh @ kh / np.sqrt(d) + bias + mask_bias
+    o = softmax(attn, axis=-1) @ vh  # [B, H, N, d]
+    o = np.transpose(o, (0, 2, 1, 3)).reshape(b, n, c_s)
+    return linear_torch(g * o, {"weight": p["proj_o"]["weight"]})
+
+
+def boltz2_pairformer_layer(p, s, z, mask, pair_mask, *, eps=1e-5):
+    """One Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:100-206``):
+    z += tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z;
+    s += attention_pair_bias(LN(s), z, mask); s += transition_s.
+
+    ``p`` holds torch-layout field dicts: ``tri_mul_out``/``tri_mul_in``
+    (``linear_a_p`` ...), ``tri_att_start``/``tri_att_end`` (``layer_norm``,
+    ``linear``, ``attention``), ``transition_z``/``transition_s``
+    (``layer_norm``, ``linear_a``, ``linear_b``, ``linear_out``), ``attention``
+    (``pre_norm_s``, ``proj_*``). Returns ``(s, z)``.
+    """
+    heads = _f(p["tri_att_start"]["linear"]["weight"]).shape[0]
+    z = _f(z) + protenix_triangle_multiplication(z, pair_mask, p["tri_mul_out"], "outgoing")
+    z = z + protenix_triangle_multiplication(z, pair_mask, p["tri_mul_in"], "incoming")
+    z = z + protenix_triangle_attention(z, pair_mask, p["tri_att_start"], num_heads=heads, starting=True)
+    z = z + protenix_triangle_attention(z, pair_mask, p["tri_att_end"], num_heads=heads, starting=False)
+    z = z + transition(z, p["transition_z"], eps=eps)
+    a = p["attention"]
+    s_ln = layer_norm(s, a["pre_norm_s"]["weight"], a["pre_norm_s"]["bias"], eps)
+    s = _f(s) + boltz2_attention_pair_bias(a, s_ln, z, mask, eps=eps)
+    s = s + transition(s, p["transition_s"], eps=eps)
+    return s, z

@@ -106,3 +106,12 @@ def tolist(tree):
     if isinstance(tree, dict):
         return {k: tolist(v) for k, v in tree.items()}
     return tree.tolist()
+
+
+def transition_row(x, p, eps=1e-5):
+    """One row of the SwiGLU transition, written out."""
+    y = ln_vec(x, p["layer_norm"]["weight"], p["layer_norm"]["bias"], eps)
+    a = matvec_torch(p["linear_a"]["weight"], y)
+    b = matvec_torch(p["linear_b"]["weight"], y)
+    h = [a[i] * sig(a[i]) * b[i] for i in range(len(a))]
+    return matvec_torch(p["linear_out"]["weight"], h)

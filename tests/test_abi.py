@@ -55,6 +55,8 @@ def test_struct_layout_matches_c(tmp_path):
         "fjx_trimul_args": _lib.TriMulArgs,
         "fjx_triattn_args": _lib.TriAttnArgs,
         "fjx_triattn_core_args": _lib.TriAttnCoreArgs,
+        "fjx_transition_args": _lib.TransitionArgs,
+        "fjx_single_attention_args": _lib.SingleAttentionArgs,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "fjx_tri.h"', "int main(void) {"]
     for cname, cls in structs.items():
@@ -108,6 +110,10 @@ def test_invalid_arguments_return_codes_without_launching(lib):
     c = _lib.TriAttnCoreArgs(batch=1, rows=1, heads=1, n=4, head_dim=64, dtype=0)
     assert lib.fjx_triattn_core(ctypes.byref(c), None) == _lib.FJX_ERR_UNSUPPORTED
     assert lib.fjx_trimul_fwd(None, None) == _lib.FJX_ERR_INVALID
+    tr = _lib.TransitionArgs(rows=4, c=256, dtype=1)
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_UNSUPPORTED
+    sa = _lib.SingleAttentionArgs(batch=1, n=4, c_s=384, c_z=128, heads=8, dtype=1)  # head_dim 48 > 32
+    assert lib.fjx_single_attention_fwd(ctypes.byref(sa), None) == _lib.FJX_ERR_UNSUPPORTED
 
 
 def test_check_maps_codes_to_exceptions(lib):

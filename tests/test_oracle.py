@@ -251,3 +251,61 @@ def test_planted_wrong_bias_index_is_caught(monkeypatch):
     monkeypatch.setattr(O, "attention_rows", lambda q, k, v, mb, tb, row_block=16: real(q, k, v, mb, np.swapaxes(tb, -1, -2)))
     got = O.protenix_triangle_attention(z, mask, ta, num_heads=2)
     assert np.max(np.abs(got - want)) > 1e-3
+
+
+# ------------------------------------------- transition, single attention
+
+
+def test_transition_matches_brute_force():
+    rng = np.random.default_rng(20)
+    x = rng.standard_normal((3, 5))
+    p = syn.transition_weights(5, seed=20)
+    want = np.array([B.transition_row(row, B.tolist(p)) for row in x.tolist()])
+    np.testing.assert_allclose(O.transition(x, p), want, rtol=1e-11, atol=1e-11)
+    m = np.array([1.0, 0.0, 1.0])
+    np.testing.assert_allclose(O.transition(x, p, mask=m), want * m[:, None], rtol=1e-11, atol=1e-11)
+
+
+def test_attention_pair_bias_matches_torch_sdpa():
+    """The Boltz-2 attention with pair bias equals gated torch SDPA with the
+    pair bias and key mask as an additive mask (``B2P/attention.py:82-115``)."""
+    rng = np.random.default_rng(21)
+    b, n, c_s, c_z, h = 2, 7, 24, 8, 4
+    s = rng.standard_normal((b, n, c_s))
+    z = rng.standard_normal((b, n, n, c_z))
+    mask = (rng.random((b, n)) > 0.3).astype(np.float64)
+    mask[:, 0] = 1.0
+    p = syn.single_attention_weights(c_s, c_z, h, seed=21)
+    got = O.boltz2_attention_pair_bias(p, s, z, mask)
+    T = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float64))  # noqa: E731
+    lin = lambda x, name: x @ T(p[name]["weight"]).T  # noqa: E731
+    st = T(s)
+    q = (lin(st, "proj_q") + T(p["proj_q"]["bias"])).reshape(b, n, h, -1).transpose(1, 2)
+    k = lin(st, "proj_k").reshape(b, n, h, -1).transpose(1, 2)
+    v = lin(st, "proj_v").reshape(b, n, h, -1).transpose(1, 2)
+    zl = torch.nn.functional.layer_norm(T(z), (c_z,), T(p["proj_z_norm"]["weight"]), T(p["proj_z_norm"]["bias"]), 1e-5)
+    bias = (zl @ T(p["proj_z"]["weight"]).T).permute(0, 3, 1, 2)
+    am = bias + ((1.0 - T(mask)) * -1e6)[:, None, None, :]
+    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=am).transpose(1, 2).reshape(b, n, c_s)
+    want = (torch.sigmoid(lin(st, "proj_g")) * o) @ T(p["proj_o"]["weight"]).T
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_pairformer_layer_padding_isolation():
+    """Padded tokens with adversarial values leave the valid region of both
+    tracks unchanged (cf. ``T/models/protenix/test_pairformer.py:91-132``)."""
+    rng = np.random.default_rng(22)
+    n, pad, c_s, c_z = 4, 2, 16, 8
+    w = syn.pairformer_layer_weights(c_s=c_s, c_z=c_z, heads_pair=2, heads_single=4, seed=22)
+    s = rng.standard_normal((1, n, c_s))
+    z = rng.standard_normal((1, n, n, c_z))
+    want_s, want_z = O.boltz2_pairformer_layer(w, s, z, np.ones((1, n)), np.ones((1, n, n)))
+    sp = np.pad(s, ((0, 0), (0, pad), (0, 0)))
+    sp[:, n:] = 1e6
+    zp = np.pad(z, ((0, 0), (0, pad), (0, pad), (0, 0)))
+    zp[:, n:, :] = -1e6
+    zp[:, :, n:] = 1e6
+    tm = syn.token_mask(n + pad, n)[None]
+    got_s, got_z = O.boltz2_pairformer_layer(w, sp, zp, tm, syn.pair_mask(n + pad, n)[None])
+    np.testing.assert_allclose(got_s[:, :n], want_s, rtol=1e-8, atol=1e-8)
+    np.testing.assert_allclose(got_z[:, :n, :n], want_z, rtol=1e-8, atol=1e-8)
