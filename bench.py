@@ -42,6 +42,8 @@ def _args():
     p.add_argument("--pad-frac", type=float, default=0.05)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     p.add_argument("--cpu-n", type=int, default=256, help="size of the CPU oracle sample")
+    p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "copy"],
+                   help="profiling aid: run only one sublayer kind per step instead of the whole block")
     return p.parse_args()
 
 
@@ -118,8 +120,21 @@ def main() -> int:
     pmask = torch.from_numpy(syn.pair_mask(n, n_real)[None]).to(dev, dtype)
     layer = PairformerLayerWeights.random(dtype, dev, seed=2)
 
+    from foldjax_amd import kernels
+
+    tri = layer.triangle
+    steps_fn = {
+        "block": lambda: layer.forward(s0, z0, tmask, pmask),
+        "trimul": lambda: (s0, kernels.trimul(z0, pmask, tri.tri_mul_out, "outgoing", residual=z0)),
+        "triattn": lambda: (s0, kernels.triattn(z0, pmask, tri.tri_att_start, starting=True, residual=z0)),
+        "transition": lambda: (s0, kernels.transition(z0, layer.transition_z, residual=z0)),
+        # a plain device copy of the pair tensor (N*N*128*2 bytes each way): the
+        # calibration point for the FETCH_SIZE / WRITE_SIZE counters
+        "copy": lambda: (s0, z0.clone()),
+    }
+    step = steps_fn[a.op]
     for _ in range(a.warmup):
-        layer.forward(s0, z0, tmask, pmask)
+        step()
     torch.cuda.synchronize(dev)
 
     _lib.prof_reset()
@@ -128,7 +143,7 @@ def main() -> int:
     t0 = time.perf_counter()
     s, z = s0, z0
     for _ in range(a.steps):
-        s, z = layer.forward(s0, z0, tmask, pmask)
+        s, z = step()
     torch.cuda.synchronize(dev)
     elapsed = time.perf_counter() - t0
     _lib.prof_enable(False)
@@ -138,6 +153,10 @@ def main() -> int:
         return 1
 
     ms_step = elapsed * 1e3 / a.steps
+    if a.op != "block":
+        per = {k: {"avg_ms": round(v[0] / v[1], 4), "launches": v[1]} for k, v in stats.items() if v[1]}
+        print(json.dumps({"op": a.op, "n": n, "ms_per_step": round(ms_step, 4), "kernels": per}))
+        return 0
     fl = flops_triangle(n)
     per_launch = {
         "trimul_contract": fl["contraction"],
