@@ -44,6 +44,7 @@ def _hipcc() -> str:
 # purpose, so max() needs no NaN canonicalisation
 FILE_FLAGS = {
     "fjx_flash.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "fjx_rowproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

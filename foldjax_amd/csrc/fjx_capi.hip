@@ -169,7 +169,7 @@ dim3 grid_for(int64_t total) {
 
 // --------------------------------------------------------------- layouts
 struct TriMulWs {
-  size_t a, b, o, g, total;
+  size_t a, b, o, total;
 };
 TriMulWs trimul_ws(int64_t batch, int64_t n, int32_t dtype) {
   const size_t per = align_up((size_t)batch * n * n * 128 * esize(dtype));
@@ -177,16 +177,14 @@ TriMulWs trimul_ws(int64_t batch, int64_t n, int32_t dtype) {
   w.a = 0;
   w.b = per;
   w.o = 2 * per;
-  w.g = 3 * per;
-  w.total = 4 * per;
+  w.total = 3 * per;
   return w;
 }
 
 struct TriAttnWs {
-  size_t q, k, vt, g, bias, mb, o, total;
+  size_t q, k, vt, bias, mb, o, total;
 };
-TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int32_t dtype, bool with_g,
-                     bool with_o) {
+TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int32_t dtype, bool with_o) {
   const int64_t np = round64(n);
   const size_t es = esize(dtype);
   const size_t qk = align_up((size_t)batch * rows * heads * np * 32 * es);
@@ -198,8 +196,6 @@ TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int3
   off += qk;
   w.vt = off;
   off += qk;
-  w.g = off;
-  if (with_g) off += align_up((size_t)batch * rows * n * heads * 32 * es);
   w.bias = off;
   off += align_up((size_t)batch * heads * np * np * es);
   w.mb = off;
@@ -222,7 +218,6 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   T* abuf = at<T>(a->workspace, ws.a);
   T* bbuf = at<T>(a->workspace, ws.b);
   T* obuf = at<T>(a->workspace, ws.o);
-  T* gbuf = at<T>(a->workspace, ws.g);
 
   TriMulPrologueParams<T> pp;
   pp.x = static_cast<const T*>(a->x);
@@ -231,10 +226,8 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   pp.ln_b = static_cast<const T*>(a->norm_in_bias);
   pp.w_p = static_cast<const T*>(a->p_in_weight);
   pp.w_g = static_cast<const T*>(a->g_in_weight);
-  pp.w_gout = static_cast<const T*>(a->g_out_weight);
   pp.a_cm = abuf;
   pp.b_cm = bbuf;
-  pp.g = gbuf;
   pp.n = a->n;
   pp.eps = a->eps;
   pp.transpose = a->direction == FJX_INCOMING;
@@ -252,19 +245,20 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] { launch_gemm<T, T>(cp, st); });
   if (rc) return rc;
 
-  EpilogueParams<T> ep;
-  ep.x = obuf;
-  ep.ln_w = static_cast<const T*>(a->norm_out_weight);
-  ep.ln_b = static_cast<const T*>(a->norm_out_bias);
-  ep.w = static_cast<const T*>(a->p_out_weight);
-  ep.gate = gbuf;
+  TriMulEpilogueParams<T> ep;
+  ep.o = obuf;
+  ep.x = static_cast<const T*>(a->x);
+  ep.ln_in_w = pp.ln_w;
+  ep.ln_in_b = pp.ln_b;
+  ep.ln_out_w = static_cast<const T*>(a->norm_out_weight);
+  ep.ln_out_b = static_cast<const T*>(a->norm_out_bias);
+  ep.w_pout = static_cast<const T*>(a->p_out_weight);
+  ep.w_gout = static_cast<const T*>(a->g_out_weight);
   ep.residual = static_cast<const T*>(a->residual);
   ep.out = static_cast<T*>(a->out);
   ep.n = a->n;
   ep.eps = a->eps;
-  ep.transpose = 0;
-  return timed(K_TRIMUL_EPILOGUE, st, "trimul_epilogue",
-               [&] { launch_epilogue<T>(ep, /*channel_major=*/true, /*ln=*/true, a->batch, st); });
+  return timed(K_TRIMUL_EPILOGUE, st, "trimul_epilogue", [&] { launch_trimul_epilogue<T>(ep, a->batch, st); });
 }
 
 // ---------------------------------------------------------- tri-attn body
@@ -272,8 +266,7 @@ template <typename T>
 int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   const int64_t n = a->n;
   const int64_t np = round64(n);
-  const bool gated = a->g_weight != nullptr;
-  const TriAttnWs ws = triattn_ws(a->batch, n, n, a->heads, a->dtype, gated, true);
+  const TriAttnWs ws = triattn_ws(a->batch, n, n, a->heads, a->dtype, true);
   void* W = a->workspace;
 
   TriAttnPrologueParams<T> pp;
@@ -285,11 +278,9 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   pp.w_q = static_cast<const T*>(a->q_weight);
   pp.w_k = static_cast<const T*>(a->k_weight);
   pp.w_v = static_cast<const T*>(a->v_weight);
-  pp.w_g = static_cast<const T*>(a->g_weight);
   pp.q = at<T>(W, ws.q);
   pp.k = at<T>(W, ws.k);
   pp.vt = at<T>(W, ws.vt);
-  pp.g = gated ? at<T>(W, ws.g) : nullptr;
   pp.bias = at<T>(W, ws.bias);
   pp.mb = at<float>(W, ws.mb);
   pp.n = n;
@@ -307,7 +298,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   fp.vt = pp.vt;
   fp.bias = pp.bias;
   fp.mb = pp.mb;
-  fp.gate = pp.g;
+  fp.gate = nullptr;
   fp.out = at<T>(W, ws.o);
   fp.n = n;
   fp.np = np;
@@ -321,19 +312,19 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
   if (rc) return rc;
 
-  EpilogueParams<T> ep;
-  ep.x = fp.out;
-  ep.ln_w = nullptr;
-  ep.ln_b = nullptr;
-  ep.w = static_cast<const T*>(a->o_weight);
-  ep.gate = nullptr;
+  TriAttnEpilogueParams<T> ep;
+  ep.o = fp.out;
+  ep.x = pp.x;
+  ep.ln_w = pp.ln_w;
+  ep.ln_b = pp.ln_b;
+  ep.w_g = static_cast<const T*>(a->g_weight);
+  ep.w_o = static_cast<const T*>(a->o_weight);
   ep.residual = static_cast<const T*>(a->residual);
   ep.out = static_cast<T*>(a->out);
   ep.n = n;
   ep.eps = a->eps;
-  ep.transpose = a->starting ? 0 : 1;
-  return timed(K_TRIATTN_EPILOGUE, st, "triattn_epilogue",
-               [&] { launch_epilogue<T>(ep, /*channel_major=*/false, /*ln=*/false, a->batch, st); });
+  ep.transpose = pp.transpose;
+  return timed(K_TRIATTN_EPILOGUE, st, "triattn_epilogue", [&] { launch_triattn_epilogue<T>(ep, a->batch, st); });
 }
 
 template <typename T>
@@ -341,7 +332,7 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   const int64_t n = a->n;
   const int64_t np = round64(n);
   const int64_t hr = a->batch * a->rows * a->heads;
-  const TriAttnWs ws = triattn_ws(a->batch, a->rows, n, a->heads, a->dtype, false, false);
+  const TriAttnWs ws = triattn_ws(a->batch, a->rows, n, a->heads, a->dtype, false);
   void* W = a->workspace;
   T* q = at<T>(W, ws.q);
   T* k = at<T>(W, ws.k);
@@ -555,7 +546,7 @@ size_t fjx_triattn_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t
   (void)c_z;
   (void)head_dim;
   if (batch < 1 || n < 1 || heads < 1 || !dtype_ok(dtype)) return 0;
-  return triattn_ws(batch, n, n, heads, dtype, true, true).total;
+  return triattn_ws(batch, n, n, heads, dtype, true).total;
 }
 
 int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
@@ -572,7 +563,7 @@ int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
   if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->bias_weight || !a->q_weight ||
       !a->k_weight || !a->v_weight || !a->o_weight)
     return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: a required pointer is NULL");
-  const size_t need = triattn_ws(a->batch, a->n, a->n, a->heads, a->dtype, a->g_weight != nullptr, true).total;
+  const size_t need = triattn_ws(a->batch, a->n, a->n, a->heads, a->dtype, true).total;
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_triattn_fwd: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);
@@ -583,7 +574,7 @@ size_t fjx_triattn_core_workspace_size(int64_t batch, int64_t rows, int64_t head
                                        int32_t dtype) {
   (void)head_dim;
   if (batch < 1 || rows < 1 || heads < 1 || n < 1 || !dtype_ok(dtype)) return 0;
-  return triattn_ws(batch, rows, n, heads, dtype, false, false).total;
+  return triattn_ws(batch, rows, n, heads, dtype, false).total;
 }
 
 int fjx_triattn_core(const fjx_triattn_core_args* a, hipStream_t st) {
@@ -597,7 +588,7 @@ int fjx_triattn_core(const fjx_triattn_core_args* a, hipStream_t st) {
                 (long long)a->head_dim);
   if (!a->q || !a->k || !a->v || !a->tri_bias || !a->out)
     return fail(FJX_ERR_INVALID, "fjx_triattn_core: a required pointer is NULL");
-  const size_t need = triattn_ws(a->batch, a->rows, a->n, a->heads, a->dtype, false, false).total;
+  const size_t need = triattn_ws(a->batch, a->rows, a->n, a->heads, a->dtype, false).total;
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_triattn_core: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);

@@ -63,6 +63,30 @@ __device__ __forceinline__ void store8(float* p, const f32x8& v) {
   *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
 }
 
+// 4 contiguous elements <-> fp32 (8 B for bf16, 16 B for fp32)
+__device__ __forceinline__ void load4f(const bf16* p, float* o) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = static_cast<float>(v[e]);
+}
+__device__ __forceinline__ void load4f(const float* p, float* o) {
+  const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = v[e];
+}
+__device__ __forceinline__ void store4f(bf16* p, const float* f) {
+  bf16x4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = static_cast<bf16>(f[e]);
+  *reinterpret_cast<bf16x4*>(p) = v;
+}
+__device__ __forceinline__ void store4f(float* p, const float* f) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{f[0], f[1], f[2], f[3]};
+}
+
+// round an fp32 value through the element type T
+template <typename T> __device__ __forceinline__ float round_to(float x) { return static_cast<float>(static_cast<T>(x)); }
+
 // 8 elements -> fp32 and back
 __device__ __forceinline__ void to_f32x8(const bf16x8& v, float* o) {
 #pragma unroll
@@ -87,8 +111,9 @@ template <> __device__ __forceinline__ f32x8 pack8<float>(const float* f) {
 }
 
 __device__ __forceinline__ float fast_sigmoid(float x) {
-  // 1 / (1 + 2^(-x log2 e)); saturates cleanly to 0 / 1 at the extremes
-  return __frcp_rn(1.0f + exp2f(-x * kLog2e));
+  // 1 / (1 + 2^(-x log2 e)) on the hardware v_exp_f32 / v_rcp_f32 (about 1 ulp
+  // each); saturates cleanly to 0 (2^big = inf, rcp(inf) = 0) and to 1
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
 
 // wave-wide xor shuffle of a float (64 lanes)

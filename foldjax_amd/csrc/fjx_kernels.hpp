@@ -15,10 +15,8 @@ struct TriMulPrologueParams {
   const T* ln_b;
   const T* w_p;     // [256][128]: rows 0..127 -> a, 128..255 -> b
   const T* w_g;     // [256][128]
-  const T* w_gout;  // [128][128]
   T* a_cm;          // [B][128][N*N] virtual grid
   T* b_cm;
-  T* g;             // [B][N*N][128] original grid
   int64_t n;
   float eps;
   int transpose;    // 1 for the incoming direction
@@ -34,11 +32,9 @@ struct TriAttnPrologueParams {
   const T* w_q;     // [128][128]
   const T* w_k;
   const T* w_v;
-  const T* w_g;     // or null
   T* q;             // [B][N][4][Np][32]
   T* k;
   T* vt;            // [B][N][128][Np]
-  T* g;             // [B][N][N][128]
   T* bias;          // [B][4][Np][Np]
   float* mb;        // [B][N][Np]
   int64_t n;
@@ -50,17 +46,34 @@ struct TriAttnPrologueParams {
 };
 
 template <typename T>
-struct EpilogueParams {
-  const T* x;         // channel-major [B][128][N*N] or position-major [B][N*N][128]
-  const T* ln_w;      // LN over the 128 input channels (tri-mul LN_out)
-  const T* ln_b;
-  const T* w;         // [128][128]
-  const T* gate;      // [B][N*N][128] at the output position, or null
-  const T* residual;  // [B][N*N][128] or null (may alias out)
+struct TriMulEpilogueParams {
+  const T* o;         // contraction output, channel-major [B][128][N*N]
+  const T* x;         // the op's input [B][N][N][128] (for the output gate)
+  const T* ln_in_w;   // LN_in, recomputed for the gate
+  const T* ln_in_b;
+  const T* ln_out_w;  // LN over the contraction output
+  const T* ln_out_b;
+  const T* w_pout;    // [128][128]
+  const T* w_gout;    // [128][128]
+  const T* residual;  // [B][N][N][128] or null (may alias out)
   T* out;
   int64_t n;
   float eps;
-  int transpose;
+};
+
+template <typename T>
+struct TriAttnEpilogueParams {
+  const T* o;         // attention output, position-major [B][N*N][128] in the virtual grid
+  const T* x;         // the op's input [B][N][N][128] (for the gate)
+  const T* ln_w;
+  const T* ln_b;
+  const T* w_g;       // [128][128] or null (ungated)
+  const T* w_o;       // [128][128]
+  const T* residual;  // original grid, or null (may alias out)
+  T* out;             // original grid
+  int64_t n;
+  float eps;
+  int transpose;      // 1 for the ending node
 };
 
 template <typename T, typename TO>
@@ -118,7 +131,9 @@ void launch_trimul_prologue(const TriMulPrologueParams<T>& p, int64_t batch, hip
 template <typename T>
 void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, hipStream_t st);
 template <typename T>
-void launch_epilogue(const EpilogueParams<T>& p, bool channel_major, bool ln, int64_t batch, hipStream_t st);
+void launch_trimul_epilogue(const TriMulEpilogueParams<T>& p, int64_t batch, hipStream_t st);
+template <typename T>
+void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st);
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st);
 template <typename T>

@@ -1,48 +1,101 @@
-// LayerNorm + projection prologues and the projection epilogue of the
+// LayerNorm + projection prologues and the projection epilogues of the
 // triangle ops, on MFMA.
 //
-// All three kernels work on tiles of 64 pair positions (one "row" r of the
-// pair grid, 64 consecutive columns s0..s0+63) with 256 threads (4 waves).
+// Work unit: a tile of 128 pair positions -- one row r of the (virtual) pair
+// grid, 128 consecutive columns s0..s0+127. The LayerNormed tile sits in LDS
+// as [position][channel]; each wave computes all 128 positions for 32 output
+// channels of one weight, streaming the 8 row tiles of 16 positions past a
+// weight slab held in registers.
+//
+// The kernels are persistent: a grid sized to the resident capacity of the
+// device loops over tiles, keeps its weight slabs in registers for the whole
+// launch and, once a tile's inputs are in LDS, issues the global loads of its
+// next tile before computing the current one. Vector-memory loads complete in
+// issue order, so after that prefetch an iteration issues no other global load
+// it has to wait for: the residual, when it is the op's own input, is read
+// back from a raw copy of the input tile in LDS.
+//
+// Results are stored straight from the MFMA accumulators, 4 contiguous
+// elements per lane:
+//   channel-major outputs use D[pos][ch] = X W^T (a lane holds 4 consecutive
+//   positions of one channel),
+//   position-major outputs use D'[ch][pos] = W X^T (a lane holds 4 consecutive
+//   channels of one position); the two differ only in the MFMA operand order.
+//
 // Prologues address the pair tensor through a *virtual* grid: virtual (r, s)
 // reads x[b, r, s] or, when transposed, x[b, s, r]. The incoming tri-mul and
-// the ending-node tri-attn run entirely in that transposed virtual grid, so
-// no transposed copy of x is ever written.
+// the ending-node tri-attn run entirely in that transposed virtual grid, so no
+// transposed copy of x is ever written.
+//
+// The output gates -- tri-mul's sigmoid(LN_in(x) g_out^T) and tri-attn's
+// sigmoid(LN(x) w_g^T) -- are computed in the epilogues, which read x anyway
+// at the output positions; no gate tensor makes an HBM round trip.
 //
 // Weights are PyTorch [out][in] row-major: output channel o is the contiguous
-// row W[o][0..127], which is exactly the MFMA B fragment (8 contiguous k for
-// one output column) and is read straight from L2.
+// row W[o][0..127], which is exactly an MFMA fragment (8 contiguous k for one
+// output channel).
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
 
 namespace fjx {
 
-constexpr int kTile = 64;        // positions per workgroup
-constexpr int kC = 128;          // channels handled by these kernels
-constexpr int kXPad = 8;         // LDS row padding (elements) for the [pos][ch] tile
-constexpr int kYPad = 8;         // LDS padding for the [ch][pos] staging tile
+namespace {
 
-// ---------------------------------------------------------------------------
-// Stage 1 shared by the prologues: load 64 positions x 128 channels, LayerNorm
-// in fp32, write the normalised (and affine-transformed) rows to LDS as T.
-// Thread t owns position t/4 and channels [32*(t%4), +32).
-// ---------------------------------------------------------------------------
+constexpr int kTP = 128;     // positions per tile
+constexpr int kC = 128;      // channels
+constexpr int kLd = kC + 8;  // padded LDS row (elements)
+
+// fp32 copy of a LayerNorm affine (gamma, beta) in LDS, staged once per
+// workgroup so the per-element normalisation does no bf16 unpacking
+struct LnAffine {
+  float w[kC];
+  float b[kC];
+};
+
 template <typename T>
-__device__ __forceinline__ void ln_tile_to_lds(const T* __restrict__ x, int64_t row_off,
-                                               bool valid, const T* __restrict__ ln_w,
-                                               const T* __restrict__ ln_b, float eps,
-                                               T (*xs)[kC + kXPad]) {
-  const int t = threadIdx.x;
-  const int p = t >> 2;
-  const int c0 = (t & 3) * 32;
-  float v[32];
-  if (valid) {
-    const T* src = x + row_off + c0;
+__device__ __forceinline__ void stage_ln(const T* __restrict__ ln_w, const T* __restrict__ ln_b, LnAffine& l) {
+  const int t = threadIdx.x;  // >= 256 threads: 0..127 gamma, 128..255 beta
+  if (t < kC) l.w[t] = to_f32(ln_w[t]);
+  else if (t < 2 * kC) l.b[t - kC] = to_f32(ln_b[t - kC]);
+}
+
+// The 32 channels [32*part, +32) of one pair-tensor row (part = threadIdx.x % 4),
+// raw, or zeros when src is null (a position outside the grid)
+template <typename T>
+struct RowPart {
+  typename Frag<T>::type f[4];
+};
+template <typename T>
+__device__ __forceinline__ void load_row_part(const T* __restrict__ src, RowPart<T>& r) {
+  const int c0 = (threadIdx.x & 3) * 32;
+  if (src) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) to_f32x8(load8(src + 8 * q), v + 8 * q);
+    for (int q = 0; q < 4; ++q) r.f[q] = load8(src + c0 + 8 * q);
   } else {
+    const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < 32; ++e) v[e] = 0.f;
+    for (int q = 0; q < 4; ++q) r.f[q] = pack8<T>(z);
   }
+}
+template <typename T>
+__device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restrict__ dst_row) {
+  const int c0 = (threadIdx.x & 3) * 32;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) store8(dst_row + c0 + 8 * q, r.f[q]);
+}
+
+// LayerNorm of 128 channels held by 4 consecutive threads (32 channels each),
+// written to dst_row[32*part ..] as T
+template <typename T>
+__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, T* __restrict__ dst_row) {
+  const int c0 = (threadIdx.x & 3) * 32;
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
   float s = 0.f;
 #pragma unroll
   for (int e = 0; e < 32; ++e) s += v[e];
@@ -58,476 +111,644 @@ __device__ __forceinline__ void ln_tile_to_lds(const T* __restrict__ x, int64_t 
   q2 += shfl_xor(q2, 1);
   q2 += shfl_xor(q2, 2);
   const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / kC) + eps);
+  const float shift = -mean * rstd;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    float w[8], b[8], o[8];
-    to_f32x8(load8(ln_w + c0 + 8 * q), w);
-    to_f32x8(load8(ln_b + c0 + 8 * q), b);
+    // one 8-channel chunk at a time: keeps the scheduler from hoisting all 16
+    // affine reads (64 VGPRs) ahead of the arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(&l.w[c0 + 8 * q]);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(&l.w[c0 + 8 * q + 4]);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(&l.b[c0 + 8 * q]);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(&l.b[c0 + 8 * q + 4]);
+    float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (v[8 * q + e] - mean) * rstd * w[e] + b[e];
-    store8(&xs[p][c0 + 8 * q], pack8<T>(o));
+    for (int e = 0; e < 4; ++e) {
+      o[e] = fmaf(fmaf(v[8 * q + e], rstd, shift), w0[e], b0[e]);
+      o[4 + e] = fmaf(fmaf(v[8 * q + 4 + e], rstd, shift), w1[e], b1[e]);
+    }
+    store8(dst_row + c0 + 8 * q, pack8<T>(o));
   }
 }
 
-// One wave: acc[rt][ct] += X[16rt.., :] * W[col0 + 16ct.., :]^T over K = 128.
+// One wave's 32 output channels col0..col0+31 of a [128][128] weight as MFMA
+// fragments: wf[ks][ct] holds W[col0 + 16ct + l%16][32ks + 8g .. +7].
 template <typename T>
-__device__ __forceinline__ void wave_gemm_64x32(const T (*xs)[kC + kXPad], const T* __restrict__ w,
-                                                int col0, f32x4 (&acc)[4][2]) {
+using WSlab = typename Frag<T>::type[4][2];
+
+template <typename T>
+__device__ __forceinline__ void load_wslab(const T* __restrict__ w, int col0, WSlab<T>& wf) {
   const int lane = threadIdx.x & 63;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < kC / 32; ++ks) {
-    typename Frag<T>::type bf[2];
+  for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
-      bf[ct] = load8(w + (int64_t)(col0 + 16 * ct + li) * kC + 32 * ks + 8 * lg);
+      wf[ks][ct] = load8(w + (int64_t)(col0 + 16 * ct + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
+}
+
+// Row tile rt (tile rows 16rt..16rt+15) against one slab, K = 128:
+//   kTrans = false: acc[ct][q] = D[pos 16rt + 4g + q][ch col0 + 16ct + l%16]
+//   kTrans = true:  acc[ct][q] = D[pos 16rt + l%16][ch col0 + 16ct + 4g + q]
+template <typename T, bool kTrans>
+__device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab<T>& wf, f32x4 (&acc)[2]) {
+  const int lane = threadIdx.x & 63;
+  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const typename Frag<T>::type af = load8(&xs[16 * rt + li][32 * ks + 8 * lg]);
+  for (int ks = 0; ks < 4; ++ks) {
+    const typename Frag<T>::type xf = load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) mma(acc[rt][ct], af, bf[ct]);
+    for (int ct = 0; ct < 2; ++ct) {
+      if (kTrans) mma(acc[ct], wf[ks][ct], xf);
+      else mma(acc[ct], xf, wf[ks][ct]);
     }
   }
 }
 
-// Copy a channel-major LDS tile ys[ch][pos] (64 positions) to dst[ch * ch_stride + pos],
-// positions [0, nvalid) of the tile; when `pad_to` > nvalid, positions
-// [nvalid, pad_to) are written with `fill`.
-template <typename T>
-__device__ __forceinline__ void store_cm_tile(const T (*ys)[kTile + kYPad], T* __restrict__ dst,
-                                              int64_t ch_stride, int nvalid, int pad_to, bool aligned,
-                                              float fill) {
-  const int t = threadIdx.x;
-  const int limit = pad_to > nvalid ? pad_to : nvalid;
-  // 128 channels x 8 chunks of 8 positions = 1024 chunks, 4 per thread
+// the same for two slabs sharing the row fragments
+template <typename T, bool kTrans>
+__device__ __forceinline__ void tile_mma2(const T (*xs)[kLd], int rt, const WSlab<T>& w1, const WSlab<T>& w2,
+                                          f32x4 (&a1)[2], f32x4 (&a2)[2]) {
+  const int lane = threadIdx.x & 63;
+  a1[0] = a1[1] = a2[0] = a2[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int idx = t + 256 * it;
-    const int ch = idx >> 3;
-    const int p0 = (idx & 7) * 8;
-    T* d = dst + (int64_t)ch * ch_stride + p0;
-    if (aligned && p0 + 8 <= nvalid) {
-      store8(d, load8(&ys[ch][p0]));
-    } else {
+  for (int ks = 0; ks < 4; ++ks) {
+    const typename Frag<T>::type xf = load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int p = p0 + e;
-        if (p < nvalid) d[e] = ys[ch][p];
-        else if (p < limit) d[e] = from_f32<T>(fill);
+    for (int ct = 0; ct < 2; ++ct) {
+      if (kTrans) {
+        mma(a1[ct], w1[ks][ct], xf);
+        mma(a2[ct], w2[ks][ct], xf);
+      } else {
+        mma(a1[ct], xf, w1[ks][ct]);
+        mma(a2[ct], xf, w2[ks][ct]);
       }
     }
   }
 }
 
+// 4 elements of T packed in registers (two VGPRs for bf16)
+template <typename T> struct Vec4;
+template <> struct Vec4<bf16> { typedef bf16x4 type; };
+template <> struct Vec4<float> { typedef f32x4 type; };
+
+template <typename T>
+__device__ __forceinline__ typename Vec4<T>::type load4raw(const T* p) {
+  return *reinterpret_cast<const typename Vec4<T>::type*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void store4raw(T* p, const typename Vec4<T>::type& v) {
+  *reinterpret_cast<typename Vec4<T>::type*>(p) = v;
+}
+
+// Store 4 consecutive elements v[0..3] at dst[0..3], of which the first `cnt`
+// exist; vectorised when all 4 exist and `vec` says the address is aligned.
+template <typename T>
+__device__ __forceinline__ void store4_masked(T* dst, const float* v, int cnt, bool vec) {
+  if (cnt >= 4 && vec) {
+    store4f(dst, v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < cnt) dst[q] = from_f32<T>(v[q]);
+  }
+}
+
+// Rows of the raw input tile kept in LDS for the residual: the whole tile for
+// bf16; fp32 tiles are twice as large, so there the residual is read from
+// global memory instead
+template <typename T>
+constexpr int raw_rows() {
+  return sizeof(T) == 2 ? kTP : 1;
+}
+
+// tile index -> (batch, row, first column); columns fastest, then rows
+struct TileRS {
+  int b;
+  int r;
+  int s0;
+};
+__device__ __forceinline__ TileRS tile_at(int64_t tile, int64_t ntx, int64_t nrows) {
+  TileRS t;
+  t.s0 = (int)(tile % ntx) * kTP;
+  const int64_t q = tile / ntx;
+  t.r = (int)(q % nrows);
+  t.b = (int)(q / nrows);
+  return t;
+}
+
+}  // namespace
+
 // ---------------------------------------------------------------------------
-// Triangle multiplication prologue.
-//   a_cm/b_cm: [B][c_h][N*N] channel-major in the virtual grid (contraction
-//   operands with the contracted axis contiguous); g: [B][N*N][c_z]
-//   position-major in the original grid, holding sigmoid(x_ln g_out^T).
+// Triangle multiplication prologue, 512 threads: waves 0-3 produce a, waves 4-7
+// produce b, each wave 32 channels, holding the p_in and g_in slabs of those
+// channels for the whole launch.
+//   a_cm/b_cm: [B][128][N*N] channel-major in the virtual grid (contraction
+//   operands with the contracted axis contiguous), each
+//   mask * sigmoid(x_ln g_in^T) * (x_ln p_in^T).
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void trimul_prologue_kernel(TriMulPrologueParams<T> P) {
-  __shared__ __attribute__((aligned(16))) T xs[kTile][kC + kXPad];
-  __shared__ __attribute__((aligned(16))) T ys[kC][kTile + kYPad];
-  __shared__ float mrow[kTile];
+__global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulPrologueParams<T> P, int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
+  __shared__ __attribute__((aligned(16))) float mrow[kTP];
+  __shared__ __attribute__((aligned(16))) LnAffine ln;
 
   const int64_t n = P.n;
-  const int r = blockIdx.y;
-  const int s0 = blockIdx.x * kTile;
-  const int b = blockIdx.z;
-  const int t = threadIdx.x;
-  const int nvalid = (int)min<int64_t>(kTile, n - s0);
   const int64_t nn = n * n;
-
-  {
-    const int p = t >> 2;
-    const int s = s0 + p;
-    const bool valid = s < n;
-    const int64_t orig = P.transpose ? (int64_t)s * n + r : (int64_t)r * n + s;
-    const int64_t off = ((int64_t)b * nn + (valid ? orig : 0)) * kC;
-    ln_tile_to_lds<T>(P.x, off, valid, P.ln_w, P.ln_b, P.eps, xs);
-    if ((t & 3) == 0) {
-      float m = 0.f;
-      if (valid) m = P.mask ? to_f32(P.mask[(int64_t)b * nn + orig]) : 1.0f;
-      mrow[p] = m;
-    }
-  }
-  __syncthreads();
-
+  const int64_t ntx = (n + kTP - 1) / kTP;
+  const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int col0 = 32 * wave;
-  const bool aligned = (n % 8) == 0;
+  const int half = wave >> 2;
+  const int col0 = 32 * (wave & 3);
+  const int p = t >> 2;  // LayerNorm position of this thread
+  const bool vec = (n % 4) == 0;
 
-  // a then b: gated projections, channel-major stores
-#pragma unroll 1
-  for (int half = 0; half < 2; ++half) {
-    f32x4 accp[4][2], accg[4][2];
-    wave_gemm_64x32<T>(xs, P.w_p + (int64_t)half * kC * kC, col0, accp);
-    wave_gemm_64x32<T>(xs, P.w_g + (int64_t)half * kC * kC, col0, accg);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = 16 * rt + 4 * lg + q;
-          const int col = col0 + 16 * ct + li;
-          const float val = mrow[row] * fast_sigmoid(accg[rt][ct][q]) * accp[rt][ct][q];
-          ys[col][row] = from_f32<T>(val);
-        }
-    __syncthreads();
-    T* dst = (half == 0 ? P.a_cm : P.b_cm) + (int64_t)b * kC * nn + (int64_t)r * n + s0;
-    store_cm_tile<T>(ys, dst, nn, nvalid, nvalid, aligned, 0.f);
-    __syncthreads();
-  }
+  WSlab<T> wp, wg;
+  load_wslab<T>(P.w_p + (int64_t)half * kC * kC, col0, wp);
+  load_wslab<T>(P.w_g + (int64_t)half * kC * kC, col0, wg);
+  stage_ln<T>(P.ln_w, P.ln_b, ln);
 
-  // output gate sigmoid(x_ln g_out^T), position-major in the original grid
-  {
-    f32x4 acc[4][2];
-    wave_gemm_64x32<T>(xs, P.w_gout, col0, acc);
-    // reuse ys as a [pos][ch] tile: 64 x 128 fits in 128 x 72
-    T(*yp)[kC + kXPad] = reinterpret_cast<T(*)[kC + kXPad]>(&ys[0][0]);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          yp[16 * rt + 4 * lg + q][col0 + 16 * ct + li] = from_f32<T>(fast_sigmoid(acc[rt][ct][q]));
+  RowPart<T> xr;
+  float mk = 0.f;
+  auto fetch = [&](int64_t tile) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int s = tl.s0 + p;
+    const bool valid = s < n;
+    const int64_t pos = (int64_t)tl.b * nn + (P.transpose ? (int64_t)s * n + tl.r : (int64_t)tl.r * n + s);
+    load_row_part<T>(valid ? P.x + pos * kC : nullptr, xr);
+    mk = valid ? (P.mask ? to_f32(P.mask[pos]) : 1.0f) : 0.f;
+  };
+
+  int64_t tile = blockIdx.x;
+  if (tile < ntiles) fetch(tile);
+  __syncthreads();  // LayerNorm affine staged
+  for (; tile < ntiles; tile += gridDim.x) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+    if ((t & 3) == 0) mrow[p] = mk;
     __syncthreads();
-    // 64 positions x 16 chunks of 8 channels = 1024 chunks, 4 per thread
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
+
+    T* dst = (half == 0 ? P.a_cm : P.b_cm) + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
+#pragma unroll 2
+    for (int rt = 0; rt < 8; ++rt) {
+      f32x4 ap[2], ag[2];
+      tile_mma2<T, false>(xs, rt, wp, wg, ap, ag);
+      const int p0 = 16 * rt + 4 * (lane >> 4);
+      const f32x4 m = *reinterpret_cast<const f32x4*>(&mrow[p0]);
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int idx = t + 256 * it;
-      const int p = idx >> 4;
-      const int c8 = (idx & 15) * 8;
-      const int s = s0 + p;
-      if (s < n) {
-        const int64_t orig = P.transpose ? (int64_t)s * n + r : (int64_t)r * n + s;
-        store8(P.g + ((int64_t)b * nn + orig) * kC + c8, load8(&yp[p][c8]));
+      for (int ct = 0; ct < 2; ++ct) {
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = m[q] * fast_sigmoid(ag[ct][q]) * ap[ct][q];
+        store4_masked<T>(dst + (int64_t)(col0 + 16 * ct + (lane & 15)) * nn + p0, v, nvalid - p0, vec);
       }
     }
+    __syncthreads();  // xs and mrow are free for the next tile
   }
 }
 
 // ---------------------------------------------------------------------------
-// Triangle attention prologue (virtual grid, transposed for the ending node).
+// Triangle attention prologue (virtual grid, transposed for the ending node),
+// 512 threads: waves 0-3 produce q and k of head w, waves 4-7 produce v
+// channels 32(w-4).. and rows 2(w-4), 2(w-4)+1 of the triangle-bias tile.
 //   q  [B][N][H][Np][D]  q_ln * (scale*log2 e)
 //   k  [B][N][H][Np][D]
 //   vt [B][N][H*D][Np]   v transposed so that keys are contiguous
-//   g  [B][N][N][H*D]    sigmoid(x_ln w_g^T), or absent
 //   bias [B][H][Np][Np]  x_ln w_bias^T times log2 e (in T)
 //   mb [B][N][Np] fp32   inf*(mask-1)*log2 e, -inf for keys >= N
-// Np = N rounded up to 64; padded key slots of q/k/vt are written as zeros.
+// Np = N rounded up to 64; key slots in [N, Np) are written as zeros.
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(256) void triattn_prologue_kernel(TriAttnPrologueParams<T> P) {
-  __shared__ __attribute__((aligned(16))) T xs[kTile][kC + kXPad];
-  __shared__ __attribute__((aligned(16))) T ys[kC][kTile + kYPad];
-
-  const int64_t n = P.n;
-  const int64_t np = P.np;
-  const int r = blockIdx.y;
-  const int s0 = blockIdx.x * kTile;
-  const int b = blockIdx.z;
-  const int t = threadIdx.x;
-  const int nvalid = (int)max<int64_t>(0, min<int64_t>(kTile, n - s0));
-  const int64_t nn = n * n;
+__global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnPrologueParams<T> P, int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
+  __shared__ __attribute__((aligned(16))) LnAffine ln;
   constexpr int D = 32;
   constexpr int H = 4;
 
-  {
-    const int p = t >> 2;
-    const int s = s0 + p;
-    const bool valid = s < n;
-    const int64_t orig = P.transpose ? (int64_t)s * n + r : (int64_t)r * n + s;
-    const int64_t off = ((int64_t)b * nn + (valid ? orig : 0)) * kC;
-    ln_tile_to_lds<T>(P.x, off, valid, P.ln_w, P.ln_b, P.eps, xs);
-    if ((t & 3) == 0) {
-      float mbv = -INFINITY;
-      if (valid) {
-        const float m = P.mask ? to_f32(P.mask[(int64_t)b * nn + orig]) : 1.0f;
-        mbv = P.inf * (m - 1.0f) * kLog2e;
-      }
-      P.mb[((int64_t)b * n + r) * np + s] = mbv;
-    }
-  }
-  __syncthreads();
-
-  // triangle bias: 64 positions x 4 heads, one dot product of length 128 per thread
-  {
-    const int p = t >> 2;
-    const int h = t & 3;
-    const int s = s0 + p;
-    if (s < np) {
-      float acc = 0.f;
-      if (s < n) {
-        const T* wrow = P.w_bias + h * kC;
-#pragma unroll 4
-        for (int c = 0; c < kC; c += 8) {
-          float xv[8], wv[8];
-          to_f32x8(load8(&xs[p][c]), xv);
-          to_f32x8(load8(wrow + c), wv);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc += xv[e] * wv[e];
-        }
-      }
-      P.bias[(((int64_t)b * H + h) * np + r) * np + s] = from_f32<T>(acc * kLog2e);
-    }
-  }
-
+  const int64_t n = P.n;
+  const int64_t np = P.np;
+  const int64_t nn = n * n;
+  const int64_t ntx = (np + kTP - 1) / kTP;
+  const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int col0 = 32 * wave;
-  const int nstore = (int)min<int64_t>(kTile, np - s0);  // positions incl. zero padding
-  T(*yp)[kC + kXPad] = reinterpret_cast<T(*)[kC + kXPad]>(&ys[0][0]);
+  const int role = wave >> 2;  // 0: q and k; 1: v and bias
+  const int col0 = 32 * (wave & 3);
+  const int p = t >> 2;
 
-  // q and k: [pos][ch] staging, per-head contiguous blocks of 64 x 32
-#pragma unroll 1
-  for (int which = 0; which < 2; ++which) {
-    f32x4 acc[4][2];
-    wave_gemm_64x32<T>(xs, which == 0 ? P.w_q : P.w_k, col0, acc);
-    const float sc = which == 0 ? P.q_scale : 1.0f;
+  // role 0: w1 = q slab, w2 = k slab of head (wave & 3)
+  // role 1: w1 = v slab; w2[ks][0] = bias weights as one 16-column tile
+  //         (columns 0..3 = heads, the rest zero)
+  WSlab<T> w1, w2;
+  if (role == 0) {
+    load_wslab<T>(P.w_q, col0, w1);
+    load_wslab<T>(P.w_k, col0, w2);
+  } else {
+    load_wslab<T>(P.w_v, col0, w1);
+    const int li = lane & 15;
+    const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = 16 * rt + 4 * lg + q;
-          const float val = (s0 + row < n) ? acc[rt][ct][q] * sc : 0.f;
-          yp[row][col0 + 16 * ct + li] = from_f32<T>(val);
-        }
-    __syncthreads();
-    T* base = (which == 0 ? P.q : P.k) + ((int64_t)b * n + r) * H * np * D;
-    // 64 positions x 4 heads x 4 chunks of 8 = 1024 chunks
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int idx = t + 256 * it;
-      const int p = idx >> 4;
-      const int h = (idx >> 2) & 3;
-      const int d8 = (idx & 3) * 8;
-      if (p < nstore) store8(base + ((int64_t)h * np + s0 + p) * D + d8, load8(&yp[p][h * D + d8]));
+    for (int ks = 0; ks < 4; ++ks) {
+      w2[ks][0] = li < H ? load8(P.w_bias + li * kC + 32 * ks + 8 * (lane >> 4)) : pack8<T>(z);
+      w2[ks][1] = pack8<T>(z);
     }
-    __syncthreads();
   }
+  stage_ln<T>(P.ln_w, P.ln_b, ln);
 
-  // v: channel-major staging -> vt[b][r][ch][s]
-  {
-    f32x4 acc[4][2];
-    wave_gemm_64x32<T>(xs, P.w_v, col0, acc);
+  RowPart<T> xr;
+  float mbv = -INFINITY;
+  auto fetch = [&](int64_t tile) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int s = tl.s0 + p;
+    const bool valid = s < n;
+    const int64_t pos = (int64_t)tl.b * nn + (P.transpose ? (int64_t)s * n + tl.r : (int64_t)tl.r * n + s);
+    load_row_part<T>(valid ? P.x + pos * kC : nullptr, xr);
+    mbv = valid ? P.inf * ((P.mask ? to_f32(P.mask[pos]) : 1.0f) - 1.0f) * kLog2e : -INFINITY;
+  };
+
+  int64_t tile = blockIdx.x;
+  if (tile < ntiles) fetch(tile);
+  __syncthreads();
+  for (; tile < ntiles; tile += gridDim.x) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int nstore = (int)min<int64_t>(kTP, np - tl.s0);  // incl. zero padding; a multiple of 64
+    const int nreal = (int)max<int64_t>(0, min<int64_t>(kTP, n - tl.s0));
+    ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+    if ((t & 3) == 0 && p < nstore) P.mb[((int64_t)tl.b * n + tl.r) * np + tl.s0 + p] = mbv;
+    __syncthreads();
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
+
+    if (role == 0) {
+      // transposed accumulators: lane (rt, ct) holds position 16rt + l%16,
+      // head dims 16ct + 4g .. +3 of head (wave & 3)
+      const int64_t head_off = (((int64_t)tl.b * n + tl.r) * H + (wave & 3)) * np * D;
+      T* qb = P.q + head_off;
+      T* kb = P.k + head_off;
+#pragma unroll 2
+      for (int rt = 0; rt < 8; ++rt) {
+        const int pp = 16 * rt + (lane & 15);
+        f32x4 aq[2], ak[2];
+        tile_mma2<T, true>(xs, rt, w1, w2, aq, ak);
+        if (pp < nstore) {
+          const bool real = pp < nreal;
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+          for (int ct = 0; ct < 2; ++ct) {
+            float vq[4], vk[4];
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int row = 16 * rt + 4 * lg + q;
-          ys[col0 + 16 * ct + li][row] = from_f32<T>(s0 + row < n ? acc[rt][ct][q] : 0.f);
+            for (int q = 0; q < 4; ++q) {
+              vq[q] = real ? aq[ct][q] * P.q_scale : 0.f;
+              vk[q] = real ? ak[ct][q] : 0.f;
+            }
+            const int64_t off = (int64_t)(tl.s0 + pp) * D + 16 * ct + 4 * (lane >> 4);
+            store4f(qb + off, vq);
+            store4f(kb + off, vk);
+          }
         }
-    __syncthreads();
-    T* dst = P.vt + ((int64_t)b * n + r) * kC * np + s0;
-    store_cm_tile<T>(ys, dst, np, nstore, nstore, true, 0.f);
-    __syncthreads();
-  }
-
-  // gate: sigmoid, position-major in the virtual grid
-  if (P.w_g) {
-    f32x4 acc[4][2];
-    wave_gemm_64x32<T>(xs, P.w_g, col0, acc);
+      }
+    } else {
+      // v, channel-major: vt[b][r][ch][s]
+      T* vdst = P.vt + ((int64_t)tl.b * n + tl.r) * kC * np + tl.s0;
+#pragma unroll 2
+      for (int rt = 0; rt < 8; ++rt) {
+        const int p0 = 16 * rt + 4 * (lane >> 4);
+        f32x4 av[2];
+        tile_mma<T, false>(xs, rt, w1, av);
+        if (p0 < nstore) {
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+          for (int ct = 0; ct < 2; ++ct) {
+            float v[4];
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+            for (int q = 0; q < 4; ++q) v[q] = p0 + q < nreal ? av[ct][q] : 0.f;
+            store4f(vdst + (int64_t)(col0 + 16 * ct + (lane & 15)) * np + p0, v);
+          }
+        }
+      }
+      // triangle bias: lane holds D[pos 16rt + 4g + q][head l%16]
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          yp[16 * rt + 4 * lg + q][col0 + 16 * ct + li] = from_f32<T>(fast_sigmoid(acc[rt][ct][q]));
-    __syncthreads();
+      for (int k = 0; k < 2; ++k) {
+        const int rt = 2 * (wave & 3) + k;
+        const int p0 = 16 * rt + 4 * (lane >> 4);
+        f32x4 ab[2];
+        tile_mma<T, false>(xs, rt, w2, ab);
+        const int h = lane & 15;
+        if (h < H && p0 < nstore) {
+          float v[4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int idx = t + 256 * it;
-      const int p = idx >> 4;
-      const int c8 = (idx & 15) * 8;
-      if (p < nvalid) store8(P.g + (((int64_t)b * n + r) * n + s0 + p) * kC + c8, load8(&yp[p][c8]));
+          for (int q = 0; q < 4; ++q) v[q] = p0 + q < nreal ? ab[0][q] * kLog2e : 0.f;
+          store4f(P.bias + (((int64_t)tl.b * H + h) * np + tl.r) * np + tl.s0 + p0, v);
+        }
+      }
     }
+    __syncthreads();  // xs is free for the next tile
   }
 }
 
 // ---------------------------------------------------------------------------
-// Epilogue: y = [LN](X) W^T [* gate] [+ residual], 128 -> 128 channels.
-//   X is channel-major ([B][128][N*N], tri-mul contraction output) or
-//   position-major ([B][N*N][128], gated attention output) in the virtual grid
-//   rows r, columns s; the result goes to out[b, r, s] or, transposed,
-//   out[b, s, r]. gate and residual are read at the output position.
+// Triangle multiplication epilogue, original grid (i, j):
+//   out[i,j] = LN_out(o[:, i, j]) p_out^T * T(sigmoid(LN_in(x[i,j]) g_out^T)) (+ residual)
+// with o channel-major [B][128][N*N]. 512 threads: wave w owns tile rows
+// 64(w/4) .. +63 and output channels 32(w%4) .. +31 of both products, holding
+// the g_out and p_out slabs of those channels; the two LayerNormed tiles sit
+// side by side in LDS so the gate and the projection of a row tile are
+// combined as soon as both accumulators are done.
 // ---------------------------------------------------------------------------
-template <typename T, bool kChannelMajor, bool kLN>
-__global__ __launch_bounds__(256) void rowgemm_epilogue_kernel(EpilogueParams<T> P) {
-  __shared__ __attribute__((aligned(16))) T xs[kTile][kC + kXPad];
-  __shared__ __attribute__((aligned(16))) float yf[kTile][kC + 4];
+template <typename T>
+__global__ __launch_bounds__(512) void trimul_epilogue_kernel(TriMulEpilogueParams<T> P, int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) T xg[kTP][kLd];    // LN_in(x)
+  __shared__ __attribute__((aligned(16))) T xp[kTP][kLd];    // LN_out(o)
+  __shared__ __attribute__((aligned(16))) T xraw[raw_rows<T>()][kLd];  // x, when it is also the residual
+  __shared__ __attribute__((aligned(16))) LnAffine ln_in, ln_out;
 
   const int64_t n = P.n;
-  const int r = blockIdx.y;
-  const int s0 = blockIdx.x * kTile;
-  const int b = blockIdx.z;
-  const int t = threadIdx.x;
-  const int nvalid = (int)min<int64_t>(kTile, n - s0);
   const int64_t nn = n * n;
-  const int64_t vrow = (int64_t)r * n + s0;  // flat virtual index of the tile's first position
-
-  if (kChannelMajor) {
-    const T* src = P.x + (int64_t)b * kC * nn + vrow;
-    const bool aligned = (n % 8) == 0;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int idx = t + 256 * it;
-      const int ch = idx >> 3;
-      const int p0 = (idx & 7) * 8;
-      float v[8];
-      if (aligned && p0 + 8 <= nvalid) {
-        to_f32x8(load8(src + (int64_t)ch * nn + p0), v);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (p0 + e < nvalid) ? to_f32(src[(int64_t)ch * nn + p0 + e]) : 0.f;
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xs[p0 + e][ch] = from_f32<T>(v[e]);
-    }
-  } else {
-    const T* src = P.x + ((int64_t)b * nn + vrow) * kC;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int idx = t + 256 * it;
-      const int p = idx >> 4;
-      const int c8 = (idx & 15) * 8;
-      if (p < nvalid) store8(&xs[p][c8], load8(src + (int64_t)p * kC + c8));
-      else {
-        const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        store8(&xs[p][c8], pack8<T>(zero));
-      }
-    }
-  }
-  __syncthreads();
-
-  if (kLN) {
-    const int p = t >> 2;
-    const int c0 = (t & 3) * 32;
-    float v[32];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) to_f32x8(load8(&xs[p][c0 + 8 * q]), v + 8 * q);
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) s += v[e];
-    s += shfl_xor(s, 1);
-    s += shfl_xor(s, 2);
-    const float mean = s * (1.0f / kC);
-    float q2 = 0.f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const float d = v[e] - mean;
-      q2 += d * d;
-    }
-    q2 += shfl_xor(q2, 1);
-    q2 += shfl_xor(q2, 2);
-    const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / kC) + P.eps);
-    // every thread of the quad has read its row before anyone rewrites it
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float w[8], bb[8], o[8];
-      to_f32x8(load8(P.ln_w + c0 + 8 * q), w);
-      to_f32x8(load8(P.ln_b + c0 + 8 * q), bb);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (v[8 * q + e] - mean) * rstd * w[e] + bb[e];
-      store8(&xs[p][c0 + 8 * q], pack8<T>(o));
-    }
-    __syncthreads();
-  }
-
+  const int64_t ntx = (n + kTP - 1) / kTP;
+  const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-  const int col0 = 32 * wave;
-  f32x4 acc[4][2];
-  wave_gemm_64x32<T>(xs, P.w, col0, acc);
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) yf[16 * rt + 4 * lg + q][col0 + 16 * ct + li] = acc[rt][ct][q];
-  __syncthreads();
+  const int row0w = 64 * (wave >> 2);
+  const int col0 = 32 * (wave & 3);
+  const int p = t >> 2;  // LayerNorm position of this thread
+  const bool res_x = raw_rows<T>() == kTP && P.residual == P.x;
+  const bool vec8 = (n % 8) == 0;
 
+  WSlab<T> wg, wp;
+  load_wslab<T>(P.w_gout, col0, wg);
+  load_wslab<T>(P.w_pout, col0, wp);
+  stage_ln<T>(P.ln_in_w, P.ln_in_b, ln_in);
+  stage_ln<T>(P.ln_out_w, P.ln_out_b, ln_out);
+
+  // per-tile inputs: the x row of position t/4 (32 channels) and 4 chunks of
+  // the channel-major o tile (chunk it: 16 channels x 4 runs of 8 positions
+  // per wave)
+  RowPart<T> xr;
+  typename Frag<T>::type ot[4];
+  auto o_chunk = [&](int it, int& ch, int& p0) {
+    const int grp = 8 * it + wave;  // 0..31
+    ch = 16 * (grp & 7) + (lane & 15);
+    p0 = 8 * (4 * (grp >> 3) + (lane >> 4));
+  };
+  auto fetch = [&](int64_t tile) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
+    load_row_part<T>(p < nvalid ? P.x + (pos0 + p) * kC : nullptr, xr);
+    const T* src = P.o + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int idx = t + 256 * it;
-    const int p = idx >> 4;
-    const int c8 = (idx & 15) * 8;
-    const int s = s0 + p;
-    if (s < n) {
-      const int64_t orig = P.transpose ? (int64_t)s * n + r : (int64_t)r * n + s;
-      const int64_t off = ((int64_t)b * nn + orig) * kC + c8;
-      float y[8];
+    for (int it = 0; it < 4; ++it) {
+      int ch, p0;
+      o_chunk(it, ch, p0);
+      if (vec8 && p0 + 8 <= nvalid) {
+        ot[it] = load8(src + (int64_t)ch * nn + p0);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = yf[p][c8 + e];
-      if (P.gate) {
-        float g[8];
-        to_f32x8(load8(P.gate + off), g);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] *= g[e];
+        for (int e = 0; e < 8; ++e) ot[it][e] = (p0 + e < nvalid) ? src[(int64_t)ch * nn + p0 + e] : from_f32<T>(0.f);
       }
-      if (P.residual) {
-        float rv[8];
-        to_f32x8(load8(P.residual + off), rv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] += rv[e];
-      }
-      store8(P.out + off, pack8<T>(y));
     }
+  };
+
+  int64_t tile = blockIdx.x;
+  if (tile < ntiles) fetch(tile);
+  __syncthreads();  // LayerNorm affines staged
+  for (; tile < ntiles; tile += gridDim.x) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
+
+    if (res_x) store_row_part<T>(xr, &xraw[p][0]);
+    ln_quad<T>(xr, ln_in, P.eps, &xg[p][0]);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      int ch, p0;
+      o_chunk(it, ch, p0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xp[p0 + e][ch] = ot[it][e];
+    }
+    __syncthreads();
+    {
+      // LN_out in place: each thread rewrites exactly the 32 channels it reads
+      RowPart<T> rp;
+      load_row_part<T>(&xp[p][0], rp);
+      ln_quad<T>(rp, ln_out, P.eps, &xp[p][0]);
+    }
+    __syncthreads();
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
+
+#pragma unroll 2
+    for (int k = 0; k < 4; ++k) {
+      const int rt = (row0w >> 4) + k;
+      f32x4 ag[2], ap[2];
+      tile_mma<T, true>(xg, rt, wg, ag);
+      tile_mma<T, true>(xp, rt, wp, ap);
+      const int pp = 16 * rt + (lane & 15);
+      if (pp < nvalid) {
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int c = col0 + 16 * ct + 4 * (lane >> 4);
+          const int64_t off = (pos0 + pp) * kC + c;
+          float y[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) y[q] = ap[ct][q] * round_to<T>(fast_sigmoid(ag[ct][q]));
+          if (P.residual) {
+            float rv[4];
+            load4f(res_x ? &xraw[pp][c] : P.residual + off, rv);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y[q] += rv[q];
+          }
+          store4f(P.out + off, y);
+        }
+      }
+    }
+    __syncthreads();  // the LDS tiles are free for the next tile
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Triangle attention epilogue, virtual grid rows r, columns s:
+//   out[orig] = T(o[r,s] * sigmoid(LN(x[orig]) w_g^T)) w_o^T (+ residual[orig])
+// with o position-major [B][N*N][128] and orig = (r, s) or (s, r). 512
+// threads: wave w owns tile rows 64(w/4) .. +63 and output channels
+// 32(w%4) .. +31 of both products, holding the w_g and w_o slabs.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(512) void triattn_epilogue_kernel(TriAttnEpilogueParams<T> P, int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];    // LN(x)
+  __shared__ __attribute__((aligned(16))) T xo[kTP][kLd];    // gated o
+  __shared__ __attribute__((aligned(16))) T xraw[raw_rows<T>()][kLd];  // x, when it is also the residual
+  __shared__ __attribute__((aligned(16))) LnAffine ln;
+
+  const int64_t n = P.n;
+  const int64_t nn = n * n;
+  const int64_t ntx = (n + kTP - 1) / kTP;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int row0w = 64 * (wave >> 2);
+  const int col0 = 32 * (wave & 3);
+  const int p = t >> 2;
+  const bool gated = P.w_g != nullptr;
+  const bool res_x = raw_rows<T>() == kTP && P.residual == P.x;
+  const bool need_x = gated || res_x;
+
+  WSlab<T> wg, wo;
+  if (gated) load_wslab<T>(P.w_g, col0, wg);
+  load_wslab<T>(P.w_o, col0, wo);
+  if (gated) stage_ln<T>(P.ln_w, P.ln_b, ln);
+
+  auto orig_of = [&](const TileRS& tl, int pp) -> int64_t {
+    const int64_t s = tl.s0 + pp;
+    return (int64_t)tl.b * nn + (P.transpose ? s * n + tl.r : (int64_t)tl.r * n + s);
+  };
+
+  // per-tile inputs: the x row of position t/4 (at its output position) and o
+  // for this wave's accumulator slots (position 16rt + l%16, channels
+  // col0 + 16ct + 4g ..)
+  RowPart<T> xr;
+  typename Vec4<T>::type ov[4][2];
+  auto fetch = [&](int64_t tile) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    if (need_x) load_row_part<T>(p < nvalid ? P.x + orig_of(tl, p) * kC : nullptr, xr);
+    const T* osrc = P.o + ((int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0) * kC;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int pp = row0w + 16 * k + (lane & 15);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        if (pp < nvalid) {
+          ov[k][ct] = load4raw<T>(osrc + (int64_t)pp * kC + col0 + 16 * ct + 4 * (lane >> 4));
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ov[k][ct][q] = from_f32<T>(0.f);
+        }
+      }
+    }
+  };
+
+  int64_t tile = blockIdx.x;
+  if (tile < ntiles) fetch(tile);
+  __syncthreads();
+  for (; tile < ntiles; tile += gridDim.x) {
+    const TileRS tl = tile_at(tile, ntx, n);
+    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+
+    if (res_x) store_row_part<T>(xr, &xraw[p][0]);
+    if (gated) {
+      ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        f32x4 ag[2];
+        tile_mma<T, true>(xs, (row0w >> 4) + k, wg, ag);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) ov[k][ct][q] = from_f32<T>(to_f32(ov[k][ct][q]) * fast_sigmoid(ag[ct][q]));
+      }
+    }
+    // gated (or raw) o -> xo; the four waves of a row half fill its 128 channels
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        store4raw<T>(&xo[row0w + 16 * k + (lane & 15)][col0 + 16 * ct + 4 * (lane >> 4)], ov[k][ct]);
+    __syncthreads();
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
+
+#pragma unroll 2
+    for (int k = 0; k < 4; ++k) {
+      const int rt = (row0w >> 4) + k;
+      f32x4 acc[2];
+      tile_mma<T, true>(xo, rt, wo, acc);
+      const int pp = 16 * rt + (lane & 15);
+      if (pp < nvalid) {
+        const int64_t pos = orig_of(tl, pp);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int c = col0 + 16 * ct + 4 * (lane >> 4);
+          const int64_t off = pos * kC + c;
+          float y[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) y[q] = acc[ct][q];
+          if (P.residual) {
+            float rv[4];
+            load4f(res_x ? &xraw[pp][c] : P.residual + off, rv);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) y[q] += rv[q];
+          }
+          store4f(P.out + off, y);
+        }
+      }
+    }
+    __syncthreads();  // the LDS tiles are free for the next tile
   }
 }
 
 // ---------------------------------------------------------------------------
 // host-side launchers
 // ---------------------------------------------------------------------------
+namespace {
+
+// Workgroups that fit on the current device at once for `kernel` (resident
+// capacity: CUs x blocks per CU), cached per (kernel, device).
+int resident_blocks(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(kernel, dev);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+  const int v = per_cu * cus;
+  cache[key] = v;
+  return v;
+}
+
+unsigned persistent_grid(const void* kernel, int threads, int64_t ntiles) {
+  const int64_t cap = resident_blocks(kernel, threads);
+  const int64_t g = ntiles < cap ? ntiles : cap;
+  return (unsigned)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
 template <typename T>
 void launch_trimul_prologue(const TriMulPrologueParams<T>& p, int64_t batch, hipStream_t st) {
-  dim3 grid((unsigned)((p.n + kTile - 1) / kTile), (unsigned)p.n, (unsigned)batch);
-  hipLaunchKernelGGL(trimul_prologue_kernel<T>, grid, dim3(256), 0, st, p);
+  const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
+  const void* k = reinterpret_cast<const void*>(&trimul_prologue_kernel<T>);
+  hipLaunchKernelGGL(trimul_prologue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
 }
 template <typename T>
 void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, hipStream_t st) {
-  dim3 grid((unsigned)(p.np / kTile), (unsigned)p.n, (unsigned)batch);
-  hipLaunchKernelGGL(triattn_prologue_kernel<T>, grid, dim3(256), 0, st, p);
+  const int64_t ntiles = (p.np + kTP - 1) / kTP * p.n * batch;
+  const void* k = reinterpret_cast<const void*>(&triattn_prologue_kernel<T>);
+  hipLaunchKernelGGL(triattn_prologue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
 }
 template <typename T>
-void launch_epilogue(const EpilogueParams<T>& p, bool channel_major, bool ln, int64_t batch, hipStream_t st) {
-  dim3 grid((unsigned)((p.n + kTile - 1) / kTile), (unsigned)p.n, (unsigned)batch);
-  if (channel_major && ln)
-    hipLaunchKernelGGL((rowgemm_epilogue_kernel<T, true, true>), grid, dim3(256), 0, st, p);
-  else if (!channel_major && !ln)
-    hipLaunchKernelGGL((rowgemm_epilogue_kernel<T, false, false>), grid, dim3(256), 0, st, p);
-  else if (channel_major)
-    hipLaunchKernelGGL((rowgemm_epilogue_kernel<T, true, false>), grid, dim3(256), 0, st, p);
-  else
-    hipLaunchKernelGGL((rowgemm_epilogue_kernel<T, false, true>), grid, dim3(256), 0, st, p);
+void launch_trimul_epilogue(const TriMulEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
+  const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
+  const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T>);
+  hipLaunchKernelGGL(trimul_epilogue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
+}
+template <typename T>
+void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
+  const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
+  const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T>);
+  hipLaunchKernelGGL(triattn_epilogue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
 }
 
-template void launch_trimul_prologue<float>(const TriMulPrologueParams<float>&, int64_t, hipStream_t);
-template void launch_trimul_prologue<bf16>(const TriMulPrologueParams<bf16>&, int64_t, hipStream_t);
-template void launch_triattn_prologue<float>(const TriAttnPrologueParams<float>&, int64_t, hipStream_t);
-template void launch_triattn_prologue<bf16>(const TriAttnPrologueParams<bf16>&, int64_t, hipStream_t);
-template void launch_epilogue<float>(const EpilogueParams<float>&, bool, bool, int64_t, hipStream_t);
-template void launch_epilogue<bf16>(const EpilogueParams<bf16>&, bool, bool, int64_t, hipStream_t);
+#define FJX_INST(T)                                                                                 \
+  template void launch_trimul_prologue<T>(const TriMulPrologueParams<T>&, int64_t, hipStream_t);   \
+  template void launch_triattn_prologue<T>(const TriAttnPrologueParams<T>&, int64_t, hipStream_t); \
+  template void launch_trimul_epilogue<T>(const TriMulEpilogueParams<T>&, int64_t, hipStream_t);   \
+  template void launch_triattn_epilogue<T>(const TriAttnEpilogueParams<T>&, int64_t, hipStream_t);
+FJX_INST(float)
+FJX_INST(bf16)
+#undef FJX_INST
 
 }  // namespace fjx
