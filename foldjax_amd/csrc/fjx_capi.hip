@@ -298,7 +298,6 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   fp.vt = pp.vt;
   fp.bias = pp.bias;
   fp.mb = pp.mb;
-  fp.gate = nullptr;
   fp.out = at<T>(W, ws.o);
   fp.n = n;
   fp.np = np;
@@ -359,7 +358,6 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   fp.vt = vt;
   fp.bias = bias;
   fp.mb = mb;
-  fp.gate = nullptr;
   fp.out = static_cast<T*>(a->out);
   fp.n = n;
   fp.np = np;
@@ -468,7 +466,6 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
   fp.vt = at<T>(W, ws.vt);
   fp.bias = at<T>(W, ws.bias);
   fp.mb = at<float>(W, ws.mb);
-  fp.gate = nullptr;
   fp.out = at<T>(W, ws.o);
   fp.n = n;
   fp.np = np;

@@ -20,8 +20,9 @@
 // {32c + 4g + 0..3, 32c + 16 + 4g + 0..3} -- the keys that lane already holds --
 // and the V^T fragment loaded with the same key assignment. The softmax
 // denominator is a third product with an all-ones A operand, so the running
-// sums cost MFMA cycles instead of VALU adds. Rescaling of O and of the sums
-// is skipped when no query's running max moved (a wave-uniform test).
+// sums cost MFMA cycles instead of VALU adds. The softmax offset of each query
+// is lazy: it moves (rescaling O and the sums, behind a wave-uniform test)
+// only when a block max exceeds it by more than 2^8 in probability.
 // Scores are in log2 units: q carries scale*log2(e), and the bias and mask
 // bias arrive multiplied by log2(e).
 #include <type_traits>
@@ -37,6 +38,7 @@ constexpr int kD = 32;    // head dim
 constexpr int kNumXcdF = 8;
 constexpr int kBiasLd = kKB + 4;  // padded LDS row (floats)
 constexpr int kMaxBlocks = 1024;  // key blocks per row: N <= 65536
+constexpr float kLazy = 8.0f;     // running-max slack before a rescale (log2 units)
 
 __device__ __forceinline__ int64_t xcd_remap_f(int64_t w, int64_t total) {
   const int64_t per = total / kNumXcdF;
@@ -210,15 +212,18 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 #pragma unroll
       for (int kt = 1; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
       mx = max_over_groups(mx);
-      const float mold = m[qt];
-      const float mnew = fmaxf(mold, mx);
-      if (__builtin_amdgcn_ballot_w64(mnew > mold) != 0) {
-        const float alpha = __builtin_amdgcn_exp2f(mold - mnew);
+      // lazy offset: m moves only when some query's block max exceeds it by
+      // more than kLazy (log2 units), so exp2(s - m) <= 2^kLazy and the
+      // rescale (a wave-uniform branch) is rare after the first block
+      if (__builtin_amdgcn_ballot_w64(mx > m[qt] + kLazy) != 0) {
+        const float mnew = fmaxf(m[qt], mx);
+        const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
         o[0][qt] *= alpha;
         o[1][qt] *= alpha;
         lsum[qt] *= alpha;
+        m[qt] = mnew;
       }
-      m[qt] = mnew;
+      const float mnew = m[qt];
       float pv[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
@@ -244,7 +249,6 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 
   if (!row_ok) return;
   T* OUT = P.out + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head;
-  const T* G = P.gate ? P.gate + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head : nullptr;
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
     const float inv = 1.0f / lsum[qt][0];
@@ -256,10 +260,6 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
       float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) v[r] = o[dt][qt][r] * inv;
-      if (G) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] *= to_f32(G[off + r]);
-      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) OUT[off + r] = from_f32<T>(v[r]);
     }

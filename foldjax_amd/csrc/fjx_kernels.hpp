@@ -113,7 +113,6 @@ struct FlashParams {
   const T* vt;       // [B][N][H*32][Np]
   const T* bias;     // [B][H][Np][Np], already times log2 e
   const float* mb;   // [B][N][Np], already times log2 e; -inf for padded keys
-  const T* gate;     // optional, indexed like out
   T* out;            // out[b][i][q][h*32+d] via the strides below
   int64_t n;
   int64_t np;

@@ -1,0 +1,203 @@
+// Tile building blocks shared by the 128-channel row kernels (triangle
+// prologues/epilogues, pair transition): LayerNorm of a tile held as
+// [position][channel] in LDS by quads of threads, and MFMA row tiles against
+// weight slabs held in registers.
+#pragma once
+
+#include "fjx_common.hpp"
+
+namespace fjx {
+namespace tile {
+
+constexpr int kTP = 128;     // positions per tile
+constexpr int kC = 128;      // channels
+constexpr int kLd = kC + 8;  // padded LDS row (elements)
+
+// fp32 copy of a LayerNorm affine (gamma, beta) in LDS, staged once per
+// workgroup so the per-element normalisation does no bf16 unpacking
+struct LnAffine {
+  float w[kC];
+  float b[kC];
+};
+
+template <typename T>
+__device__ __forceinline__ void stage_ln(const T* __restrict__ ln_w, const T* __restrict__ ln_b, LnAffine& l) {
+  const int t = threadIdx.x;  // >= 256 threads: 0..127 gamma, 128..255 beta
+  if (t < kC) l.w[t] = to_f32(ln_w[t]);
+  else if (t < 2 * kC) l.b[t - kC] = to_f32(ln_b[t - kC]);
+}
+
+// The 32 channels [32*part, +32) of one pair-tensor row (part = threadIdx.x % 4),
+// raw, or zeros when src is null (a position outside the grid)
+template <typename T>
+struct RowPart {
+  typename Frag<T>::type f[4];
+};
+template <typename T>
+__device__ __forceinline__ void load_row_part(const T* __restrict__ src, RowPart<T>& r) {
+  const int c0 = (threadIdx.x & 3) * 32;
+  if (src) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.f[q] = load8(src + c0 + 8 * q);
+  } else {
+    const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) r.f[q] = pack8<T>(z);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restrict__ dst_row) {
+  const int c0 = (threadIdx.x & 3) * 32;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) store8(dst_row + c0 + 8 * q, r.f[q]);
+}
+
+// LayerNorm of 128 channels held by 4 consecutive threads (32 channels each),
+// written to dst_row[32*part ..] as T
+template <typename T>
+__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, T* __restrict__ dst_row) {
+  const int c0 = (threadIdx.x & 3) * 32;
+  float v[32];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) s += v[e];
+  s += shfl_xor(s, 1);
+  s += shfl_xor(s, 2);
+  const float mean = s * (1.0f / kC);
+  float q2 = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float d = v[e] - mean;
+    q2 += d * d;
+  }
+  q2 += shfl_xor(q2, 1);
+  q2 += shfl_xor(q2, 2);
+  const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / kC) + eps);
+  const float shift = -mean * rstd;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    // one 8-channel chunk at a time: keeps the scheduler from hoisting all 16
+    // affine reads (64 VGPRs) ahead of the arithmetic
+    __builtin_amdgcn_sched_barrier(0);
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(&l.w[c0 + 8 * q]);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(&l.w[c0 + 8 * q + 4]);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(&l.b[c0 + 8 * q]);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(&l.b[c0 + 8 * q + 4]);
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = fmaf(fmaf(v[8 * q + e], rstd, shift), w0[e], b0[e]);
+      o[4 + e] = fmaf(fmaf(v[8 * q + 4 + e], rstd, shift), w1[e], b1[e]);
+    }
+    store8(dst_row + c0 + 8 * q, pack8<T>(o));
+  }
+}
+
+// One wave's 32 output channels col0..col0+31 of a [128][128] weight as MFMA
+// fragments: wf[ks][ct] holds W[col0 + 16ct + l%16][32ks + 8g .. +7].
+template <typename T>
+using WSlab = typename Frag<T>::type[4][2];
+
+template <typename T>
+__device__ __forceinline__ void load_wslab(const T* __restrict__ w, int col0, WSlab<T>& wf) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+      wf[ks][ct] = load8(w + (int64_t)(col0 + 16 * ct + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
+}
+
+// Row tile rt (tile rows 16rt..16rt+15) against one slab, K = 128:
+//   kTrans = false: acc[ct][q] = D[pos 16rt + 4g + q][ch col0 + 16ct + l%16]
+//   kTrans = true:  acc[ct][q] = D[pos 16rt + l%16][ch col0 + 16ct + 4g + q]
+template <typename T, bool kTrans>
+__device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab<T>& wf, f32x4 (&acc)[2]) {
+  const int lane = threadIdx.x & 63;
+  acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const typename Frag<T>::type xf = load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      if (kTrans) mma(acc[ct], wf[ks][ct], xf);
+      else mma(acc[ct], xf, wf[ks][ct]);
+    }
+  }
+}
+
+// the same for two slabs sharing the row fragments
+template <typename T, bool kTrans>
+__device__ __forceinline__ void tile_mma2(const T (*xs)[kLd], int rt, const WSlab<T>& w1, const WSlab<T>& w2,
+                                          f32x4 (&a1)[2], f32x4 (&a2)[2]) {
+  const int lane = threadIdx.x & 63;
+  a1[0] = a1[1] = a2[0] = a2[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const typename Frag<T>::type xf = load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      if (kTrans) {
+        mma(a1[ct], w1[ks][ct], xf);
+        mma(a2[ct], w2[ks][ct], xf);
+      } else {
+        mma(a1[ct], xf, w1[ks][ct]);
+        mma(a2[ct], xf, w2[ks][ct]);
+      }
+    }
+  }
+}
+
+// 4 elements of T packed in registers (two VGPRs for bf16)
+template <typename T> struct Vec4;
+template <> struct Vec4<bf16> { typedef bf16x4 type; };
+template <> struct Vec4<float> { typedef f32x4 type; };
+
+template <typename T>
+__device__ __forceinline__ typename Vec4<T>::type load4raw(const T* p) {
+  return *reinterpret_cast<const typename Vec4<T>::type*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void store4raw(T* p, const typename Vec4<T>::type& v) {
+  *reinterpret_cast<typename Vec4<T>::type*>(p) = v;
+}
+
+// Store 4 consecutive elements v[0..3] at dst[0..3], of which the first `cnt`
+// exist; vectorised when all 4 exist and `vec` says the address is aligned.
+template <typename T>
+__device__ __forceinline__ void store4_masked(T* dst, const float* v, int cnt, bool vec) {
+  if (cnt >= 4 && vec) {
+    store4f(dst, v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (q < cnt) dst[q] = from_f32<T>(v[q]);
+  }
+}
+
+// One 16-column tile of a weight over K = 128: wf[ks] holds
+// W[row0 + l%16][k0 + 32ks + 8g .. +7] with rows ldw elements apart.
+template <typename T>
+using WCol = typename Frag<T>::type[4];
+
+template <typename T>
+__device__ __forceinline__ void load_wcol(const T* __restrict__ w, int64_t ldw, int row0, int64_t k0, WCol<T>& wf) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) wf[ks] = load8(w + (int64_t)(row0 + (lane & 15)) * ldw + k0 + 32 * ks + 8 * (lane >> 4));
+}
+
+// acc += rows 16rt.. of the tile against one 16-column tile, transposed form:
+// acc[q] = D[pos 16rt + l%16][col 4g + q]
+template <typename T>
+__device__ __forceinline__ void tile_mma1_acc(const T (*xs)[kLd], int rt, const WCol<T>& wf, f32x4& acc) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+    mma(acc, wf[ks], load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]));
+}
+
+}  // namespace tile
+}  // namespace fjx

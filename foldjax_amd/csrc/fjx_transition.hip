@@ -9,6 +9,7 @@
 // columns. The [rows, 4C] hidden tensor never reaches HBM.
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
+#include "fjx_tile.hpp"
 
 namespace fjx {
 
@@ -164,13 +165,96 @@ __global__ __launch_bounds__(256) void transition_kernel(TransitionParams<T> P) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Pair-track transition (C = 128, hidden 512): 128-row tiles, 512 threads.
+// Wave w owns hidden columns 16w .. 16w+15 of every 128-wide hidden chunk and
+// output channels 16w .. 16w+15, so per chunk it holds just three 16-column
+// weight tiles (W_a, W_b rows of its hidden columns, W_o rows of its output
+// channels) in registers while the 8 row tiles of 16 stream past. Both
+// products use the transposed accumulator form (a lane holds 4 consecutive
+// columns of one row), so silu(a)*b and the output go out 8 bytes per lane.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> P) {
+  using namespace tile;
+  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];  // LN(x)
+  __shared__ __attribute__((aligned(16))) T hs[kTP][kLd];  // silu(a) * b, one hidden chunk
+  __shared__ __attribute__((aligned(16))) LnAffine ln;
+
+  const int64_t m0 = (int64_t)blockIdx.x * kTP;
+  const int nvalid = (int)min<int64_t>(kTP, P.rows - m0);
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int p = t >> 2;
+  const int col = 16 * wave;
+
+  {
+    RowPart<T> xr;
+    load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
+    stage_ln<T>(P.ln_w, P.ln_b, ln);
+    __syncthreads();
+    ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+  }
+  __syncthreads();
+
+  f32x4 out[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) out[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+  for (int ch = 0; ch < 4; ++ch) {
+    WCol<T> wa, wb, wo;
+    load_wcol<T>(P.w_a, kC, ch * kC + col, 0, wa);
+    load_wcol<T>(P.w_b, kC, ch * kC + col, 0, wb);
+    load_wcol<T>(P.w_o, 4 * kC, col, ch * kC, wo);
+#pragma unroll 2
+    for (int rt = 0; rt < 8; ++rt) {
+      f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = f32x4{0.f, 0.f, 0.f, 0.f};
+      tile_mma1_acc<T>(xs, rt, wa, a);
+      tile_mma1_acc<T>(xs, rt, wb, b);
+      float h[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) h[q] = silu(a[q]) * b[q];
+      store4f(&hs[16 * rt + (lane & 15)][col + 4 * (lane >> 4)], h);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) tile_mma1_acc<T>(hs, rt, wo, out[rt]);
+    __syncthreads();  // hs is rewritten by the next chunk
+  }
+
+  // the update is rounded to T (the reference's projection output is), then
+  // the residual is added
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+    const int row = 16 * rt + (lane & 15);
+    if (row < nvalid) {
+      const float m = P.row_mask ? to_f32(P.row_mask[m0 + row]) : 1.0f;
+      const int64_t off = (m0 + row) * kC + col + 4 * (lane >> 4);
+      float y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y[q] = round_to<T>(out[rt][q] * m);
+      if (P.residual) {
+        float r[4];
+        load4f(P.residual + off, r);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[q] += r[q];
+      }
+      store4f(P.out + off, y);
+    }
+  }
+}
+
 template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st) {
-  const dim3 grid((unsigned)((p.rows + kRowsT - 1) / kRowsT));
-  if (c == 128)
-    hipLaunchKernelGGL((transition_kernel<T, 128>), grid, dim3(256), 0, st, p);
-  else
+  if (c == 128) {
+    const dim3 grid((unsigned)((p.rows + tile::kTP - 1) / tile::kTP));
+    hipLaunchKernelGGL(transition128_kernel<T>, grid, dim3(512), 0, st, p);
+  } else {
+    const dim3 grid((unsigned)((p.rows + kRowsT - 1) / kRowsT));
     hipLaunchKernelGGL((transition_kernel<T, 384>), grid, dim3(256), 0, st, p);
+  }
 }
 
 template void launch_transition<bf16>(const TransitionParams<bf16>&, int, hipStream_t);
