@@ -34,10 +34,6 @@
 // Weights are PyTorch [out][in] row-major: output channel o is the contiguous
 // row W[o][0..127], which is exactly an MFMA fragment (8 contiguous k for one
 // output channel).
-#include <map>
-#include <mutex>
-#include <utility>
-
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
 #include "fjx_tile.hpp"
@@ -54,21 +50,6 @@ namespace {
 template <typename T>
 constexpr int raw_rows() {
   return sizeof(T) == 2 ? kTP : 1;
-}
-
-// tile index -> (batch, row, first column); columns fastest, then rows
-struct TileRS {
-  int b;
-  int r;
-  int s0;
-};
-__device__ __forceinline__ TileRS tile_at(int64_t tile, int64_t ntx, int64_t nrows) {
-  TileRS t;
-  t.s0 = (int)(tile % ntx) * kTP;
-  const int64_t q = tile / ntx;
-  t.r = (int)(q % nrows);
-  t.b = (int)(q / nrows);
-  return t;
 }
 
 }  // namespace
@@ -523,35 +504,6 @@ __global__ __launch_bounds__(512) void triattn_epilogue_kernel(TriAttnEpiloguePa
 // ---------------------------------------------------------------------------
 // host-side launchers
 // ---------------------------------------------------------------------------
-namespace {
-
-// Workgroups that fit on the current device at once for `kernel` (resident
-// capacity: CUs x blocks per CU), cached per (kernel, device).
-int resident_blocks(const void* kernel, int threads) {
-  static std::mutex mu;
-  static std::map<std::pair<const void*, int>, int> cache;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  std::lock_guard<std::mutex> lock(mu);
-  const auto key = std::make_pair(kernel, dev);
-  auto it = cache.find(key);
-  if (it != cache.end()) return it->second;
-  int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
-  const int v = per_cu * cus;
-  cache[key] = v;
-  return v;
-}
-
-unsigned persistent_grid(const void* kernel, int threads, int64_t ntiles) {
-  const int64_t cap = resident_blocks(kernel, threads);
-  const int64_t g = ntiles < cap ? ntiles : cap;
-  return (unsigned)(g < 1 ? 1 : g);
-}
-
-}  // namespace
-
 template <typename T>
 void launch_trimul_prologue(const TriMulPrologueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;

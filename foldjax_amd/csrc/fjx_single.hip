@@ -4,6 +4,7 @@
 // bias and the gate-and-unpad step before the output projection.
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
+#include "fjx_tile.hpp"
 
 namespace fjx {
 
@@ -72,56 +73,86 @@ __global__ void split_heads_kernel(const T* __restrict__ qkv, int64_t ld, int64_
   }
 }
 
-// bias[b][h][q][k] = log2(e) * LN(z[b,q,k,:]) . w[h,:], 128 channels, 4 threads per
-// position of the padded [np, np] grid; padded entries are written as zeros so
-// that the attention never reads uninitialised memory next to a -inf key mask
+// bias[b][h][q][k] = log2(e) * LN(z[b,q,k,:]) . w[h,:] over the padded
+// [np, np] grid, zeros outside [n, n] (the attention never reads
+// uninitialised memory next to a -inf key mask). Persistent 512-thread
+// workgroups over tiles of 128 keys of one query row: the LayerNormed tile
+// goes to LDS, wave w multiplies row tile w (16 keys) by the [heads][128]
+// weight, 16 heads per MFMA column tile, and each lane stores 4 consecutive
+// keys of one head. The next tile's z rows are loaded before the current one
+// is multiplied; the weight is held in registers when heads <= 16.
 template <typename T>
-__global__ __launch_bounds__(256) void pair_bias_kernel(const T* __restrict__ z, const T* __restrict__ ln_w,
+__global__ __launch_bounds__(512) void pair_bias_kernel(const T* __restrict__ z, const T* __restrict__ ln_w,
                                                         const T* __restrict__ ln_b, const T* __restrict__ w,
-                                                        T* __restrict__ bias, int64_t batch, int64_t n,
-                                                        int64_t np, int heads, float eps) {
-  constexpr int C = 128;
-  const int64_t ppos = (int64_t)blockIdx.x * 64 + (threadIdx.x >> 2);  // padded position
-  const int part = threadIdx.x & 3;
-  const int64_t total = batch * np * np;
-  const bool in_grid = ppos < total;
-  const int64_t b = in_grid ? ppos / (np * np) : 0;
-  const int64_t qi = in_grid ? (ppos / np) % np : 0;
-  const int64_t ki = in_grid ? ppos % np : 0;
-  const bool ok = in_grid && qi < n && ki < n;
-  const int64_t pos = (b * n + qi) * n + ki;
-  float v[32];
-  const int c0 = part * 32;
-  if (ok) {
+                                                        T* __restrict__ bias, int64_t n, int64_t np, int heads,
+                                                        float eps, int64_t ntiles) {
+  using namespace tile;
+  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
+  __shared__ __attribute__((aligned(16))) LnAffine ln;
+
+  const int64_t ntx = (np + kTP - 1) / kTP;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int p = t >> 2;
+  const int nht = (heads + 15) / 16;
+
+  auto load_heads = [&](int ht, typename Frag<T>::type (&wf)[4]) {
+    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int h = 16 * ht + li;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) to_f32x8(load8(z + pos * C + c0 + 8 * q), v + 8 * q);
-  } else {
+    for (int ks = 0; ks < 4; ++ks) wf[ks] = h < heads ? load8(w + (int64_t)h * kC + 32 * ks + 8 * lg) : pack8<T>(zero);
+  };
+  typename Frag<T>::type w0[4];
+  load_heads(0, w0);
+  stage_ln<T>(ln_w, ln_b, ln);
+
+  RowPart<T> xr;
+  auto fetch = [&](int64_t tile) {
+    const TileRS tl = tile_at(tile, ntx, np);
+    const int64_t kk = tl.s0 + p;
+    const bool valid = tl.r < n && kk < n;
+    load_row_part<T>(valid ? z + (((int64_t)tl.b * n + tl.r) * n + kk) * kC : nullptr, xr);
+  };
+
+  int64_t tile = blockIdx.x;
+  if (tile < ntiles) fetch(tile);
+  __syncthreads();
+  for (; tile < ntiles; tile += gridDim.x) {
+    const TileRS tl = tile_at(tile, ntx, np);
+    const int nstore = (int)min<int64_t>(kTP, np - tl.s0);  // a multiple of 64
+    const int nreal = tl.r < n ? (int)max<int64_t>(0, min<int64_t>(kTP, n - tl.s0)) : 0;
+    ln_quad<T>(xr, ln, eps, &xs[p][0]);
+    __syncthreads();
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
+
+    const int p0 = 16 * wave + 4 * lg;  // this lane's 4 keys within the tile
+#pragma unroll 1
+    for (int ht = 0; ht < nht; ++ht) {
+      typename Frag<T>::type wf[4];
+      if (ht == 0) {
 #pragma unroll
-    for (int e = 0; e < 32; ++e) v[e] = 0.f;
-  }
-  float s = 0.f;
+        for (int ks = 0; ks < 4; ++ks) wf[ks] = w0[ks];
+      } else {
+        load_heads(ht, wf);
+      }
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int e = 0; e < 32; ++e) s += v[e];
-  s += shfl_xor(s, 1);
-  s += shfl_xor(s, 2);
-  const float mean = s * (1.0f / C);
-  float q2 = 0.f;
+      for (int ks = 0; ks < 4; ++ks) mma(acc, load8(&xs[16 * wave + li][32 * ks + 8 * lg]), wf[ks]);
+      const int h = 16 * ht + li;
+      if (h < heads && p0 < nstore) {
+        float v[4];
 #pragma unroll
-  for (int e = 0; e < 32; ++e) q2 += (v[e] - mean) * (v[e] - mean);
-  q2 += shfl_xor(q2, 1);
-  q2 += shfl_xor(q2, 2);
-  const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / C) + eps);
-#pragma unroll
-  for (int e = 0; e < 32; ++e) v[e] = (v[e] - mean) * rstd * to_f32(ln_w[c0 + e]) + to_f32(ln_b[c0 + e]);
-  for (int h = 0; h < heads; ++h) {
-    float acc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) acc += v[e] * to_f32(w[h * C + c0 + e]);
-    acc += shfl_xor(acc, 1);
-    acc += shfl_xor(acc, 2);
-    if (in_grid && part == 0) bias[((b * heads + h) * np + qi) * np + ki] = from_f32<T>(ok ? acc * kLog2e : 0.f);
+        for (int q = 0; q < 4; ++q) v[q] = p0 + q < nreal ? acc[q] * kLog2e : 0.f;
+        store4f(bias + (((int64_t)tl.b * heads + h) * np + tl.r) * np + tl.s0 + p0, v);
+      }
+    }
+    __syncthreads();  // xs is free for the next tile
   }
 }
+
 
 // mb[b][k] = log2(e) * (1 - mask[b,k]) * (-inf_const), -inf for padded keys
 template <typename T>
@@ -177,9 +208,10 @@ void launch_split_heads(const T* qkv, int64_t ld, int64_t batch, int64_t n, int6
 template <typename T>
 void launch_pair_bias(const T* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
                       int64_t np, int heads, float eps, hipStream_t st) {
-  const int64_t total = batch * np * np;
-  hipLaunchKernelGGL(pair_bias_kernel<T>, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, st, z, ln_w, ln_b, w,
-                     bias, batch, n, np, heads, eps);
+  const int64_t ntiles = (np + tile::kTP - 1) / tile::kTP * np * batch;
+  const unsigned grid = tile::persistent_grid(reinterpret_cast<const void*>(&pair_bias_kernel<T>), 512, ntiles);
+  hipLaunchKernelGGL(pair_bias_kernel<T>, dim3(grid), dim3(512), 0, st, z, ln_w, ln_b, w, bias, n, np, heads, eps,
+                     ntiles);
 }
 template <typename T>
 void launch_key_mask(const T* mask, float* mb, int64_t batch, int64_t n, int64_t np, float inf, hipStream_t st) {

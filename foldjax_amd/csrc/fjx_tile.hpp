@@ -4,6 +4,10 @@
 // weight slabs held in registers.
 #pragma once
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 #include "fjx_common.hpp"
 
 namespace fjx {
@@ -197,6 +201,48 @@ __device__ __forceinline__ void tile_mma1_acc(const T (*xs)[kLd], int rt, const 
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks)
     mma(acc, wf[ks], load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]));
+}
+
+// tile index -> (batch, row, first column); columns fastest, then rows
+struct TileRS {
+  int b;
+  int r;
+  int s0;
+};
+__device__ __forceinline__ TileRS tile_at(int64_t tile, int64_t ntx, int64_t nrows) {
+  TileRS t;
+  t.s0 = (int)(tile % ntx) * kTP;
+  const int64_t q = tile / ntx;
+  t.r = (int)(q % nrows);
+  t.b = (int)(q / nrows);
+  return t;
+}
+
+
+// Workgroups that fit on the current device at once for `kernel` (resident
+// capacity: CUs x blocks per CU), cached per (kernel, device). Persistent
+// kernels size their grid with it.
+inline int resident_blocks(const void* kernel, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<const void*, int>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_pair(kernel, dev);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu < 1) per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+  cache[key] = per_cu * cus;
+  return per_cu * cus;
+}
+
+// grid for a persistent kernel over ntiles tiles
+inline unsigned persistent_grid(const void* kernel, int threads, int64_t ntiles) {
+  const int64_t cap = resident_blocks(kernel, threads);
+  const int64_t g = ntiles < cap ? ntiles : cap;
+  return (unsigned)(g < 1 ? 1 : g);
 }
 
 }  // namespace tile
