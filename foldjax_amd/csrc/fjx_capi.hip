@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "fjx_tri.h"
@@ -236,15 +237,21 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] { launch_trimul_prologue<T>(pp, a->batch, st); });
   if (rc) return rc;
 
-  GemmParams<T, T> cp = {};
-  cp.a = abuf;
-  cp.b = bbuf;
-  cp.c = obuf;
-  cp.m = cp.n = cp.k = a->n;
-  cp.lda = cp.ldb = cp.ldc = a->n;
-  cp.sa = cp.sb = cp.sc = a->n * a->n;
-  cp.batches = a->batch * 128;
-  rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] { launch_gemm<T, T>(cp, st); });
+  rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] {
+    if constexpr (std::is_same<T, bf16>::value) {
+      launch_contract(abuf, bbuf, obuf, a->n, a->batch * 128, st);
+    } else {
+      GemmParams<T, T> cp = {};
+      cp.a = abuf;
+      cp.b = bbuf;
+      cp.c = obuf;
+      cp.m = cp.n = cp.k = a->n;
+      cp.lda = cp.ldb = cp.ldc = a->n;
+      cp.sa = cp.sb = cp.sc = a->n * a->n;
+      cp.batches = a->batch * 128;
+      launch_gemm<T, T>(cp, st);
+    }
+  });
   if (rc) return rc;
 
   TriMulEpilogueParams<T> ep;

@@ -158,6 +158,130 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Triangle contraction, bf16: for every batch c, O[c] = A[c] B[c]^T with all
+// three n x n and k-contiguous (channel-major a and b of the tri-mul).
+// 256 x 256 output tile per 512-thread workgroup, 2 x 4 waves of 128 x 64;
+// k-tiles of 64 double-buffered in LDS with a register prefetch of the next
+// one. The accumulators are computed transposed (A operand = B rows) so each
+// lane ends up holding 4 consecutive output columns of one row.
+// ---------------------------------------------------------------------------
+constexpr int kCT = 256;
+constexpr int kCK = 64;
+constexpr int kCLd = kCK + 8;
+
+__global__ __launch_bounds__(512) void contract_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
+                                                       bf16* __restrict__ O, int64_t n, int64_t batches) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2][kCT][kCLd];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2][kCT][kCLd];
+
+  const int64_t tpd = (n + kCT - 1) / kCT;
+  const int64_t total = batches * tpd * tpd;
+  const int64_t lid = xcd_remap(blockIdx.x, total);
+  const int64_t bat = lid / (tpd * tpd);
+  const int64_t tile = lid % (tpd * tpd);
+  const int64_t m0 = (tile / tpd) * kCT;
+  const int64_t n0 = (tile % tpd) * kCT;
+  const bf16* Ab = A + bat * n * n;
+  const bf16* Bb = B + bat * n * n;
+
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int wm = (wave >> 2) * 128;
+  const int wn = (wave & 3) * 64;
+  const bool vec = (n % 8) == 0;
+
+  // global -> registers -> LDS: 256 rows x 8 chunks of 8 per operand, 4 chunks per thread
+  bf16x8 ra[4], rb[4];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int c = t + 512 * it;
+      const int row = c >> 3;
+      const int64_t gk = k0 + (c & 7) * 8;
+      const int64_t ga = m0 + row;
+      const int64_t gb = n0 + row;
+      if (vec && gk + 8 <= n) {
+        ra[it] = ga < n ? load8(Ab + ga * n + gk) : bf16x8{};
+        rb[it] = gb < n ? load8(Bb + gb * n + gk) : bf16x8{};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const bool kin = gk + e < n;
+          ra[it][e] = (kin && ga < n) ? Ab[ga * n + gk + e] : static_cast<bf16>(0.f);
+          rb[it][e] = (kin && gb < n) ? Bb[gb * n + gk + e] : static_cast<bf16>(0.f);
+        }
+      }
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const int c = t + 512 * it;
+      store8(&As[buf][c >> 3][(c & 7) * 8], ra[it]);
+      store8(&Bs[buf][c >> 3][(c & 7) * 8], rb[it]);
+    }
+  };
+
+  f32x4 acc[4][8];  // [j: 16-column tile][i: 16-row tile], transposed: lane holds C[row 16i + l%16][col 16j + 4g + q]
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t ktiles = (n + kCK - 1) / kCK;
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  for (int64_t kt = 0; kt < ktiles; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ktiles) load_stage((kt + 1) * kCK);
+#pragma unroll
+    for (int ks = 0; ks < kCK / 32; ++ks) {
+      bf16x8 af[8], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) af[i] = load8(&As[buf][wm + 16 * i + li][32 * ks + 8 * lg]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bfr[j] = load8(&Bs[buf][wn + 16 * j + li][32 * ks + 8 * lg]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) mma(acc[j][i], bfr[j], af[i]);
+    }
+    if (kt + 1 < ktiles) store_stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  bf16* Ob = O + bat * n * n;
+  const bool vec4 = (n % 4) == 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t row = m0 + wm + 16 * i + li;
+    if (row >= n) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + wn + 16 * j + 4 * lg;
+      float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
+      bf16* dst = Ob + row * n + col;
+      if (vec4 && col + 4 <= n) {
+        store4f(dst, v);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (col + q < n) dst[q] = static_cast<bf16>(v[q]);
+      }
+    }
+  }
+}
+
+void launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st) {
+  const int64_t tpd = (n + kCT - 1) / kCT;
+  hipLaunchKernelGGL(contract_kernel, dim3((unsigned)(batches * tpd * tpd)), dim3(512), 0, st, a, b, o, n, batches);
+}
+
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st) {
   const int64_t tm = (p.m + kBM - 1) / kBM;

@@ -135,6 +135,8 @@ template <typename T>
 void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st);
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st);
+// triangle contraction, bf16: o[c] = a[c] b[c]^T for c < batches, each n x n
+void launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st);
 template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st);
 
