@@ -47,6 +47,24 @@ def _args():
     return p.parse_args()
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_pairformer_block_n1024_bf16.json")
+
+
+def measured_traffic(kernel: str, n: int):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy-kernel
+    calibration), or None when that summary does not cover this kernel/N."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    if rec.get("n") != n or not k:
+        return None
+    return int(k["hbm_bytes"])
+
+
 def cpu_baseline(n_target: int, n_sample: int, budget_s: float = 25.0) -> dict:
     """Time the float64 oracle on one Pairformer layer at ``n_sample`` and
     scale to ``n_target`` by the ratio of algorithmic flops."""
@@ -182,13 +200,14 @@ def main() -> int:
     secondary = (2 * fl["trimul"] + 2 * fl["triattn"]) / (sub_t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
     block_tflops = sum(flops_block(n).values()) / (ms_step * 1e-3) / 1e12
     dom_flops = per_launch.get(dominant)
+    traffic = measured_traffic(dominant, n)
     if dom_flops is not None:
         ach = dom_flops / (kern[dominant]["avg_ms"] * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": dominant}
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "kernel": dominant}
     else:
         roof = {"bound": "hbm", "achieved": None, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": None,
-                "traffic": None, "kernel": dominant}
+                "traffic": traffic, "kernel": dominant}
 
     cpu = None
     if not a.no_cpu:
