@@ -44,13 +44,6 @@ using namespace tile;
 
 namespace {
 
-// Rows of the raw input tile kept in LDS for the residual: the whole tile for
-// bf16; fp32 tiles are twice as large, so there the residual is read from
-// global memory instead
-template <typename T>
-constexpr int raw_rows() {
-  return sizeof(T) == 2 ? kTP : 1;
-}
 
 }  // namespace
 
@@ -261,32 +254,34 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   }
 }
 
+// Epilogue tiles are 64 positions wide (256 threads, 52 KB of LDS in bf16),
+// so three workgroups share a CU and their phases interleave.
+constexpr int kTE = 64;
+
 // ---------------------------------------------------------------------------
 // Triangle multiplication epilogue, original grid (i, j):
 //   out[i,j] = LN_out(o[:, i, j]) p_out^T * T(sigmoid(LN_in(x[i,j]) g_out^T)) (+ residual)
-// with o channel-major [B][128][N*N]. 512 threads: wave w owns tile rows
-// 64(w/4) .. +63 and output channels 32(w%4) .. +31 of both products, holding
-// the g_out and p_out slabs of those channels; the two LayerNormed tiles sit
-// side by side in LDS so the gate and the projection of a row tile are
-// combined as soon as both accumulators are done.
+// with o channel-major [B][128][N*N]. 256 threads: wave w owns output channels
+// 32w .. 32w+31 of both products for the 64 positions, holding the g_out and
+// p_out slabs of those channels; the two LayerNormed tiles sit side by side
+// in LDS so the gate and the projection of a row tile combine at once.
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(512) void trimul_epilogue_kernel(TriMulEpilogueParams<T> P, int64_t ntiles) {
-  __shared__ __attribute__((aligned(16))) T xg[kTP][kLd];    // LN_in(x)
-  __shared__ __attribute__((aligned(16))) T xp[kTP][kLd];    // LN_out(o)
-  __shared__ __attribute__((aligned(16))) T xraw[raw_rows<T>()][kLd];  // x, when it is also the residual
+__global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpilogueParams<T> P, int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) T xg[kTE][kLd];    // LN_in(x)
+  __shared__ __attribute__((aligned(16))) T xp[kTE][kLd];    // LN_out(o)
+  __shared__ __attribute__((aligned(16))) T xraw[kTE][kLd];  // x, when it is also the residual
   __shared__ __attribute__((aligned(16))) LnAffine ln_in, ln_out;
 
   const int64_t n = P.n;
   const int64_t nn = n * n;
-  const int64_t ntx = (n + kTP - 1) / kTP;
+  const int64_t ntx = (n + kTE - 1) / kTE;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int row0w = 64 * (wave >> 2);
-  const int col0 = 32 * (wave & 3);
+  const int col0 = 32 * wave;
   const int p = t >> 2;  // LayerNorm position of this thread
-  const bool res_x = raw_rows<T>() == kTP && P.residual == P.x;
+  const bool res_x = P.residual == P.x;
   const bool vec8 = (n % 8) == 0;
 
   WSlab<T> wg, wp;
@@ -295,19 +290,18 @@ __global__ __launch_bounds__(512) void trimul_epilogue_kernel(TriMulEpiloguePara
   stage_ln<T>(P.ln_in_w, P.ln_in_b, ln_in);
   stage_ln<T>(P.ln_out_w, P.ln_out_b, ln_out);
 
-  // per-tile inputs: the x row of position t/4 (32 channels) and 4 chunks of
-  // the channel-major o tile (chunk it: 16 channels x 4 runs of 8 positions
-  // per wave)
+  // per-tile inputs: the x row of position t/4 and 4 chunks of the
+  // channel-major o tile (chunk it: 16 channels x 4 runs of 8 positions per wave)
   RowPart<T> xr;
   typename Frag<T>::type ot[4];
   auto o_chunk = [&](int it, int& ch, int& p0) {
-    const int grp = 8 * it + wave;  // 0..31
+    const int grp = 4 * it + wave;  // 0..15
     ch = 16 * (grp & 7) + (lane & 15);
     p0 = 8 * (4 * (grp >> 3) + (lane >> 4));
   };
   auto fetch = [&](int64_t tile) {
-    const TileRS tl = tile_at(tile, ntx, n);
-    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    const TileRS tl = tile_at(tile, ntx, n, kTE);
+    const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
     load_row_part<T>(p < nvalid ? P.x + (pos0 + p) * kC : nullptr, xr);
     const T* src = P.o + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
@@ -328,8 +322,8 @@ __global__ __launch_bounds__(512) void trimul_epilogue_kernel(TriMulEpiloguePara
   if (tile < ntiles) fetch(tile);
   __syncthreads();  // LayerNorm affines staged
   for (; tile < ntiles; tile += gridDim.x) {
-    const TileRS tl = tile_at(tile, ntx, n);
-    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    const TileRS tl = tile_at(tile, ntx, n, kTE);
+    const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
 
     if (res_x) store_row_part<T>(xr, &xraw[p][0]);
@@ -352,8 +346,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_kernel(TriMulEpiloguePara
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
 #pragma unroll 2
-    for (int k = 0; k < 4; ++k) {
-      const int rt = (row0w >> 4) + k;
+    for (int rt = 0; rt < kTE / 16; ++rt) {
       f32x4 ag[2], ap[2];
       tile_mma<T, true>(xg, rt, wg, ag);
       tile_mma<T, true>(xp, rt, wp, ap);
@@ -383,28 +376,27 @@ __global__ __launch_bounds__(512) void trimul_epilogue_kernel(TriMulEpiloguePara
 // ---------------------------------------------------------------------------
 // Triangle attention epilogue, virtual grid rows r, columns s:
 //   out[orig] = T(o[r,s] * sigmoid(LN(x[orig]) w_g^T)) w_o^T (+ residual[orig])
-// with o position-major [B][N*N][128] and orig = (r, s) or (s, r). 512
-// threads: wave w owns tile rows 64(w/4) .. +63 and output channels
-// 32(w%4) .. +31 of both products, holding the w_g and w_o slabs.
+// with o position-major [B][N*N][128] and orig = (r, s) or (s, r). 256
+// threads: wave w owns output channels 32w .. 32w+31 of both products for the
+// 64 positions, holding the w_g and w_o slabs.
 // ---------------------------------------------------------------------------
 template <typename T>
-__global__ __launch_bounds__(512) void triattn_epilogue_kernel(TriAttnEpilogueParams<T> P, int64_t ntiles) {
-  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];    // LN(x)
-  __shared__ __attribute__((aligned(16))) T xo[kTP][kLd];    // gated o
-  __shared__ __attribute__((aligned(16))) T xraw[raw_rows<T>()][kLd];  // x, when it is also the residual
+__global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpilogueParams<T> P, int64_t ntiles) {
+  __shared__ __attribute__((aligned(16))) T xs[kTE][kLd];    // LN(x)
+  __shared__ __attribute__((aligned(16))) T xo[kTE][kLd];    // gated o
+  __shared__ __attribute__((aligned(16))) T xraw[kTE][kLd];  // x, when it is also the residual
   __shared__ __attribute__((aligned(16))) LnAffine ln;
 
   const int64_t n = P.n;
   const int64_t nn = n * n;
-  const int64_t ntx = (n + kTP - 1) / kTP;
+  const int64_t ntx = (n + kTE - 1) / kTE;
   const int t = threadIdx.x;
   const int wave = t >> 6;
   const int lane = t & 63;
-  const int row0w = 64 * (wave >> 2);
-  const int col0 = 32 * (wave & 3);
+  const int col0 = 32 * wave;
   const int p = t >> 2;
   const bool gated = P.w_g != nullptr;
-  const bool res_x = raw_rows<T>() == kTP && P.residual == P.x;
+  const bool res_x = P.residual == P.x;
   const bool need_x = gated || res_x;
 
   WSlab<T> wg, wo;
@@ -421,22 +413,22 @@ __global__ __launch_bounds__(512) void triattn_epilogue_kernel(TriAttnEpiloguePa
   // for this wave's accumulator slots (position 16rt + l%16, channels
   // col0 + 16ct + 4g ..)
   RowPart<T> xr;
-  typename Vec4<T>::type ov[4][2];
+  typename Vec4<T>::type ov[kTE / 16][2];
   auto fetch = [&](int64_t tile) {
-    const TileRS tl = tile_at(tile, ntx, n);
-    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    const TileRS tl = tile_at(tile, ntx, n, kTE);
+    const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     if (need_x) load_row_part<T>(p < nvalid ? P.x + orig_of(tl, p) * kC : nullptr, xr);
     const T* osrc = P.o + ((int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0) * kC;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int pp = row0w + 16 * k + (lane & 15);
+    for (int rt = 0; rt < kTE / 16; ++rt) {
+      const int pp = 16 * rt + (lane & 15);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         if (pp < nvalid) {
-          ov[k][ct] = load4raw<T>(osrc + (int64_t)pp * kC + col0 + 16 * ct + 4 * (lane >> 4));
+          ov[rt][ct] = load4raw<T>(osrc + (int64_t)pp * kC + col0 + 16 * ct + 4 * (lane >> 4));
         } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ov[k][ct][q] = from_f32<T>(0.f);
+          for (int q = 0; q < 4; ++q) ov[rt][ct][q] = from_f32<T>(0.f);
         }
       }
     }
@@ -446,35 +438,34 @@ __global__ __launch_bounds__(512) void triattn_epilogue_kernel(TriAttnEpiloguePa
   if (tile < ntiles) fetch(tile);
   __syncthreads();
   for (; tile < ntiles; tile += gridDim.x) {
-    const TileRS tl = tile_at(tile, ntx, n);
-    const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
+    const TileRS tl = tile_at(tile, ntx, n, kTE);
+    const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
 
     if (res_x) store_row_part<T>(xr, &xraw[p][0]);
     if (gated) {
       ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
       __syncthreads();
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int rt = 0; rt < kTE / 16; ++rt) {
         f32x4 ag[2];
-        tile_mma<T, true>(xs, (row0w >> 4) + k, wg, ag);
+        tile_mma<T, true>(xs, rt, wg, ag);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ov[k][ct][q] = from_f32<T>(to_f32(ov[k][ct][q]) * fast_sigmoid(ag[ct][q]));
+          for (int q = 0; q < 4; ++q) ov[rt][ct][q] = from_f32<T>(to_f32(ov[rt][ct][q]) * fast_sigmoid(ag[ct][q]));
       }
     }
-    // gated (or raw) o -> xo; the four waves of a row half fill its 128 channels
+    // gated (or raw) o -> xo; the four waves fill its 128 channels
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int rt = 0; rt < kTE / 16; ++rt)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct)
-        store4raw<T>(&xo[row0w + 16 * k + (lane & 15)][col0 + 16 * ct + 4 * (lane >> 4)], ov[k][ct]);
+        store4raw<T>(&xo[16 * rt + (lane & 15)][col0 + 16 * ct + 4 * (lane >> 4)], ov[rt][ct]);
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
 #pragma unroll 2
-    for (int k = 0; k < 4; ++k) {
-      const int rt = (row0w >> 4) + k;
+    for (int rt = 0; rt < kTE / 16; ++rt) {
       f32x4 acc[2];
       tile_mma<T, true>(xo, rt, wo, acc);
       const int pp = 16 * rt + (lane & 15);
@@ -518,15 +509,15 @@ void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, h
 }
 template <typename T>
 void launch_trimul_epilogue(const TriMulEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
-  const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
+  const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
   const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T>);
-  hipLaunchKernelGGL(trimul_epilogue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
+  hipLaunchKernelGGL(trimul_epilogue_kernel<T>, dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p, ntiles);
 }
 template <typename T>
 void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
-  const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
+  const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
   const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T>);
-  hipLaunchKernelGGL(triattn_epilogue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
+  hipLaunchKernelGGL(triattn_epilogue_kernel<T>, dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p, ntiles);
 }
 
 #define FJX_INST(T)                                                                                 \

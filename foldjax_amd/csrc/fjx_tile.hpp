@@ -209,9 +209,9 @@ struct TileRS {
   int r;
   int s0;
 };
-__device__ __forceinline__ TileRS tile_at(int64_t tile, int64_t ntx, int64_t nrows) {
+__device__ __forceinline__ TileRS tile_at(int64_t tile, int64_t ntx, int64_t nrows, int width = kTP) {
   TileRS t;
-  t.s0 = (int)(tile % ntx) * kTP;
+  t.s0 = (int)(tile % ntx) * width;
   const int64_t q = tile / ntx;
   t.r = (int)(q % nrows);
   t.b = (int)(q / nrows);
