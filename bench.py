@@ -14,6 +14,7 @@ total time. The CPU baseline times the float64 numpy oracle (``oracle/``) on a
 bounded sample and scales it to the metric's unit.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--n N] [--no-cpu]
+    python bench.py --config trunk|long      (the N=2048 trunk / the N=3072 block)
 """
 
 from __future__ import annotations
@@ -44,6 +45,9 @@ def _args():
     p.add_argument("--cpu-n", type=int, default=256, help="size of the CPU oracle sample")
     p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "copy"],
                    help="profiling aid: run only one sublayer kind per step instead of the whole block")
+    p.add_argument("--config", default="block", choices=["block", "trunk", "long"],
+                   help="block: one layer at N=1024 (the headline line); trunk: the 48-layer trunk at N=2048 "
+                        "with an all-ones mask; long: one unchunked layer at N=3072 with 3012 real tokens")
     return p.parse_args()
 
 
@@ -112,6 +116,65 @@ def cpu_baseline(n_target: int, n_sample: int, budget_s: float = 25.0) -> dict:
     }
 
 
+def run_config(a) -> int:
+    """The other two BASELINE configurations, reported as their own JSON
+    lines: the 48-layer trunk at N=2048 (all-ones mask, each layer with its
+    own random weights) and one unchunked layer at N=3072 (3012 real tokens)."""
+    import torch
+
+    from foldjax_amd import _lib
+    from foldjax_amd import synthetic as syn
+    from foldjax_amd.pairformer import PairformerLayerWeights, flops_block
+
+    dev = torch.device("cuda:0")
+    dtype = torch.bfloat16
+    if a.config == "trunk":
+        n, n_real, layers = 2048, 2048, 48
+    else:
+        n, n_real, layers = 3072, 3012, 1
+    z0 = torch.from_numpy(syn.pair_input(n, 128, seed=0, batch=1)).to(dev, dtype)
+    s0 = torch.from_numpy(syn.single_input(n, 384, seed=1, batch=1)).to(dev, dtype)
+    tmask = torch.from_numpy(syn.token_mask(n, n_real)[None]).to(dev, dtype)
+    pmask = torch.from_numpy(syn.pair_mask(n, n_real)[None]).to(dev, dtype)
+    stack = [PairformerLayerWeights.random(dtype, dev, seed=2 + l) for l in range(layers)]
+
+    def step():
+        s, z = s0, z0
+        for layer in stack:
+            s, z = layer.forward(s, z, tmask, pmask)
+        return s, z
+
+    steps = max(1, min(a.steps, 3 if layers > 1 else a.steps))
+    for _ in range(max(1, min(a.warmup, 1))):
+        step()
+    torch.cuda.synchronize(dev)
+    _lib.prof_reset()
+    _lib.prof_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        s, z = step()
+    torch.cuda.synchronize(dev)
+    elapsed = time.perf_counter() - t0
+    _lib.prof_enable(False)
+    stats = _lib.prof_read()
+    if not (torch.isfinite(z.float()).all() and torch.isfinite(s.float()).all()):
+        print("non-finite output", file=sys.stderr)
+        return 1
+    ms = elapsed * 1e3 / steps
+    per = {k: {"avg_ms": round(v[0] / v[1], 4), "launches": v[1]} for k, v in stats.items() if v[1]}
+    fl = sum(flops_block(n).values()) * layers
+    what = "48-layer Pairformer trunk" if layers > 1 else "one Pairformer block, unchunked in HBM"
+    print(json.dumps({
+        "metric": f"ms per {what} @N={n} c_z=128 bf16",
+        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": steps, "higher_is_better": False,
+        "ms_per_block": round(ms / layers, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "dtype": "bf16",
+        "data": "synthetic: z, s ~ N(0,1), random-init weights per layer",
+        "config": {"workload": what, "n": n, "n_real": n_real, "layers": layers, "c_z": 128, "c_s": 384},
+        "kernels": per,
+    }))
+    return 0
+
+
 def main() -> int:
     a = _args()
     if a.gpus != 1:
@@ -121,6 +184,8 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if a.config != "block":
+        return run_config(a)
 
     import torch
 
