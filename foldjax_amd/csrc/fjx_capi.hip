@@ -611,7 +611,7 @@ int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
   if (a->c != 128 && a->c != 384)
     return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: this build supports c in {128, 384}, got %lld",
                 (long long)a->c);
-  if ((a->rows + 63) / 64 > 0x7fffffffLL) return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: too many rows");
+  if ((a->rows + 15) / 16 > 0x7fffffffLL) return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: too many rows");
   if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->w_a || !a->w_b || !a->w_o)
     return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a required pointer is NULL");
   return a->dtype == FJX_DTYPE_BF16 ? transition_run<bf16>(a, st) : transition_run<float>(a, st);

@@ -2,11 +2,11 @@
 // for rows of C channels with a 4C hidden width (Boltz-2 transition_forward,
 // Protenix transition, OpenFold3 swiglu_transition).
 //
-// One 256-thread workgroup owns 64 rows. The LayerNormed rows stay in LDS; the
-// hidden width is walked in chunks of 128: each wave forms 32 hidden columns
-// of a and b for all 64 rows on MFMA, writes silu(a)*b to an LDS chunk, and
-// after a barrier every wave accumulates that chunk into its C/4 output
-// columns. The [rows, 4C] hidden tensor never reaches HBM.
+// A workgroup owns a tile of rows. The LayerNormed rows stay in LDS; the
+// hidden width is walked in chunks of 128: each wave forms 16 hidden columns
+// of a and b for the tile's rows on MFMA, writes silu(a)*b to an LDS chunk,
+// and after a barrier every wave accumulates that chunk into its share of the
+// output channels. The [rows, 4C] hidden tensor never reaches HBM.
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
 #include "fjx_tile.hpp"
@@ -15,155 +15,9 @@ namespace fjx {
 
 namespace {
 
-constexpr int kRowsT = 64;
-constexpr int kHC = 128;  // hidden chunk
-
-// acc[rt][ct] += A[16rt.., k] * W[col0 + 16ct.., k]^T, k over [0, K)
-template <typename T, int K, int CT, int LDA>
-__device__ __forceinline__ void wave_gemm(const T (*a)[LDA], const T* __restrict__ w, int64_t ldw, int col0,
-                                          f32x4 (&acc)[4][CT]) {
-  const int lane = threadIdx.x & 63;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-#pragma unroll 2
-  for (int ks = 0; ks < K / 32; ++ks) {
-    typename Frag<T>::type bf[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) bf[ct] = load8(w + (int64_t)(col0 + 16 * ct + li) * ldw + 32 * ks + 8 * lg);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      const typename Frag<T>::type af = load8(&a[16 * rt + li][32 * ks + 8 * lg]);
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) mma(acc[rt][ct], af, bf[ct]);
-    }
-  }
-}
-
 __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e)); }
 
 }  // namespace
-
-template <typename T, int C>
-__global__ __launch_bounds__(256) void transition_kernel(TransitionParams<T> P) {
-  constexpr int XLD = C + 8;
-  constexpr int HLD = kHC + 8;
-  constexpr int CT = C / 64;  // 16-column output tiles per wave (C/4 columns)
-  __shared__ __attribute__((aligned(16))) T xs[kRowsT][XLD];
-  __shared__ __attribute__((aligned(16))) T hs[kRowsT][HLD];
-
-  const int64_t m0 = (int64_t)blockIdx.x * kRowsT;
-  const int nvalid = (int)min<int64_t>(kRowsT, P.rows - m0);
-  const int t = threadIdx.x;
-
-  // LayerNorm: 4 threads per row, C/4 channels each
-  {
-    constexpr int PER = C / 4;
-    const int p = t >> 2;
-    const int c0 = (t & 3) * PER;
-    float v[PER];
-    if (p < nvalid) {
-      const T* src = P.x + (m0 + p) * C + c0;
-#pragma unroll
-      for (int q = 0; q < PER / 8; ++q) to_f32x8(load8(src + 8 * q), v + 8 * q);
-    } else {
-#pragma unroll
-      for (int e = 0; e < PER; ++e) v[e] = 0.f;
-    }
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) s += v[e];
-    s += shfl_xor(s, 1);
-    s += shfl_xor(s, 2);
-    const float mean = s * (1.0f / C);
-    float q2 = 0.f;
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-      const float d = v[e] - mean;
-      q2 += d * d;
-    }
-    q2 += shfl_xor(q2, 1);
-    q2 += shfl_xor(q2, 2);
-    const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / C) + P.eps);
-#pragma unroll
-    for (int q = 0; q < PER / 8; ++q) {
-      float w[8], b[8], o[8];
-      to_f32x8(load8(P.ln_w + c0 + 8 * q), w);
-      to_f32x8(load8(P.ln_b + c0 + 8 * q), b);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (v[8 * q + e] - mean) * rstd * w[e] + b[e];
-      store8(&xs[p][c0 + 8 * q], pack8<T>(o));
-    }
-  }
-  __syncthreads();
-
-  const int wave = t >> 6;
-  const int lane = t & 63;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
-
-  f32x4 out[4][CT];
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) out[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  constexpr int NCHUNK = 4 * C / kHC;
-#pragma unroll 1
-  for (int ch = 0; ch < NCHUNK; ++ch) {
-    const int hcol0 = ch * kHC + 32 * wave;  // this wave's 32 hidden columns
-    f32x4 a[4][2], b[4][2];
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        a[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-        b[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-    wave_gemm<T, C, 2, XLD>(xs, P.w_a, C, hcol0, a);
-    wave_gemm<T, C, 2, XLD>(xs, P.w_b, C, hcol0, b);
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          hs[16 * rt + 4 * lg + q][32 * wave + 16 * ct + li] = from_f32<T>(silu(a[rt][ct][q]) * b[rt][ct][q]);
-    __syncthreads();
-    wave_gemm<T, kHC, CT, HLD>(hs, P.w_o + ch * kHC, 4 * C, wave * (C / 4), out);
-    __syncthreads();
-  }
-
-  // stage the update (rounded to T, as the reference's projection output is)
-  // in xs, then add the residual row by row with coalesced accesses
-#pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int row = 16 * rt + 4 * lg + q;
-        float y = out[rt][ct][q];
-        if (P.row_mask && row < nvalid) y *= to_f32(P.row_mask[m0 + row]);
-        xs[row][wave * (C / 4) + 16 * ct + li] = from_f32<T>(y);
-      }
-  __syncthreads();
-  constexpr int CH8 = C / 8;
-  for (int idx = t; idx < kRowsT * CH8; idx += 256) {
-    const int p = idx / CH8;
-    const int c8 = (idx % CH8) * 8;
-    if (p < nvalid) {
-      float y[8];
-      to_f32x8(load8(&xs[p][c8]), y);
-      if (P.residual) {
-        float r[8];
-        to_f32x8(load8(P.residual + (m0 + p) * C + c8), r);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] += r[e];
-      }
-      store8(P.out + (m0 + p) * C + c8, pack8<T>(y));
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Pair-track transition (C = 128, hidden 512): 128-row tiles, 512 threads.
@@ -246,14 +100,127 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Single-track transition (C = 384, hidden 1536) over few rows (one per
+// token): 16-row tiles so that even 1024 rows spread over 64 workgroups.
+// 512 threads; per 128-wide hidden chunk, wave w forms hidden columns
+// 16w .. 16w+15 (K = 384) and then adds the chunk's contribution to output
+// channels 48w .. 48w+47. All weight fragments of a chunk are requested at
+// its start, so each chunk costs about one L2 round trip.
+// ---------------------------------------------------------------------------
+constexpr int kC3 = 384;
+constexpr int kR3 = 16;
+constexpr int kLd3 = kC3 + 8;
+
+template <typename T>
+__global__ __launch_bounds__(512) void transition384_kernel(TransitionParams<T> P) {
+  using tile::kLd;
+  __shared__ __attribute__((aligned(16))) T xs[kR3][kLd3];  // LN(x)
+  __shared__ __attribute__((aligned(16))) T hs[kR3][kLd];   // silu(a) * b, one hidden chunk
+
+  const int64_t m0 = (int64_t)blockIdx.x * kR3;
+  const int nvalid = (int)min<int64_t>(kR3, P.rows - m0);
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  // LayerNorm: wave w normalises rows 2w and 2w+1, 6 channels per lane
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int r = 2 * wave + k;
+    float v[6];
+#pragma unroll
+    for (int u = 0; u < 6; ++u) v[u] = r < nvalid ? to_f32(P.x[(m0 + r) * kC3 + lane + 64 * u]) : 0.f;
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < 6; ++u) s += v[u];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += shfl_xor(s, o);
+    const float mean = s * (1.0f / kC3);
+    float q2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 6; ++u) q2 += (v[u] - mean) * (v[u] - mean);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) q2 += shfl_xor(q2, o);
+    const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / kC3) + P.eps);
+#pragma unroll
+    for (int u = 0; u < 6; ++u) {
+      const int c = lane + 64 * u;
+      xs[r][c] = from_f32<T>((v[u] - mean) * rstd * to_f32(P.ln_w[c]) + to_f32(P.ln_b[c]));
+    }
+  }
+  __syncthreads();
+
+  f32x4 out[3];
+#pragma unroll
+  for (int ct = 0; ct < 3; ++ct) out[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll 1
+  for (int ch = 0; ch < 12; ++ch) {
+    const int hc = ch * 128 + 16 * wave;  // this wave's hidden columns
+    typename Frag<T>::type wa[12], wb[12], wo[4][3];
+#pragma unroll
+    for (int ks = 0; ks < 12; ++ks) {
+      wa[ks] = load8(P.w_a + (int64_t)(hc + li) * kC3 + 32 * ks + 8 * lg);
+      wb[ks] = load8(P.w_b + (int64_t)(hc + li) * kC3 + 32 * ks + 8 * lg);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int ct = 0; ct < 3; ++ct)
+        wo[ks][ct] = load8(P.w_o + (int64_t)(48 * wave + 16 * ct + li) * (4 * kC3) + ch * 128 + 32 * ks + 8 * lg);
+    // transposed form: lane holds row l%16, hidden columns hc + 4g .. +3
+    f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 12; ++ks) {
+      const typename Frag<T>::type xf = load8(&xs[li][32 * ks + 8 * lg]);
+      mma(a, wa[ks], xf);
+      mma(b, wb[ks], xf);
+    }
+    float h[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) h[q] = silu(a[q]) * b[q];
+    store4f(&hs[li][16 * wave + 4 * lg], h);
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const typename Frag<T>::type hf = load8(&hs[li][32 * ks + 8 * lg]);
+#pragma unroll
+      for (int ct = 0; ct < 3; ++ct) mma(out[ct], wo[ks][ct], hf);
+    }
+    __syncthreads();  // hs is rewritten by the next chunk
+  }
+
+  const int row = li;
+  if (row < nvalid) {
+    const float m = P.row_mask ? to_f32(P.row_mask[m0 + row]) : 1.0f;
+#pragma unroll
+    for (int ct = 0; ct < 3; ++ct) {
+      const int64_t off = (m0 + row) * kC3 + 48 * wave + 16 * ct + 4 * lg;
+      float y[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y[q] = round_to<T>(out[ct][q] * m);
+      if (P.residual) {
+        float r[4];
+        load4f(P.residual + off, r);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) y[q] += r[q];
+      }
+      store4f(P.out + off, y);
+    }
+  }
+}
+
 template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st) {
   if (c == 128) {
     const dim3 grid((unsigned)((p.rows + tile::kTP - 1) / tile::kTP));
     hipLaunchKernelGGL(transition128_kernel<T>, grid, dim3(512), 0, st, p);
   } else {
-    const dim3 grid((unsigned)((p.rows + kRowsT - 1) / kRowsT));
-    hipLaunchKernelGGL((transition_kernel<T, 384>), grid, dim3(256), 0, st, p);
+    const dim3 grid((unsigned)((p.rows + kR3 - 1) / kR3));
+    hipLaunchKernelGGL(transition384_kernel<T>, grid, dim3(512), 0, st, p);
   }
 }
 
