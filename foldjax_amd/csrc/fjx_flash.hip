@@ -5,7 +5,15 @@
 // head and query tile, so the [64 x 64] tile of the triangle bias -- shared by
 // every row -- is staged once in LDS per key block (double-buffered, the next
 // tile prefetched into registers while the current one is consumed) and read
-// by all of them.
+// by all of them. Each row's mask bias for the block travels the same way.
+//
+// Memory pipeline per key block: at its top the wave issues the loads of the
+// next block's V (into a second register set), bias tile and mask bias; after
+// the last query tile has used K it issues the next block's K. Every prefetch
+// is unconditional (the last block re-reads itself), so no path through the
+// loop leaves a load outstanding at its top, and the in-order memory counter
+// never makes a product wait for a prefetch issued after its own operands. Q
+// lives in LDS (fragment order, conflict-free) to leave registers for V.
 //
 // Everything is computed transposed so that each lane keeps one query:
 //   S^T[key][q] = K[key][:] . Q[q][:]   (A = K fragment, B = Q fragment)
@@ -37,7 +45,6 @@ constexpr int kKB = 64;   // keys per block
 constexpr int kD = 32;    // head dim
 constexpr int kNumXcdF = 8;
 constexpr int kBiasLd = kKB + 4;  // padded LDS row (floats)
-constexpr int kMaxBlocks = 1024;  // key blocks per row: N <= 65536
 constexpr float kLazy = 8.0f;     // running-max slack before a rescale (log2 units)
 
 __device__ __forceinline__ int64_t xcd_remap_f(int64_t w, int64_t total) {
@@ -77,8 +84,10 @@ template <> __device__ __forceinline__ f32x8 ones8<float>() { return f32x8{1.f, 
 
 template <typename T, int ROWS>
 __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
+  typedef typename Frag<T>::type FragT;
   __shared__ __attribute__((aligned(16))) float bias_s[2][kQT][kBiasLd];
-  __shared__ unsigned char blk_masked[ROWS][kMaxBlocks];
+  __shared__ __attribute__((aligned(16))) FragT q_s[ROWS][4][64];  // [wave][qt][lane]: B fragments of Q
+  __shared__ __attribute__((aligned(16))) float mb_s[2][ROWS][kKB];  // each row's mask bias, one key block
 
   const int64_t n = P.n;
   const int64_t np = P.np;
@@ -111,26 +120,15 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   const float* MB = P.mb + (b * P.rows + i) * np;
   const T* BIAS = P.bias + b * P.bias_stride_b + h * np * np;
 
-  // which key blocks of this row hold a non-zero mask bias (masked or padded keys)
   const int64_t nblk = np / kKB;
-  for (int64_t blk0 = 0; blk0 < nblk; blk0 += 8) {
-    float mv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) mv[u] = blk0 + u < nblk ? MB[(blk0 + u) * kKB + lane] : 0.f;
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const bool any = __builtin_amdgcn_ballot_w64(mv[u] != 0.f) != 0;
-      if (lane == 0 && blk0 + u < nblk) blk_masked[wave][blk0 + u] = any ? 1 : 0;
-    }
-  }
 
-  typedef typename Frag<T>::type FragT;
-  FragT qf[4];
+  // Q stays in LDS (in fragment order: conflict-free 16-byte reads) and is
+  // re-read per key block, which leaves registers for a second V buffer
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) qf[qt] = load8(Q + (q0 + 16 * qt + li) * kD + 8 * lg);
-  const FragT ones = ones8<T>();
+  for (int qt = 0; qt < 4; ++qt) q_s[wave][qt][lane] = load8(Q + (q0 + 16 * qt + li) * kD + 8 * lg);
 
   float m[4];
+  const FragT ones = ones8<T>();
   f32x4 o[2][4], lsum[4];
 #pragma unroll
   for (int qt = 0; qt < 4; ++qt) {
@@ -147,10 +145,17 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   const int br = e0 / kKB;
   const int bc = e0 % kKB;
   const T* bsrc = BIAS + (q0 + br) * np + bc;
+  // the next key block's bias tile and mask bias travel in registers and are
+  // written to the other LDS buffer at the end of the current block; the
+  // mask flag (any non-zero mask bias in this row's block) is wave-uniform
   typename Frag<T>::type breg[PER / 8];
+  float mbn;
+  auto fetch_tile = [&](int64_t k0) {
 #pragma unroll
-  for (int c = 0; c < PER / 8; ++c) breg[c] = load8(bsrc + 8 * c);
-  auto put_bias = [&](int buf) {
+    for (int c = 0; c < PER / 8; ++c) breg[c] = load8(bsrc + k0 + 8 * c);
+    mbn = MB[k0 + lane];
+  };
+  auto put_tile = [&](int buf) {
 #pragma unroll
     for (int c = 0; c < PER / 8; ++c) {
       float f[8];
@@ -158,55 +163,62 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
       *reinterpret_cast<f32x4*>(&bias_s[buf][br][bc + 8 * c]) = f32x4{f[0], f[1], f[2], f[3]};
       *reinterpret_cast<f32x4*>(&bias_s[buf][br][bc + 8 * c + 4]) = f32x4{f[4], f[5], f[6], f[7]};
     }
+    mb_s[buf][wave][lane] = mbn;
+    return __builtin_amdgcn_ballot_w64(mbn != 0.f) != 0;
   };
-  put_bias(0);
+  fetch_tile(0);
+  bool masked_blk = put_tile(0);
 
   FragT kf[4];
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (16 * kt + li) * kD + 8 * lg);
-  __syncthreads();
-
-  for (int64_t blk = 0; blk < nblk; ++blk) {
-    const int buf = blk & 1;
-    const int64_t k0 = blk * kKB;
-    const bool more = blk + 1 < nblk;
-    if (more) {
-#pragma unroll
-      for (int c = 0; c < PER / 8; ++c) breg[c] = load8(bsrc + k0 + kKB + 8 * c);
-    }
-    const bool masked_blk = blk_masked[wave][blk] != 0;
-    FragT vf[2][2];  // [dt][c]
+  // V of the current block in vf, the next block's arriving in vn
+  FragT vf[2][2], vn[2][2];  // [dt][c]
+  auto load_v = [&](FragT (&v)[2][2], int64_t k0) {
 #pragma unroll
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const T* vrow = VT + (int64_t)(16 * dt + li) * np + k0 + 32 * c + 4 * lg;
-        load4_into(vrow, vf[dt][c], 0);
-        load4_into(vrow + 16, vf[dt][c], 1);
+        load4_into(vrow, v[dt][c], 0);
+        load4_into(vrow + 16, v[dt][c], 1);
       }
+  };
+  load_v(vf, 0);
+  // drain every counter once here: the loop's own waits then see nothing
+  // pending from before it (an outstanding pre-loop load would be waited on,
+  // in issue order, behind the next block's prefetch)
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
 
-    // the two instantiations differ only in adding the mask bias; branching
-    // here keeps the common all-valid block free of those adds
-    auto block_body = [&](auto masked_tag) {
-      constexpr bool kMasked = decltype(masked_tag)::value;
-      f32x4 mbv[4];
-      if (kMasked) {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) mbv[kt] = *reinterpret_cast<const f32x4*>(MB + k0 + 16 * kt + 4 * lg);
-      }
+  for (int64_t blk = 0; blk < nblk; ++blk) {
+    const int buf = blk & 1;
+    const int64_t k0 = blk * kKB;
+    // prefetches run unconditionally (the last block re-reads itself), so
+    // that no path through the loop leaves a load outstanding at its top
+    const int64_t kn = blk + 1 < nblk ? k0 + kKB : k0;
+    load_v(vn, kn);
+    fetch_tile(kn);
+
 #pragma unroll
     for (int qt = 0; qt < 4; ++qt) {
+      const FragT qf = q_s[wave][qt][lane];
       f32x4 s[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        s[kt] = *reinterpret_cast<const f32x4*>(&bias_s[buf][16 * qt + li][16 * kt + 4 * lg]);
-        if (kMasked) s[kt] += mbv[kt];
-        mma(s[kt], kf[kt], qf[qt]);
+      for (int kt = 0; kt < 4; ++kt) s[kt] = *reinterpret_cast<const f32x4*>(&bias_s[buf][16 * qt + li][16 * kt + 4 * lg]);
+      // blocks holding masked or padded keys add the mask bias (re-read per
+      // query tile, a cache hit, so that it is not live across the block);
+      // the test is wave-uniform, a scalar branch
+      if (masked_blk) {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s[kt] += *reinterpret_cast<const f32x4*>(&mb_s[buf][wave][16 * kt + 4 * lg]);
       }
-      if (qt == 3 && more) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) mma(s[kt], kf[kt], qf);
+      if (qt == 3) {
         // K of this block is consumed: fetch the next block's into the same registers
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (k0 + kKB + 16 * kt + li) * kD + 8 * lg);
+        for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (kn + 16 * kt + li) * kD + 8 * lg);
       }
       float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
 #pragma unroll
@@ -239,11 +251,12 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
         mma(lsum[qt], ones, pf);
       }
     }
-    };
-    if (masked_blk) block_body(std::true_type{});
-    else block_body(std::false_type{});
 
-    if (more) put_bias(buf ^ 1);
+    masked_blk = put_tile(buf ^ 1);
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) vf[dt][c] = vn[dt][c];
     __syncthreads();
   }
 

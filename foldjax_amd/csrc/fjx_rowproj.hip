@@ -246,7 +246,13 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = p0 + q < nreal ? ab[0][q] * kLog2e : 0.f;
-          store4f(P.bias + (((int64_t)tl.b * H + h) * np + tl.r) * np + tl.s0 + p0, v);
+          T* brow = P.bias + (((int64_t)tl.b * H + h) * np + tl.r) * np + tl.s0 + p0;
+          store4f(brow, v);
+          // the bias rows of the padded queries n .. np-1 (whose outputs are
+          // dropped) are zeroed too, so the attention never reads stale
+          // workspace memory
+          const float zero[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int64_t rz = n + tl.r; rz < np; rz += n) store4f(brow + (rz - tl.r) * np, zero);
         }
       }
     }
