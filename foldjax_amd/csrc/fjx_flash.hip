@@ -17,20 +17,22 @@
 //
 // Everything is computed transposed so that each lane keeps one query:
 //   S^T[key][q] = K[key][:] . Q[q][:]   (A = K fragment, B = Q fragment)
-//   lane l holds S^T[16kt + 4g + r][16qt + l%16], g = l/16
+//   lane l holds S^T[key_of(kt, 4g + r)][16qt + l%16], g = l/16
 // with the accumulator initialised to the bias tile (plus the mask bias when
-// the block holds masked keys). The online-softmax max lives in the lane of
-// its query; the block max needs one reduction over the 4 lane groups
-// (v_permlane16/32_swap). The probabilities feed the second product directly
-// as the B operand,
+// the block holds masked keys). The K rows of a block are loaded in a
+// permuted order (key_of below) so that lane group g ends up holding the 8
+// consecutive keys 32c + 8g .. +7 of each 32-key chunk c: the probabilities
+// then feed the second product directly as the B operand,
 //   O^T[d][q] += V^T[d][keys] . P^T[keys][q]
-// with the 8 keys of lane group g in a 32-key chunk c taken as
-// {32c + 4g + 0..3, 32c + 16 + 4g + 0..3} -- the keys that lane already holds --
-// and the V^T fragment loaded with the same key assignment. The softmax
+// and each V^T fragment is one contiguous 16-byte load (an unpermuted order
+// needs two 8-byte pieces per lane, twice the load instructions and cache-line
+// touches, and the memory pipeline bounds this kernel). The
+// online-softmax max lives in the lane of its query. The softmax
 // denominator is a third product with an all-ones A operand, so the running
 // sums cost MFMA cycles instead of VALU adds. The softmax offset of each query
 // is lazy: it moves (rescaling O and the sums, behind a wave-uniform test)
-// only when a block max exceeds it by more than 2^8 in probability.
+// only when some score of the block exceeds it by more than 2^8 in
+// probability.
 // Scores are in log2 units: q carries scale*log2(e), and the bias and mask
 // bias arrive multiplied by log2(e).
 #include <type_traits>
@@ -53,17 +55,14 @@ __device__ __forceinline__ int64_t xcd_remap_f(int64_t w, int64_t total) {
   return (w % kNumXcdF) * per + w / kNumXcdF;
 }
 
-// 4 contiguous elements into half of an 8-element fragment
-__device__ __forceinline__ void load4_into(const bf16* p, bf16x8& f, int half) {
-  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) f[4 * half + e] = v[e];
-}
-__device__ __forceinline__ void load4_into(const float* p, f32x8& f, int half) {
-  const f32x4 v = *reinterpret_cast<const f32x4*>(p);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) f[4 * half + e] = v[e];
-}
+// Key order inside a 64-key block. Row i of the K tile kt holds key
+//   key_of(kt, i) = 32 (kt/2) + 8 (i/4) + 4 (kt%2) + i%4,
+// so accumulator row 4g + r of tile kt is key 32 (kt/2) + 8g + 4 (kt%2) + r:
+// lane group g holds, for the 32-key chunk c = kt/2, the 8 consecutive keys
+// 32c + 8g .. +7 -- one contiguous 16-byte V^T fragment per lane -- and its
+// 4 bias / mask values of tile kt are 4 consecutive columns.
+__device__ __forceinline__ int key_of(int kt, int i) { return 32 * (kt >> 1) + 8 * (i >> 2) + 4 * (kt & 1) + (i & 3); }
+__device__ __forceinline__ int col_of(int kt, int g) { return 32 * (kt >> 1) + 8 * g + 4 * (kt & 1); }
 
 // max over the 4 lanes {l%16 + 16g}
 __device__ __forceinline__ float max_over_groups(float x) {
@@ -138,30 +137,32 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
     o[1][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // bias tile fill: each thread moves PER consecutive elements of one row
+  // bias tile fill: 8 threads cover one 64-key row (a whole cache line in
+  // bf16), 64*ROWS/8 rows per pass
   constexpr int NT = 64 * ROWS;
-  constexpr int PER = kQT * kKB / NT;
-  const int e0 = t * PER;
-  const int br = e0 / kKB;
-  const int bc = e0 % kKB;
+  constexpr int RPP = NT / 8;             // rows per pass
+  constexpr int PASSES = kQT / RPP;
+  static_assert(PASSES * RPP == kQT, "bias tile fill");
+  const int br = t >> 3;
+  const int bc = 8 * (t & 7);
   const T* bsrc = BIAS + (q0 + br) * np + bc;
   // the next key block's bias tile and mask bias travel in registers and are
   // written to the other LDS buffer at the end of the current block; the
   // mask flag (any non-zero mask bias in this row's block) is wave-uniform
-  typename Frag<T>::type breg[PER / 8];
+  typename Frag<T>::type breg[PASSES];
   float mbn;
   auto fetch_tile = [&](int64_t k0) {
 #pragma unroll
-    for (int c = 0; c < PER / 8; ++c) breg[c] = load8(bsrc + k0 + 8 * c);
+    for (int c = 0; c < PASSES; ++c) breg[c] = load8(bsrc + (int64_t)RPP * c * np + k0);
     mbn = MB[k0 + lane];
   };
   auto put_tile = [&](int buf) {
 #pragma unroll
-    for (int c = 0; c < PER / 8; ++c) {
+    for (int c = 0; c < PASSES; ++c) {
       float f[8];
       to_f32x8(breg[c], f);
-      *reinterpret_cast<f32x4*>(&bias_s[buf][br][bc + 8 * c]) = f32x4{f[0], f[1], f[2], f[3]};
-      *reinterpret_cast<f32x4*>(&bias_s[buf][br][bc + 8 * c + 4]) = f32x4{f[4], f[5], f[6], f[7]};
+      *reinterpret_cast<f32x4*>(&bias_s[buf][br + RPP * c][bc]) = f32x4{f[0], f[1], f[2], f[3]};
+      *reinterpret_cast<f32x4*>(&bias_s[buf][br + RPP * c][bc + 4]) = f32x4{f[4], f[5], f[6], f[7]};
     }
     mb_s[buf][wave][lane] = mbn;
     return __builtin_amdgcn_ballot_w64(mbn != 0.f) != 0;
@@ -171,7 +172,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 
   FragT kf[4];
 #pragma unroll
-  for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (16 * kt + li) * kD + 8 * lg);
+  for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + key_of(kt, li) * kD + 8 * lg);
   // V of the current block in vf, the next block's arriving in vn
   FragT vf[2][2], vn[2][2];  // [dt][c]
   auto load_v = [&](FragT (&v)[2][2], int64_t k0) {
@@ -179,9 +180,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
     for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const T* vrow = VT + (int64_t)(16 * dt + li) * np + k0 + 32 * c + 4 * lg;
-        load4_into(vrow, v[dt][c], 0);
-        load4_into(vrow + 16, v[dt][c], 1);
+        v[dt][c] = load8(VT + (int64_t)(16 * dt + li) * np + k0 + 32 * c + 8 * lg);
       }
   };
   load_v(vf, 0);
@@ -191,13 +190,14 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int64_t blk = 0; blk < nblk; ++blk) {
+  // one key block; V of this block in vc, the next block's loaded into vx
+  auto key_block = [&](int64_t blk, FragT (&vc)[2][2], FragT (&vx)[2][2]) {
     const int buf = blk & 1;
     const int64_t k0 = blk * kKB;
     // prefetches run unconditionally (the last block re-reads itself), so
     // that no path through the loop leaves a load outstanding at its top
     const int64_t kn = blk + 1 < nblk ? k0 + kKB : k0;
-    load_v(vn, kn);
+    load_v(vx, kn);
     fetch_tile(kn);
 
 #pragma unroll
@@ -205,30 +205,37 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
       const FragT qf = q_s[wave][qt][lane];
       f32x4 s[4];
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) s[kt] = *reinterpret_cast<const f32x4*>(&bias_s[buf][16 * qt + li][16 * kt + 4 * lg]);
+      for (int kt = 0; kt < 4; ++kt) s[kt] = *reinterpret_cast<const f32x4*>(&bias_s[buf][16 * qt + li][col_of(kt, lg)]);
       // blocks holding masked or padded keys add the mask bias (re-read per
       // query tile, a cache hit, so that it is not live across the block);
       // the test is wave-uniform, a scalar branch
       if (masked_blk) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s[kt] += *reinterpret_cast<const f32x4*>(&mb_s[buf][wave][16 * kt + 4 * lg]);
+        for (int kt = 0; kt < 4; ++kt) s[kt] += *reinterpret_cast<const f32x4*>(&mb_s[buf][wave][col_of(kt, lg)]);
       }
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) mma(s[kt], kf[kt], qf);
       if (qt == 3) {
         // K of this block is consumed: fetch the next block's into the same registers
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (kn + 16 * kt + li) * kD + 8 * lg);
+        for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (kn + key_of(kt, li)) * kD + 8 * lg);
       }
-      float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
-#pragma unroll
-      for (int kt = 1; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(s[kt][0], s[kt][1]), fmaxf(s[kt][2], s[kt][3])));
-      mx = max_over_groups(mx);
-      // lazy offset: m moves only when some query's block max exceeds it by
-      // more than kLazy (log2 units), so exp2(s - m) <= 2^kLazy and the
-      // rescale (a wave-uniform branch) is rare after the first block
-      if (__builtin_amdgcn_ballot_w64(mx > m[qt] + kLazy) != 0) {
-        const float mnew = fmaxf(m[qt], mx);
+      // this lane's 16 scores: a max3 tree (5 + 2 + 1)
+      const float t0 = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
+      const float t1 = fmaxf(fmaxf(s[0][3], s[1][0]), s[1][1]);
+      const float t2 = fmaxf(fmaxf(s[1][2], s[1][3]), s[2][0]);
+      const float t3 = fmaxf(fmaxf(s[2][1], s[2][2]), s[2][3]);
+      const float t4 = fmaxf(fmaxf(s[3][0], s[3][1]), s[3][2]);
+      const float u0 = fmaxf(fmaxf(t0, t1), t2);
+      const float u1 = fmaxf(fmaxf(t3, t4), s[3][3]);
+      const float lmx = fmaxf(u0, u1);
+      // lazy offset: m moves only when some score of the block exceeds it by
+      // more than kLazy (log2 units), so exp2(s - m) <= 2^kLazy; the test
+      // needs no cross-lane reduction, and the rescale (a wave-uniform
+      // branch, rare after the first block) takes the exact block max of
+      // each query over its 4 lane groups
+      if (__builtin_amdgcn_ballot_w64(lmx > m[qt] + kLazy) != 0) {
+        const float mnew = fmaxf(m[qt], max_over_groups(lmx));
         const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
         o[0][qt] *= alpha;
         o[1][qt] *= alpha;
@@ -246,18 +253,21 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
         const float f[8] = {pv[2 * c][0], pv[2 * c][1], pv[2 * c][2], pv[2 * c][3],
                             pv[2 * c + 1][0], pv[2 * c + 1][1], pv[2 * c + 1][2], pv[2 * c + 1][3]};
         const FragT pf = pack8<T>(f);
-        mma(o[0][qt], vf[0][c], pf);
-        mma(o[1][qt], vf[1][c], pf);
+        mma(o[0][qt], vc[0][c], pf);
+        mma(o[1][qt], vc[1][c], pf);
         mma(lsum[qt], ones, pf);
       }
     }
 
     masked_blk = put_tile(buf ^ 1);
-#pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-      for (int c = 0; c < 2; ++c) vf[dt][c] = vn[dt][c];
     __syncthreads();
+  };
+  // unrolled by two so that the V register sets alternate instead of being copied
+  for (int64_t blk = 0;;) {
+    key_block(blk, vf, vn);
+    if (++blk >= nblk) break;
+    key_block(blk, vn, vf);
+    if (++blk >= nblk) break;
   }
 
   if (!row_ok) return;
