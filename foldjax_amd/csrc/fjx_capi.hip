@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <mutex>
 #include <string>
+#include <initializer_list>
 #include <type_traits>
 #include <vector>
 
@@ -514,6 +515,13 @@ bool dtype_ok(int32_t dt) { return dt == FJX_DTYPE_F32 || dt == FJX_DTYPE_BF16; 
 // grid dimensions are 32-bit; y/z additionally capped at 65535
 bool grid_ok(int64_t n, int64_t batch) { return n <= 65535 && batch <= 65535; }
 
+// every kernel moves rows in 16-byte pieces; NULL (an absent optional) passes
+bool aligned16(std::initializer_list<const void*> ps) {
+  for (const void* q : ps)
+    if (reinterpret_cast<uintptr_t>(q) & 15u) return false;
+  return true;
+}
+
 }  // namespace
 
 extern "C" {
@@ -542,6 +550,9 @@ int fjx_trimul_fwd(const fjx_trimul_args* a, hipStream_t st) {
   if (!a->x || !a->out || !a->norm_in_weight || !a->norm_in_bias || !a->p_in_weight || !a->g_in_weight ||
       !a->norm_out_weight || !a->norm_out_bias || !a->p_out_weight || !a->g_out_weight)
     return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: a required pointer is NULL");
+  if (!aligned16({a->x, a->out, a->residual, a->norm_in_weight, a->norm_in_bias, a->p_in_weight, a->g_in_weight,
+                  a->norm_out_weight, a->norm_out_bias, a->p_out_weight, a->g_out_weight}))
+    return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: tensors must be 16-byte aligned");
   const size_t need = trimul_ws(a->batch, a->n, a->dtype).total;
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_trimul_fwd: workspace of %zu bytes needed, %zu given", need,
@@ -571,6 +582,9 @@ int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
   if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->bias_weight || !a->q_weight ||
       !a->k_weight || !a->v_weight || !a->o_weight)
     return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: a required pointer is NULL");
+  if (!aligned16({a->x, a->out, a->residual, a->norm_weight, a->norm_bias, a->bias_weight, a->q_weight, a->k_weight,
+                  a->v_weight, a->g_weight, a->o_weight}))
+    return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: tensors must be 16-byte aligned");
   const size_t need = triattn_ws(a->batch, a->n, a->n, a->heads, a->dtype, true).total;
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_triattn_fwd: workspace of %zu bytes needed, %zu given", need,
@@ -596,6 +610,8 @@ int fjx_triattn_core(const fjx_triattn_core_args* a, hipStream_t st) {
                 (long long)a->head_dim);
   if (!a->q || !a->k || !a->v || !a->tri_bias || !a->out)
     return fail(FJX_ERR_INVALID, "fjx_triattn_core: a required pointer is NULL");
+  if (!aligned16({a->q, a->k, a->v, a->tri_bias, a->out}))
+    return fail(FJX_ERR_INVALID, "fjx_triattn_core: tensors must be 16-byte aligned");
   const size_t need = triattn_ws(a->batch, a->rows, a->n, a->heads, a->dtype, false).total;
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_triattn_core: workspace of %zu bytes needed, %zu given", need,
@@ -614,6 +630,8 @@ int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
   if ((a->rows + 15) / 16 > 0x7fffffffLL) return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: too many rows");
   if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->w_a || !a->w_b || !a->w_o)
     return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a required pointer is NULL");
+  if (!aligned16({a->x, a->out, a->residual, a->norm_weight, a->norm_bias, a->w_a, a->w_b, a->w_o}))
+    return fail(FJX_ERR_INVALID, "fjx_transition_fwd: tensors must be 16-byte aligned");
   return a->dtype == FJX_DTYPE_BF16 ? transition_run<bf16>(a, st) : transition_run<float>(a, st);
 }
 
@@ -640,6 +658,10 @@ int fjx_single_attention_fwd(const fjx_single_attention_args* a, hipStream_t st)
       !a->z_norm_bias || !a->z_weight || !a->q_weight || !a->k_weight || !a->v_weight || !a->g_weight ||
       !a->o_weight)
     return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: a required pointer is NULL");
+  if (!aligned16({a->s, a->z, a->out, a->residual, a->pre_norm_weight, a->pre_norm_bias, a->z_norm_weight,
+                  a->z_norm_bias, a->z_weight, a->q_weight, a->q_bias, a->k_weight, a->v_weight, a->g_weight,
+                  a->o_weight}))
+    return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: tensors must be 16-byte aligned");
   const size_t need = single_ws(a->batch, a->n, a->c_s, a->heads, a->dtype).total;
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_single_attention_fwd: workspace of %zu bytes needed, %zu given", need,

@@ -291,8 +291,8 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
   const bool vec8 = (n % 8) == 0;
 
   WSlab<T> wg, wp;
-  load_wslab<T>(P.w_gout, col0, wg);
-  load_wslab<T>(P.w_pout, col0, wp);
+  load_wslab_paired<T>(P.w_gout, col0, wg);
+  load_wslab_paired<T>(P.w_pout, col0, wp);
   stage_ln<T>(P.ln_in_w, P.ln_in_b, ln_in);
   stage_ln<T>(P.ln_out_w, P.ln_out_b, ln_out);
 
@@ -356,23 +356,23 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
       f32x4 ag[2], ap[2];
       tile_mma<T, true>(xg, rt, wg, ag);
       tile_mma<T, true>(xp, rt, wp, ap);
+      // paired slabs: this lane holds channels col0 + 8g .. +7 of position pp
       const int pp = 16 * rt + (lane & 15);
       if (pp < nvalid) {
+        const int c = col0 + 8 * (lane >> 4);
+        const int64_t off = (pos0 + pp) * kC + c;
+        float y[8];
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const int c = col0 + 16 * ct + 4 * (lane >> 4);
-          const int64_t off = (pos0 + pp) * kC + c;
-          float y[4];
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) y[q] = ap[ct][q] * round_to<T>(fast_sigmoid(ag[ct][q]));
-          if (P.residual) {
-            float rv[4];
-            load4f(res_x ? &xraw[pp][c] : P.residual + off, rv);
+          for (int q = 0; q < 4; ++q) y[4 * ct + q] = ap[ct][q] * round_to<T>(fast_sigmoid(ag[ct][q]));
+        if (P.residual) {
+          float rv[8];
+          to_f32x8(load8(res_x ? &xraw[pp][c] : P.residual + off), rv);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] += rv[q];
-          }
-          store4f(P.out + off, y);
+          for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
+        store8(P.out + off, pack8<T>(y));
       }
     }
     __syncthreads();  // the LDS tiles are free for the next tile
@@ -405,9 +405,11 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
   const bool res_x = P.residual == P.x;
   const bool need_x = gated || res_x;
 
+  // paired slabs: lane group g works on the 8 consecutive channels
+  // col0 + 8g .. +7, so o, the residual and the output move 16 bytes a lane
   WSlab<T> wg, wo;
-  if (gated) load_wslab<T>(P.w_g, col0, wg);
-  load_wslab<T>(P.w_o, col0, wo);
+  if (gated) load_wslab_paired<T>(P.w_g, col0, wg);
+  load_wslab_paired<T>(P.w_o, col0, wo);
   if (gated) stage_ln<T>(P.ln_w, P.ln_b, ln);
 
   auto orig_of = [&](const TileRS& tl, int pp) -> int64_t {
@@ -417,9 +419,9 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
 
   // per-tile inputs: the x row of position t/4 (at its output position) and o
   // for this wave's accumulator slots (position 16rt + l%16, channels
-  // col0 + 16ct + 4g ..)
+  // col0 + 8g .. +7)
   RowPart<T> xr;
-  typename Vec4<T>::type ov[kTE / 16][2];
+  typename Frag<T>::type ov[kTE / 16];
   auto fetch = [&](int64_t tile) {
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
@@ -428,14 +430,11 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
 #pragma unroll
     for (int rt = 0; rt < kTE / 16; ++rt) {
       const int pp = 16 * rt + (lane & 15);
+      if (pp < nvalid) {
+        ov[rt] = load8(osrc + (int64_t)pp * kC + col0 + 8 * (lane >> 4));
+      } else {
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        if (pp < nvalid) {
-          ov[rt][ct] = load4raw<T>(osrc + (int64_t)pp * kC + col0 + 16 * ct + 4 * (lane >> 4));
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) ov[rt][ct][q] = from_f32<T>(0.f);
-        }
+        for (int e = 0; e < 8; ++e) ov[rt][e] = from_f32<T>(0.f);
       }
     }
   };
@@ -458,15 +457,13 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) ov[rt][ct][q] = from_f32<T>(to_f32(ov[rt][ct][q]) * fast_sigmoid(ag[ct][q]));
+          for (int q = 0; q < 4; ++q)
+            ov[rt][4 * ct + q] = from_f32<T>(to_f32(ov[rt][4 * ct + q]) * fast_sigmoid(ag[ct][q]));
       }
     }
     // gated (or raw) o -> xo; the four waves fill its 128 channels
 #pragma unroll
-    for (int rt = 0; rt < kTE / 16; ++rt)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
-        store4raw<T>(&xo[16 * rt + (lane & 15)][col0 + 16 * ct + 4 * (lane >> 4)], ov[rt][ct]);
+    for (int rt = 0; rt < kTE / 16; ++rt) store8(&xo[16 * rt + (lane & 15)][col0 + 8 * (lane >> 4)], ov[rt]);
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
@@ -476,22 +473,20 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
       tile_mma<T, true>(xo, rt, wo, acc);
       const int pp = 16 * rt + (lane & 15);
       if (pp < nvalid) {
-        const int64_t pos = orig_of(tl, pp);
+        const int c = col0 + 8 * (lane >> 4);
+        const int64_t off = orig_of(tl, pp) * kC + c;
+        float y[8];
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const int c = col0 + 16 * ct + 4 * (lane >> 4);
-          const int64_t off = pos * kC + c;
-          float y[4];
+        for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) y[q] = acc[ct][q];
-          if (P.residual) {
-            float rv[4];
-            load4f(res_x ? &xraw[pp][c] : P.residual + off, rv);
+          for (int q = 0; q < 4; ++q) y[4 * ct + q] = acc[ct][q];
+        if (P.residual) {
+          float rv[8];
+          to_f32x8(load8(res_x ? &xraw[pp][c] : P.residual + off), rv);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) y[q] += rv[q];
-          }
-          store4f(P.out + off, y);
+          for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
+        store8(P.out + off, pack8<T>(y));
       }
     }
     __syncthreads();  // the LDS tiles are free for the next tile

@@ -114,6 +114,21 @@ __device__ __forceinline__ void load_wslab(const T* __restrict__ w, int col0, WS
       wf[ks][ct] = load8(w + (int64_t)(col0 + 16 * ct + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
 }
 
+// The same slab with its output channels paired: row i of column tile ct is
+// channel col0 + 8 (i/4) + 4 ct + i%4, so in the transposed form lane group g
+// holds the 8 consecutive channels col0 + 8g .. +7 (acc[0] the first four,
+// acc[1] the next four) and a row goes out in one 16-byte store per lane.
+template <typename T>
+__device__ __forceinline__ void load_wslab_paired(const T* __restrict__ w, int col0, WSlab<T>& wf) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+      wf[ks][ct] = load8(w + (int64_t)(col0 + 8 * (li >> 2) + 4 * ct + (li & 3)) * kC + 32 * ks + 8 * (lane >> 4));
+}
+
 // Row tile rt (tile rows 16rt..16rt+15) against one slab, K = 128:
 //   kTrans = false: acc[ct][q] = D[pos 16rt + 4g + q][ch col0 + 16ct + l%16]
 //   kTrans = true:  acc[ct][q] = D[pos 16rt + l%16][ch col0 + 16ct + 4g + q]

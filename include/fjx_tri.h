@@ -11,6 +11,10 @@
  * Errors: every int-returning call returns FJX_OK (0) or an FJX_ERR_* code;
  * fjx_last_error() then gives a message for the calling thread.
  *
+ * Alignment: every activation, weight, output and residual pointer must be
+ * 16-byte aligned (the kernels move rows in 16-byte pieces); masks need only
+ * element alignment. A misaligned pointer is rejected with FJX_ERR_INVALID.
+ *
  * Reference interfaces replaced (paths relative to the eightmm/FoldJAX tree):
  *   fjx_trimul_fwd     cuex.triangle_multiplicative_update as called from
  *                      src/foldjax/models/boltz2/models/triangle/triangle_cueq.py:88-102

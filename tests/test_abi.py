@@ -105,6 +105,13 @@ def test_invalid_arguments_return_codes_without_launching(lib):
     assert lib.fjx_trimul_fwd(ctypes.byref(a), None) == _lib.FJX_ERR_WORKSPACE
     assert "workspace" in lib.fjx_last_error().decode()
 
+    a = _lib.TriMulArgs(batch=1, n=8, c_z=128, c_h=128, direction=0, dtype=1, eps=1e-5,
+                        x=fake + 8, norm_in_weight=fake, norm_in_bias=fake, p_in_weight=fake, g_in_weight=fake,
+                        norm_out_weight=fake, norm_out_bias=fake, p_out_weight=fake, g_out_weight=fake,
+                        out=fake, workspace=fake, workspace_bytes=16)
+    assert lib.fjx_trimul_fwd(ctypes.byref(a), None) == _lib.FJX_ERR_INVALID  # misaligned x
+    assert "16-byte aligned" in lib.fjx_last_error().decode()
+
     t = _lib.TriAttnArgs(batch=1, n=8, c_z=128, heads=8, head_dim=16, starting=1, dtype=0)
     assert lib.fjx_triattn_fwd(ctypes.byref(t), None) == _lib.FJX_ERR_UNSUPPORTED
     c = _lib.TriAttnCoreArgs(batch=1, rows=1, heads=1, n=4, head_dim=64, dtype=0)
