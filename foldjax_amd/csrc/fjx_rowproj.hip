@@ -70,7 +70,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
   const int half = wave >> 2;
   const int col0 = 32 * (wave & 3);
   const int p = t >> 2;  // LayerNorm position of this thread
-  const bool vec = (n % 4) == 0;
+  const bool vec4 = (n % 4) == 0;
+  const bool vec8 = (n % 8) == 0;
 
   WSlab<T> wp, wg;
   load_wslab<T>(P.w_p + (int64_t)half * kC * kC, col0, wp);
@@ -100,18 +101,25 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
     T* dst = (half == 0 ? P.a_cm : P.b_cm) + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
-#pragma unroll 2
-    for (int rt = 0; rt < 8; ++rt) {
-      f32x4 ap[2], ag[2];
-      tile_mma2<T, false>(xs, rt, wp, wg, ap, ag);
-      const int p0 = 16 * rt + 4 * (lane >> 4);
-      const f32x4 m = *reinterpret_cast<const f32x4*>(&mrow[p0]);
+    // row tiles in pairs with paired rows: lane group g holds positions
+    // 32j + 8g .. +7 of its channel, one 16-byte store per channel row
+#pragma unroll 1
+    for (int j = 0; j < kTP / 32; ++j) {
+      f32x4 ap[2][2], ag[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) tile_mma2_row<T, false>(xs, paired_row(j, h, lane & 15), wp, wg, ap[h], ag[h]);
+      const int p0 = 32 * j + 8 * (lane >> 4);
+      const f32x4 m0 = *reinterpret_cast<const f32x4*>(&mrow[p0]);
+      const f32x4 m1 = *reinterpret_cast<const f32x4*>(&mrow[p0 + 4]);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        float v[4];
+        float v[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = m[q] * fast_sigmoid(ag[ct][q]) * ap[ct][q];
-        store4_masked<T>(dst + (int64_t)(col0 + 16 * ct + (lane & 15)) * nn + p0, v, nvalid - p0, vec);
+        for (int q = 0; q < 4; ++q) {
+          v[q] = m0[q] * fast_sigmoid(ag[0][ct][q]) * ap[0][ct][q];
+          v[4 + q] = m1[q] * fast_sigmoid(ag[1][ct][q]) * ap[1][ct][q];
+        }
+        store8_masked<T>(dst + (int64_t)(col0 + 16 * ct + (lane & 15)) * nn + p0, v, nvalid - p0, vec8, vec4);
       }
     }
     __syncthreads();  // xs and mrow are free for the next tile
@@ -152,8 +160,9 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   //         (columns 0..3 = heads, the rest zero)
   WSlab<T> w1, w2;
   if (role == 0) {
-    load_wslab<T>(P.w_q, col0, w1);
-    load_wslab<T>(P.w_k, col0, w2);
+    // paired: lane group g holds head dims 8g .. +7, a quarter of a q/k row
+    load_wslab_paired<T>(P.w_q, col0, w1);
+    load_wslab_paired<T>(P.w_k, col0, w2);
   } else {
     load_wslab<T>(P.w_v, col0, w1);
     const int li = lane & 15;
@@ -190,8 +199,9 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
     if (role == 0) {
-      // transposed accumulators: lane (rt, ct) holds position 16rt + l%16,
-      // head dims 16ct + 4g .. +3 of head (wave & 3)
+      // transposed accumulators, paired slabs: lane (rt) holds position
+      // 16rt + l%16, head dims 8g .. +7 of head (wave & 3) -- 16 lanes cover
+      // 16 whole 64-byte q (k) rows
       const int64_t head_off = (((int64_t)tl.b * n + tl.r) * H + (wave & 3)) * np * D;
       T* qb = P.q + head_off;
       T* kb = P.k + head_off;
@@ -202,57 +212,59 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
         tile_mma2<T, true>(xs, rt, w1, w2, aq, ak);
         if (pp < nstore) {
           const bool real = pp < nreal;
+          float vq[8], vk[8];
 #pragma unroll
-          for (int ct = 0; ct < 2; ++ct) {
-            float vq[4], vk[4];
+          for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              vq[q] = real ? aq[ct][q] * P.q_scale : 0.f;
-              vk[q] = real ? ak[ct][q] : 0.f;
+              vq[4 * ct + q] = real ? aq[ct][q] * P.q_scale : 0.f;
+              vk[4 * ct + q] = real ? ak[ct][q] : 0.f;
             }
-            const int64_t off = (int64_t)(tl.s0 + pp) * D + 16 * ct + 4 * (lane >> 4);
-            store4f(qb + off, vq);
-            store4f(kb + off, vk);
-          }
+          const int64_t off = (int64_t)(tl.s0 + pp) * D + 8 * (lane >> 4);
+          store8(qb + off, pack8<T>(vq));
+          store8(kb + off, pack8<T>(vk));
         }
       }
     } else {
-      // v, channel-major: vt[b][r][ch][s]
+      // v, channel-major: vt[b][r][ch][s]; row tiles in pairs with paired
+      // rows, so lane group g holds positions 32j + 8g .. +7 of its channel
       T* vdst = P.vt + ((int64_t)tl.b * n + tl.r) * kC * np + tl.s0;
-#pragma unroll 2
-      for (int rt = 0; rt < 8; ++rt) {
-        const int p0 = 16 * rt + 4 * (lane >> 4);
-        f32x4 av[2];
-        tile_mma<T, false>(xs, rt, w1, av);
-        if (p0 < nstore) {
+#pragma unroll 1
+      for (int j = 0; j < kTP / 32; ++j) {
+        const int p0 = 32 * j + 8 * (lane >> 4);
+        f32x4 av[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) tile_mma_row<T, false>(xs, paired_row(j, h, lane & 15), w1, av[h]);
+        if (p0 < nstore) {  // nstore is a multiple of 64: all 8 positions are stored
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
-            float v[4];
+            float v[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = p0 + q < nreal ? av[ct][q] : 0.f;
-            store4f(vdst + (int64_t)(col0 + 16 * ct + (lane & 15)) * np + p0, v);
+            for (int e = 0; e < 8; ++e) v[e] = p0 + e < nreal ? av[e >> 2][ct][e & 3] : 0.f;
+            store8(vdst + (int64_t)(col0 + 16 * ct + (lane & 15)) * np + p0, pack8<T>(v));
           }
         }
       }
-      // triangle bias: lane holds D[pos 16rt + 4g + q][head l%16]
+      // triangle bias, pair j = wave & 3: lane holds positions 32j + 8g .. +7
+      // of head l%16
+      {
+        const int j = wave & 3;
+        const int p0 = 32 * j + 8 * (lane >> 4);
+        f32x4 ab[2][2];
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int rt = 2 * (wave & 3) + k;
-        const int p0 = 16 * rt + 4 * (lane >> 4);
-        f32x4 ab[2];
-        tile_mma<T, false>(xs, rt, w2, ab);
-        const int h = lane & 15;
-        if (h < H && p0 < nstore) {
-          float v[4];
+        for (int h = 0; h < 2; ++h) tile_mma_row<T, false>(xs, paired_row(j, h, lane & 15), w2, ab[h]);
+        const int hd = lane & 15;
+        if (hd < H && p0 < nstore) {
+          float v[8];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = p0 + q < nreal ? ab[0][q] * kLog2e : 0.f;
-          T* brow = P.bias + (((int64_t)tl.b * H + h) * np + tl.r) * np + tl.s0 + p0;
-          store4f(brow, v);
+          for (int e = 0; e < 8; ++e) v[e] = p0 + e < nreal ? ab[e >> 2][0][e & 3] * kLog2e : 0.f;
+          T* brow = P.bias + (((int64_t)tl.b * H + hd) * np + tl.r) * np + tl.s0 + p0;
+          store8(brow, pack8<T>(v));
           // the bias rows of the padded queries n .. np-1 (whose outputs are
           // dropped) are zeroed too, so the attention never reads stale
           // workspace memory
-          const float zero[4] = {0.f, 0.f, 0.f, 0.f};
-          for (int64_t rz = n + tl.r; rz < np; rz += n) store4f(brow + (rz - tl.r) * np, zero);
+          const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+          for (int64_t rz = n + tl.r; rz < np; rz += n) store8(brow + (rz - tl.r) * np, pack8<T>(zero));
         }
       }
     }

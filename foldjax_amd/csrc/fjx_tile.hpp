@@ -129,16 +129,17 @@ __device__ __forceinline__ void load_wslab_paired(const T* __restrict__ w, int c
       wf[ks][ct] = load8(w + (int64_t)(col0 + 8 * (li >> 2) + 4 * ct + (li & 3)) * kC + 32 * ks + 8 * (lane >> 4));
 }
 
-// Row tile rt (tile rows 16rt..16rt+15) against one slab, K = 128:
-//   kTrans = false: acc[ct][q] = D[pos 16rt + 4g + q][ch col0 + 16ct + l%16]
-//   kTrans = true:  acc[ct][q] = D[pos 16rt + l%16][ch col0 + 16ct + 4g + q]
+// One 16-row tile against one slab, K = 128; `row` is the tile row this lane
+// feeds (16rt + l%16 for row tile rt):
+//   kTrans = false: acc[ct][q] = D[row of lane 4g + q][ch col0 + 16ct + l%16]
+//   kTrans = true:  acc[ct][q] = D[row of lane l%16][ch col0 + 16ct + 4g + q]
 template <typename T, bool kTrans>
-__device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab<T>& wf, f32x4 (&acc)[2]) {
+__device__ __forceinline__ void tile_mma_row(const T (*xs)[kLd], int row, const WSlab<T>& wf, f32x4 (&acc)[2]) {
   const int lane = threadIdx.x & 63;
   acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const typename Frag<T>::type xf = load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]);
+    const typename Frag<T>::type xf = load8(&xs[row][32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       if (kTrans) mma(acc[ct], wf[ks][ct], xf);
@@ -146,16 +147,26 @@ __device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab
     }
   }
 }
+template <typename T, bool kTrans>
+__device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab<T>& wf, f32x4 (&acc)[2]) {
+  tile_mma_row<T, kTrans>(xs, 16 * rt + (threadIdx.x & 15), wf, acc);
+}
+
+// Rows of the tile pair j (rows 32j .. 32j+31) in paired order: half h of
+// the pair feeds row 32j + 8 (l%16 / 4) + 4h + l%4 from lane l, so in the
+// plain form lane group g holds rows 32j + 8g .. +7 (half 0 the first four,
+// half 1 the next four): a channel-major output goes out 16 bytes a lane.
+__device__ __forceinline__ int paired_row(int j, int h, int li) { return 32 * j + 8 * (li >> 2) + 4 * h + (li & 3); }
 
 // the same for two slabs sharing the row fragments
 template <typename T, bool kTrans>
-__device__ __forceinline__ void tile_mma2(const T (*xs)[kLd], int rt, const WSlab<T>& w1, const WSlab<T>& w2,
-                                          f32x4 (&a1)[2], f32x4 (&a2)[2]) {
+__device__ __forceinline__ void tile_mma2_row(const T (*xs)[kLd], int row, const WSlab<T>& w1, const WSlab<T>& w2,
+                                              f32x4 (&a1)[2], f32x4 (&a2)[2]) {
   const int lane = threadIdx.x & 63;
   a1[0] = a1[1] = a2[0] = a2[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const typename Frag<T>::type xf = load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]);
+    const typename Frag<T>::type xf = load8(&xs[row][32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       if (kTrans) {
@@ -167,6 +178,11 @@ __device__ __forceinline__ void tile_mma2(const T (*xs)[kLd], int rt, const WSla
       }
     }
   }
+}
+template <typename T, bool kTrans>
+__device__ __forceinline__ void tile_mma2(const T (*xs)[kLd], int rt, const WSlab<T>& w1, const WSlab<T>& w2,
+                                          f32x4 (&a1)[2], f32x4 (&a2)[2]) {
+  tile_mma2_row<T, kTrans>(xs, 16 * rt + (threadIdx.x & 15), w1, w2, a1, a2);
 }
 
 // 4 elements of T packed in registers (two VGPRs for bf16)
@@ -185,6 +201,20 @@ __device__ __forceinline__ void store4raw(T* p, const typename Vec4<T>::type& v)
 
 // Store 4 consecutive elements v[0..3] at dst[0..3], of which the first `cnt`
 // exist; vectorised when all 4 exist and `vec` says the address is aligned.
+// 8 consecutive elements: one 16-byte store when `vec8` and all are in
+// range, else two store4_masked halves (8-byte stores when `vec4`)
+template <typename T>
+__device__ __forceinline__ void store4_masked(T* dst, const float* v, int cnt, bool vec);
+template <typename T>
+__device__ __forceinline__ void store8_masked(T* dst, const float* v, int cnt, bool vec8, bool vec4) {
+  if (cnt >= 8 && vec8) {
+    store8(dst, pack8<T>(v));
+  } else {
+    store4_masked<T>(dst, v, cnt, vec4);
+    if (cnt > 4) store4_masked<T>(dst + 4, v + 4, cnt - 4, vec4);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ void store4_masked(T* dst, const float* v, int cnt, bool vec) {
   if (cnt >= 4 && vec) {
