@@ -1,8 +1,8 @@
 // Flash triangle attention on MFMA.
 //
-// One wave owns one attention row i of the pair grid and 64 queries of one
-// head; the ROWS waves of a workgroup own ROWS consecutive rows with the same
-// head and query tile, so the [64 x 64] tile of the triangle bias -- shared by
+// One wave owns one attention row i of the pair grid and 64 or 128 queries of
+// one head; the ROWS waves of a workgroup own ROWS consecutive rows with the same
+// head and query tile, so the [queries x 64] tile of the triangle bias -- shared by
 // every row -- is staged once in LDS per key block (double-buffered, the next
 // tile prefetched into registers while the current one is consumed) and read
 // by all of them. Each row's mask bias for the block travels the same way.
@@ -74,24 +74,37 @@ __device__ __forceinline__ float max_over_groups(float x) {
   return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
-template <typename T> __device__ __forceinline__ typename Frag<T>::type ones8();
-template <> __device__ __forceinline__ bf16x8 ones8<bf16>() {
-  const bf16 o = static_cast<bf16>(1.0f);
+// all eight elements 1 when `on`, else 0
+template <typename T> __device__ __forceinline__ typename Frag<T>::type ones8(bool on);
+template <> __device__ __forceinline__ bf16x8 ones8<bf16>(bool on) {
+  const bf16 o = static_cast<bf16>(on ? 1.0f : 0.0f);
   return bf16x8{o, o, o, o, o, o, o, o};
 }
-template <> __device__ __forceinline__ f32x8 ones8<float>() { return f32x8{1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f}; }
+template <> __device__ __forceinline__ f32x8 ones8<float>(bool on) {
+  const float o = on ? 1.f : 0.f;
+  return f32x8{o, o, o, o, o, o, o, o};
+}
 
-template <typename T, int ROWS>
+// NQT query tiles of 16 per wave: 4 (64 queries; Q fragments in LDS, one
+// softmax-sum accumulator per tile) or 8 (128 queries: every K and V load
+// serves twice the queries; Q in registers, and the sums of 4 tiles share an
+// accumulator whose A operand is 1 only in rows 4(qt%4) .. +3, so lane group
+// g holds the sums of tile 4(qt/4) + g -- padded queries have zero scores,
+// so the zero-weighted rows add nothing)
+template <typename T, int ROWS, int NQT>
 __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   typedef typename Frag<T>::type FragT;
-  __shared__ __attribute__((aligned(16))) float bias_s[2][kQT][kBiasLd];
-  __shared__ __attribute__((aligned(16))) FragT q_s[ROWS][4][64];  // [wave][qt][lane]: B fragments of Q
+  constexpr int QTL = 16 * NQT;
+  constexpr bool kQLds = NQT == 4;
+  constexpr int NLS = kQLds ? 4 : NQT / 4;
+  __shared__ __attribute__((aligned(16))) float bias_s[2][QTL][kBiasLd];
+  __shared__ __attribute__((aligned(16))) FragT q_s[kQLds ? ROWS : 1][4][64];  // [wave][qt][lane]: B fragments of Q
   __shared__ __attribute__((aligned(16))) float mb_s[2][ROWS][kKB];  // each row's mask bias, one key block
 
   const int64_t n = P.n;
   const int64_t np = P.np;
   const int64_t H = P.heads;
-  const int64_t QT = np / kQT;
+  const int64_t QT = np / QTL;
   const int64_t RG = (P.rows + ROWS - 1) / ROWS;
   const int64_t total = (int64_t)gridDim.x;
   int64_t lid = xcd_remap_f(blockIdx.x, total);
@@ -110,7 +123,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   const int64_t row = rg * ROWS + wave;
   const bool row_ok = row < P.rows;
   const int64_t i = row_ok ? row : P.rows - 1;
-  const int64_t q0 = qtile * kQT;
+  const int64_t q0 = qtile * QTL;
 
   const int64_t head_off = ((b * P.rows + i) * H + h) * np;  // in rows of length kD
   const T* Q = P.q + head_off * kD;
@@ -123,26 +136,32 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 
   // Q stays in LDS (in fragment order: conflict-free 16-byte reads) and is
   // re-read per key block, which leaves registers for a second V buffer
+  FragT qreg[kQLds ? 1 : NQT];
+  if constexpr (kQLds) {
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) q_s[wave][qt][lane] = load8(Q + (q0 + 16 * qt + li) * kD + 8 * lg);
+    for (int qt = 0; qt < 4; ++qt) q_s[wave][qt][lane] = load8(Q + (q0 + 16 * qt + li) * kD + 8 * lg);
+  } else {
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) qreg[qt] = load8(Q + (q0 + 16 * qt + li) * kD + 8 * lg);
+  }
 
-  float m[4];
-  const FragT ones = ones8<T>();
-  f32x4 o[2][4], lsum[4];
+  float m[NQT];
+  f32x4 o[2][NQT], lsum[NLS];
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
+  for (int qt = 0; qt < NQT; ++qt) {
     m[qt] = -1.0e30f;
-    lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     o[0][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     o[1][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+#pragma unroll
+  for (int u = 0; u < NLS; ++u) lsum[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // bias tile fill: 8 threads cover one 64-key row (a whole cache line in
   // bf16), 64*ROWS/8 rows per pass
   constexpr int NT = 64 * ROWS;
   constexpr int RPP = NT / 8;             // rows per pass
-  constexpr int PASSES = kQT / RPP;
-  static_assert(PASSES * RPP == kQT, "bias tile fill");
+  constexpr int PASSES = QTL / RPP;
+  static_assert(PASSES * RPP == QTL, "bias tile fill");
   const int br = t >> 3;
   const int bc = 8 * (t & 7);
   const T* bsrc = BIAS + (q0 + br) * np + bc;
@@ -201,8 +220,10 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
     fetch_tile(kn);
 
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-      const FragT qf = q_s[wave][qt][lane];
+    for (int qt = 0; qt < NQT; ++qt) {
+      FragT qf;
+      if constexpr (kQLds) qf = q_s[wave][qt][lane];
+      else qf = qreg[qt];
       f32x4 s[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) s[kt] = *reinterpret_cast<const f32x4*>(&bias_s[buf][16 * qt + li][col_of(kt, lg)]);
@@ -215,7 +236,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
       }
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) mma(s[kt], kf[kt], qf);
-      if (qt == 3) {
+      if (qt == NQT - 1) {
         // K of this block is consumed: fetch the next block's into the same registers
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (kn + key_of(kt, li)) * kD + 8 * lg);
@@ -239,7 +260,8 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
         const float alpha = __builtin_amdgcn_exp2f(m[qt] - mnew);
         o[0][qt] *= alpha;
         o[1][qt] *= alpha;
-        lsum[qt] *= alpha;
+        if constexpr (kQLds) lsum[qt] *= alpha;
+        else lsum[qt >> 2] *= lg == (qt & 3) ? alpha : 1.0f;
         m[qt] = mnew;
       }
       const float mnew = m[qt];
@@ -255,7 +277,8 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
         const FragT pf = pack8<T>(f);
         mma(o[0][qt], vc[0][c], pf);
         mma(o[1][qt], vc[1][c], pf);
-        mma(lsum[qt], ones, pf);
+        if constexpr (kQLds) mma(lsum[qt], ones8<T>(true), pf);
+        else mma(lsum[qt >> 2], ones8<T>((li >> 2) == (qt & 3)), pf);
       }
     }
 
@@ -273,8 +296,11 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   if (!row_ok) return;
   T* OUT = P.out + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head;
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    const float inv = 1.0f / lsum[qt][0];
+  for (int qt = 0; qt < NQT; ++qt) {
+    float ls;
+    if constexpr (kQLds) ls = lsum[qt][0];
+    else ls = __shfl(lsum[qt >> 2][0], 16 * (qt & 3) + li, 64);
+    const float inv = 1.0f / ls;
     const int64_t q = q0 + 16 * qt + li;
     if (q >= n) continue;
 #pragma unroll
@@ -290,23 +316,31 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 
 constexpr int kRows = 4;
 
+// 128 queries per wave (bf16, np a multiple of 128): 256 VGPRs, 2 waves per
+// SIMD, 72 KB of LDS (two workgroups per CU); measured a few percent faster
+// than 64 queries at 3 waves per SIMD, as each K and V load serves twice the
+// queries
+__global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_tri8_kernel_bf16(FlashParams<bf16> P) {
+  flash_tri_body<bf16, kRows, 8>(P);
+}
+
 // bf16: 3 waves per SIMD (168 VGPRs) measured faster than 2 without spills;
 // the fp32 variant would spill heavily under that cap and keeps 2.
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void flash_tri_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows>(P);
+  flash_tri_body<bf16, kRows, 4>(P);
 }
 __global__ __launch_bounds__(64 * kRows) void flash_tri_kernel_f32(FlashParams<float> P) {
-  flash_tri_body<float, kRows>(P);
+  flash_tri_body<float, kRows, 4>(P);
 }
 // the same body for the single-track attention (rows == 1), under its own
 // name so that per-kernel profiles keep the two workloads apart
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void flash_single_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows>(P);
+  flash_tri_body<bf16, kRows, 4>(P);
 }
 __global__ __launch_bounds__(64 * kRows) void flash_single_kernel_f32(FlashParams<float> P) {
-  flash_tri_body<float, kRows>(P);
+  flash_tri_body<float, kRows, 4>(P);
 }
 
 template <typename T>
@@ -314,9 +348,14 @@ void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t rg = (p.rows + kRows - 1) / kRows;
   const dim3 grid((unsigned)(batch * p.heads * rg * (p.np / kQT)));
   const bool single = p.rows == 1;
-  if constexpr (std::is_same<T, bf16>::value)
-    hipLaunchKernelGGL(single ? flash_single_kernel_bf16 : flash_tri_kernel_bf16, grid, dim3(64 * kRows), 0, st, p);
-  else
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (!single && p.np % 128 == 0) {
+      const dim3 grid8((unsigned)(batch * p.heads * rg * (p.np / 128)));
+      hipLaunchKernelGGL(flash_tri8_kernel_bf16, grid8, dim3(64 * kRows), 0, st, p);
+    } else {
+      hipLaunchKernelGGL(single ? flash_single_kernel_bf16 : flash_tri_kernel_bf16, grid, dim3(64 * kRows), 0, st, p);
+    }
+  } else
     hipLaunchKernelGGL(single ? flash_single_kernel_f32 : flash_tri_kernel_f32, grid, dim3(64 * kRows), 0, st, p);
 }
 

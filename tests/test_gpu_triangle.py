@@ -68,7 +68,8 @@ def _triattn_case(n, dt, starting, mask_kind, seed=0, heads=4):
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 @pytest.mark.parametrize("starting", [True, False])
-@pytest.mark.parametrize("n,mask_kind", [(5, "random"), (17, "ones"), (33, "tail"), (64, "random"), (100, "row0"), (130, "tail")])
+@pytest.mark.parametrize("n,mask_kind", [(5, "random"), (17, "ones"), (33, "tail"), (64, "random"), (100, "row0"), (130, "tail"),
+                                         (200, "random")])
 def test_triattn_parity(dt, starting, n, mask_kind):
     got, want, dtype, m = _triattn_case(n, dt, starting, mask_kind)
     assert np.all(np.isfinite(got)), "non-finite output (fully masked rows must stay finite)"
