@@ -191,3 +191,50 @@ def pairformer_layer_forward(
     if triangle_backend != "hip":
         raise RuntimeError(_REFERENCE_ONLY.format(kind="triangle attention", name=triangle_backend))
     return w.forward(s, z, mask, pair_mask, eps=eps)
+
+
+def pairformer_module_forward(
+    params,
+    s: torch.Tensor,
+    z: torch.Tensor,
+    mask: torch.Tensor,
+    pair_mask: torch.Tensor,
+    eps: float = 1e-5,
+    use_scan: bool = True,
+    chunk_size: int = 128,
+    triangle_attention_chunk: int | None = None,
+    triangle_attention_q_chunk: int | None = None,
+    transition_hidden_chunk: int | None = None,
+    matmul_precision: str = "highest",
+    attention_backend: str = "xla",
+    triangle_backend: str = DEFAULT_BACKEND,
+    glu_backend: str = "xla",
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Boltz-2 ``pairformer_module_forward`` (``B2K/pairformer.py:30-97``):
+    the layers of ``params["layers"]`` applied in order, each one
+    ``pairformer_layer_forward``. A layer entry is the Boltz-2 layer dict or a
+    pre-packed ``PairformerLayerWeights`` (packing once and passing the packed
+    layers avoids re-laying out the weights on every call). ``use_scan`` and
+    the chunk arguments are accepted for signature parity: the reference uses
+    them to bound XLA's memory, while every layer here streams through fused
+    kernels with a fixed workspace, so both settings run the same loop."""
+    layers = params["layers"]
+    for layer in layers:
+        s, z = pairformer_layer_forward(
+            layer,
+            s,
+            z,
+            mask,
+            pair_mask,
+            eps=eps,
+            chunk_size=chunk_size,
+            triangle_attention_chunk=triangle_attention_chunk,
+            triangle_attention_q_chunk=triangle_attention_q_chunk,
+            transition_hidden_chunk=transition_hidden_chunk,
+            matmul_precision=matmul_precision,
+            attention_backend=attention_backend,
+            triangle_backend=triangle_backend,
+            glu_backend=glu_backend,
+        )
+    return s, z
+

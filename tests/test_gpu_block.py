@@ -104,3 +104,31 @@ def test_pairformer_layer_parity(dt):
                                              device_tensor(z, dtype), device_tensor(tm, dtype),
                                              device_tensor(pm, dtype))
     assert torch.equal(ms, gs) and torch.equal(mz, gz)
+
+
+@pytest.mark.gpu
+def test_pairformer_module_two_layers():
+    """``pairformer_module_forward`` over two layers equals the oracle layer
+    applied twice (bf16), and a pre-packed stack gives identical bits."""
+    dtype = DTYPES["bf16"]
+    n, n_real = 40, 37
+    say(f"pairformer module 2 layers n={n} bf16")
+    ws_ = [syn.pairformer_layer_weights(seed=20), syn.pairformer_layer_weights(seed=40)]
+    s = syn.single_input(n, 384, seed=1, batch=1)
+    z = syn.pair_input(n, 128, seed=0, batch=1)
+    tm = syn.token_mask(n, n_real)[None]
+    pm = syn.pair_mask(n, n_real)[None]
+    params = {"layers": [P.pairformer_layer_to_boltz2(w) for w in ws_]}
+    args = (device_tensor(s, dtype), device_tensor(z, dtype), device_tensor(tm, dtype), device_tensor(pm, dtype))
+    gs, gz = boltz2.pairformer_module_forward(params, *args)
+    torch.cuda.synchronize()
+    es, ez = prep(s, dtype), prep(z, dtype)
+    for w in ws_:
+        es, ez = O.boltz2_pairformer_layer(prep_tree(w, dtype), es, ez, tm, pm)
+    v = slice(0, n_real)
+    assert_parity(to_np(gz)[:, v, v], ez[:, v, v], dtype, "module z")
+    assert_parity(to_np(gs)[:, v], es[:, v], dtype, "module s")
+    packed = {"layers": [PairformerLayerWeights.from_fields(w, dtype, "cuda") for w in ws_]}
+    ps, pz = boltz2.pairformer_module_forward(packed, *args, use_scan=False)
+    assert torch.equal(ps, gs) and torch.equal(pz, gz)
+
