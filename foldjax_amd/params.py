@@ -81,6 +81,18 @@ class OpenFold3TriangleAttentionParams(NamedTuple):
     mha: AttentionParams
 
 
+class OpenFold3PairBlockParams(NamedTuple):
+    """OpenFold3 ``PairBlockParams`` (``OF3/pair_block.py:35-46``): the
+    AF3 SwiGLU / non-fused layout. Each field is that sublayer's parameter
+    container (or a pre-packed weight object of ``foldjax_amd.kernels``)."""
+
+    tri_mul_out: object
+    tri_mul_in: object
+    tri_att_start: object
+    tri_att_end: object
+    pair_transition: object
+
+
 def _t(x) -> torch.Tensor:
     if isinstance(x, torch.Tensor):
         return x

@@ -132,3 +132,50 @@ def test_pairformer_module_two_layers():
     ps, pz = boltz2.pairformer_module_forward(packed, *args, use_scan=False)
     assert torch.equal(ps, gs) and torch.equal(pz, gz)
 
+
+def _of3_pair_block_oracle(z, p, pm, *, mask_transition, tri_mul_first):
+    """The reference's ``pair_block`` composition on the oracle, with the
+    ending node as a starting module between two transposes (as upstream)."""
+    def mul_pair(z):
+        z = z + O.openfold3_triangle_multiplication(z, p["tri_mul_out"], outgoing=True, mask=pm)
+        return z + O.openfold3_triangle_multiplication(z, p["tri_mul_in"], outgoing=False, mask=pm)
+
+    def att_pair(z):
+        z = z + O.openfold3_triangle_attention(z, p["tri_att_start"], no_heads=4, mask=pm)
+        zt = np.swapaxes(z, -2, -3)
+        zt = zt + O.openfold3_triangle_attention(zt, p["tri_att_end"], no_heads=4, mask=np.swapaxes(pm, -1, -2))
+        return np.swapaxes(zt, -2, -3)
+
+    z = att_pair(mul_pair(z)) if tri_mul_first else mul_pair(att_pair(z))
+    return z + O.transition(z, p["pair_transition"], mask=pm if mask_transition else None)
+
+
+@pytest.mark.parametrize("dt,mask_transition,tri_mul_first", [("fp32", True, True), ("bf16", True, True),
+                                                              ("fp32", False, False)])
+def test_openfold3_pair_block(dt, mask_transition, tri_mul_first):
+    dtype = DTYPES[dt]
+    n, n_real = 36, 31
+    say(f"openfold3 pair_block n={n} {dt} mask_transition={mask_transition} tri_mul_first={tri_mul_first}")
+    z = syn.pair_input(n, 128, seed=11, batch=1)
+    pm = syn.pair_mask(n, n_real)[None]
+    tw = syn.transition_weights(128, seed=16)
+    fields = {"tri_mul_out": syn.trimul_weights(seed=12), "tri_mul_in": syn.trimul_weights(seed=13),
+              "tri_att_start": syn.triattn_weights(seed=14), "tri_att_end": syn.triattn_weights(seed=15)}
+    of3 = {k: (P.trimul_to_openfold3(v) if k.startswith("tri_mul") else P.triattn_to_openfold3(v))
+           for k, v in fields.items()}
+    of3["pair_transition"] = {"layer_norm": tw["layer_norm"],
+                              "swiglu": {"linear_a": tw["linear_a"], "linear_b": tw["linear_b"]},
+                              "linear_out": tw["linear_out"]}
+    params = openfold3.PairBlockParams(**of3)
+    got = openfold3.pair_block(device_tensor(z, dtype), params, pair_mask=device_tensor(pm, dtype), no_heads_pair=4,
+                               mask_transition=mask_transition, tri_mul_first=tri_mul_first)
+    torch.cuda.synchronize()
+    ref = {k: prep_tree(v, dtype) for k, v in fields.items()}
+    for k in ("tri_att_start", "tri_att_end"):  # OpenFold3 field names of the oracle
+        ref[k] = {"layer_norm": ref[k]["layer_norm"], "linear_z": ref[k]["linear"], "mha": ref[k]["attention"]}
+    ref["pair_transition"] = prep_tree(tw, dtype)
+    want = _of3_pair_block_oracle(prep(z, dtype), ref, pm, mask_transition=mask_transition,
+                                  tri_mul_first=tri_mul_first)
+    v = slice(0, n_real)
+    assert_parity(to_np(got)[:, v, v], want[:, v, v], dtype, "openfold3 pair_block")
+
