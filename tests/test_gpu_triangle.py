@@ -39,7 +39,8 @@ def _trimul_case(n, dt, direction, mask_kind, seed=0):
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
-@pytest.mark.parametrize("n,mask_kind", [(5, "random"), (17, "ones"), (33, "tail"), (64, "random"), (100, "row0"), (130, "tail")])
+@pytest.mark.parametrize("n,mask_kind", [(5, "random"), (17, "ones"), (33, "tail"), (64, "random"), (100, "row0"), (130, "tail"),
+                                         (256, "tail")])
 def test_trimul_parity(dt, direction, n, mask_kind):
     got, want, dtype = _trimul_case(n, dt, direction, mask_kind)
     assert got.shape == want.shape
