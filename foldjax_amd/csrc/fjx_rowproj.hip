@@ -309,7 +309,9 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
   stage_ln<T>(P.ln_out_w, P.ln_out_b, ln_out);
 
   // per-tile inputs: the x row of position t/4 and 4 chunks of the
-  // channel-major o tile (chunk it: 16 channels x 4 runs of 8 positions per wave)
+  // channel-major o tile (chunk it: 16 channels x 4 runs of 8 positions per
+  // wave; measured faster than 8 lanes per channel reading whole lines,
+  // whose transposing LDS writes collide more)
   RowPart<T> xr;
   typename Frag<T>::type ot[4];
   auto o_chunk = [&](int it, int& ch, int& p0) {

@@ -37,12 +37,16 @@ template <typename T>
 struct RowPart {
   typename Frag<T>::type f[4];
 };
+// The 4 threads of a position hold interleaved 8-channel chunks: part j has
+// chunks j, 4+j, 8+j, 12+j (f[q] = channels 32q + 8j .. +7), so each of the
+// four 16-byte loads of the quad reads 64 contiguous bytes of the row.
+__device__ __forceinline__ int row_chunk(int q) { return 32 * q + 8 * (threadIdx.x & 3); }
+
 template <typename T>
 __device__ __forceinline__ void load_row_part(const T* __restrict__ src, RowPart<T>& r) {
-  const int c0 = (threadIdx.x & 3) * 32;
   if (src) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) r.f[q] = load8(src + c0 + 8 * q);
+    for (int q = 0; q < 4; ++q) r.f[q] = load8(src + row_chunk(q));
   } else {
     const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -51,16 +55,14 @@ __device__ __forceinline__ void load_row_part(const T* __restrict__ src, RowPart
 }
 template <typename T>
 __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restrict__ dst_row) {
-  const int c0 = (threadIdx.x & 3) * 32;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) store8(dst_row + c0 + 8 * q, r.f[q]);
+  for (int q = 0; q < 4; ++q) store8(dst_row + row_chunk(q), r.f[q]);
 }
 
-// LayerNorm of 128 channels held by 4 consecutive threads (32 channels each),
-// written to dst_row[32*part ..] as T
+// LayerNorm of 128 channels held by 4 consecutive threads (the chunks of
+// load_row_part), written to the same channels of dst_row as T
 template <typename T>
 __device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, T* __restrict__ dst_row) {
-  const int c0 = (threadIdx.x & 3) * 32;
   float v[32];
 #pragma unroll
   for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
@@ -85,17 +87,18 @@ __device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, 
     // one 8-channel chunk at a time: keeps the scheduler from hoisting all 16
     // affine reads (64 VGPRs) ahead of the arithmetic
     __builtin_amdgcn_sched_barrier(0);
-    const f32x4 w0 = *reinterpret_cast<const f32x4*>(&l.w[c0 + 8 * q]);
-    const f32x4 w1 = *reinterpret_cast<const f32x4*>(&l.w[c0 + 8 * q + 4]);
-    const f32x4 b0 = *reinterpret_cast<const f32x4*>(&l.b[c0 + 8 * q]);
-    const f32x4 b1 = *reinterpret_cast<const f32x4*>(&l.b[c0 + 8 * q + 4]);
+    const int c = row_chunk(q);
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(&l.w[c]);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(&l.w[c + 4]);
+    const f32x4 b0 = *reinterpret_cast<const f32x4*>(&l.b[c]);
+    const f32x4 b1 = *reinterpret_cast<const f32x4*>(&l.b[c + 4]);
     float o[8];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       o[e] = fmaf(fmaf(v[8 * q + e], rstd, shift), w0[e], b0[e]);
       o[4 + e] = fmaf(fmaf(v[8 * q + 4 + e], rstd, shift), w1[e], b1[e]);
     }
-    store8(dst_row + c0 + 8 * q, pack8<T>(o));
+    store8(dst_row + c, pack8<T>(o));
   }
 }
 
