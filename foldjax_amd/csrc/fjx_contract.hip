@@ -9,7 +9,8 @@
 // Epilogue, in order: + bias[j], sigmoid, * gate[i][j], + residual[i][j].
 //
 // Tiling: 128 x 128 output tile per 256-thread workgroup, 2 x 2 waves of
-// 64 x 64 (4 x 4 MFMA tiles of 16 x 16), k-tiles of BK staged through LDS with
+// 64 x 64 (4 x 4 MFMA tiles of 16 x 16) -- 64 x 64 tiles when the problem has
+// too few 128-tiles to occupy the GPU -- k-tiles of BK staged through LDS with
 // a register prefetch of the next k-tile. Blocks are numbered so that all
 // tiles of one batch land on one XCD (workgroups are dealt round-robin over
 // the 8 XCDs), keeping that batch's operands in the XCD's L2.
@@ -18,7 +19,6 @@
 
 namespace fjx {
 
-constexpr int kBM = 128;
 constexpr int kNumXcd = 8;
 
 template <typename T> struct GemmCfg;
@@ -33,12 +33,17 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t w, int64_t total) {
   return (w % kNumXcd) * per + w / kNumXcd;
 }
 
-template <typename T, typename TO>
+// BM x BM output tile per 256-thread workgroup (BM = 128, or 64 for small
+// problems that would otherwise leave most CUs idle), 2 x 2 waves of
+// (BM/2) x (BM/2).
+template <typename T, typename TO, int kBM>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
   constexpr int BK = GemmCfg<T>::BK;
   constexpr int LD = BK + 8;                  // padded LDS row (elements)
   constexpr int CHUNKS = kBM * BK / 8;        // 8-element chunks per operand tile
   constexpr int PER_T = CHUNKS / 256;         // chunks per thread per operand
+  constexpr int WT = kBM / 32;                // 16 x 16 MFMA tiles per wave and dimension
+  static_assert(PER_T >= 1 && PER_T * 256 == CHUNKS, "tile fill");
   __shared__ __attribute__((aligned(16))) T As[2][kBM][LD];
   __shared__ __attribute__((aligned(16))) T Bs[2][kBM][LD];
 
@@ -101,14 +106,14 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
   const int lane = t & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
-  const int wm = (wave >> 1) * 64;
-  const int wn = (wave & 1) * 64;
+  const int wm = (wave >> 1) * (kBM / 2);
+  const int wn = (wave & 1) * (kBM / 2);
 
-  f32x4 acc[4][4];
+  f32x4 acc[WT][WT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int64_t ktiles = (K + BK - 1) / BK;
   load_tile(0);
@@ -120,15 +125,15 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
     if (kt + 1 < ktiles) load_tile((kt + 1) * BK);
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
-      typename Frag<T>::type af[4], bf[4];
+      typename Frag<T>::type af[WT], bf[WT];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) af[i] = load8(&As[buf][wm + 16 * i + li][32 * ks + 8 * lg]);
+      for (int i = 0; i < WT; ++i) af[i] = load8(&As[buf][wm + 16 * i + li][32 * ks + 8 * lg]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = load8(&Bs[buf][wn + 16 * j + li][32 * ks + 8 * lg]);
+      for (int j = 0; j < WT; ++j) bf[j] = load8(&Bs[buf][wn + 16 * j + li][32 * ks + 8 * lg]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < WT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) mma(acc[i][j], af[i], bf[j]);
+        for (int j = 0; j < WT; ++j) mma(acc[i][j], af[i], bf[j]);
     }
     if (kt + 1 < ktiles) store_tile(buf ^ 1);
     __syncthreads();
@@ -138,9 +143,9 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
   const TO* G = P.gate ? P.gate + bat * P.sc : nullptr;
   const TO* R = P.residual ? P.residual + bat * P.sc : nullptr;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WT; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < WT; ++j) {
       const int64_t col = n0 + wn + 16 * j + li;
       if (col >= N) continue;
       const float bias = P.bias ? to_f32(P.bias[col]) : 0.f;
@@ -397,10 +402,12 @@ void launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t b
 
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st) {
-  const int64_t tm = (p.m + kBM - 1) / kBM;
-  const int64_t tn = (p.n + kBM - 1) / kBM;
-  const int64_t total = p.batches * tm * tn;
-  hipLaunchKernelGGL((gemm_nt_kernel<T, TO>), dim3((unsigned)total), dim3(256), 0, st, p);
+  auto tiles = [&](int64_t bm) { return p.batches * ((p.m + bm - 1) / bm) * ((p.n + bm - 1) / bm); };
+  // 128-wide tiles unless they would leave most of the 256 CUs idle
+  if (tiles(128) >= 512)
+    hipLaunchKernelGGL((gemm_nt_kernel<T, TO, 128>), dim3((unsigned)tiles(128)), dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<T, TO, 64>), dim3((unsigned)tiles(64)), dim3(256), 0, st, p);
 }
 
 template void launch_gemm<bf16, bf16>(const GemmParams<bf16, bf16>&, hipStream_t);
