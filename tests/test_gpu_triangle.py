@@ -149,6 +149,26 @@ def test_batch_axis_matches_per_item():
         torch.testing.assert_close(att[i], kernels.triattn(zb[i], mb[i], wa, starting=True), rtol=0, atol=0)
 
 
+def test_batch_axis_matches_per_item_bf16_n256():
+    """The same at a size that takes the bf16 fast paths (the LDS-DMA
+    contraction for n a multiple of 256, the 128-query attention for Np a
+    multiple of 128): a batch of 2 equals the items run alone, bit for bit."""
+    say("batch axis n=256 B=2 bf16")
+    n, dtype = 256, torch.bfloat16
+    zb = device_tensor(syn.pair_input(n, seed=21, batch=2), dtype)
+    mb = device_tensor(np.stack([mask_case(k, n) for k in ("tail", "random")]), dtype)
+    w = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(seed=22)), dtype, "cuda")
+    wa = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(seed=23)), dtype, "cuda")
+    for direction in ("outgoing", "incoming"):
+        out = kernels.trimul(zb, mb, w, direction)
+        for i in range(2):
+            torch.testing.assert_close(out[i], kernels.trimul(zb[i], mb[i], w, direction), rtol=0, atol=0)
+    for starting in (True, False):
+        att = kernels.triattn(zb, mb, wa, starting=starting)
+        for i in range(2):
+            torch.testing.assert_close(att[i], kernels.triattn(zb[i], mb[i], wa, starting=starting), rtol=0, atol=0)
+
+
 def test_mask_none_equals_all_ones():
     say("mask None n=20")
     n, dtype = 20, torch.bfloat16
