@@ -296,9 +296,12 @@ __global__ __launch_bounds__(512) void contract_kernel(const bf16* __restrict__ 
 // waits for its own DMA with an explicit vmcnt, then a bare s_barrier (a
 // fenced __syncthreads would wait for every DMA still in flight).
 // ---------------------------------------------------------------------------
-// chunk c (16 bytes) of row r of a stage with CH chunks per row
+// chunk c (16 bytes) of row r of a stage with CH chunks per row sits in
+// slot CH*r + (c ^ dma_swz<CH>(r))
 template <int CH>
-__device__ __forceinline__ int dma_slot(int r, int c) { return CH * r + (c ^ ((r / (16 / CH)) % CH)); }
+__device__ __forceinline__ int dma_swz(int r) { return (r / (16 / CH)) % CH; }
+template <int CH>
+__device__ __forceinline__ int dma_slot(int r, int c) { return CH * r + (c ^ dma_swz<CH>(r)); }
 
 template <int DS, int DK>
 __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
@@ -324,22 +327,29 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
   const int wm = (wave >> 2) * 128;
   const int wn = (wave & 3) * 64;
 
-  const bf16* src[2][NI];
+  // DMA sources: a uniform base per operand plus a 32-bit per-lane byte
+  // offset that is the same for both operands (row r of the tile, swizzled
+  // chunk c); 64-bit per-lane pointers would cost 32 VGPRs at a point where
+  // the accumulators leave none to spare
+  const char* base[2] = {reinterpret_cast<const char*>(A + (bat * n + m0) * n),
+                         reinterpret_cast<const char*>(B + (bat * n + n0) * n)};
+  uint32_t voff[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int r = 32 * wave + RPI * j + lane / CH;
-    const int c = (lane % CH) ^ ((r / (16 / CH)) % CH);
-    src[0][j] = A + bat * n * n + (m0 + r) * n + 8 * c;
-    src[1][j] = B + bat * n * n + (n0 + r) * n + 8 * c;
+    const int c = (lane % CH) ^ dma_swz<CH>(r);
+    voff[j] = (uint32_t)(r * n * 2 + 16 * c);
   }
-  auto issue = [&](int64_t kt) {
-    const int st = (int)(kt % DS);
+  // k-tile kt goes to stage kt % DS; the stage is always a compile-time
+  // constant (a run-time stage index makes the compiler wait for every DMA in
+  // flight before each LDS read)
+  auto issue = [&](int64_t kt, int st) {
     const int64_t k0 = kt * DK;
 #pragma unroll
     for (int op = 0; op < 2; ++op)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src[op][j] + k0),
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base[op] + 2 * k0 + voff[j]),
                                          reinterpret_cast<void*>(&S[st][op][(32 * wave + RPI * j) * DK]), 16, 0, 0);
   };
 
@@ -349,31 +359,39 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t ktiles = n / DK;
+  const int64_t ktiles = n / DK;  // a multiple of DS (checked by the launcher)
 #pragma unroll
-  for (int s0 = 0; s0 < DS - 1; ++s0) issue(s0);
-  for (int64_t kt = 0; kt < ktiles; ++kt) {
-    const int64_t later = min<int64_t>(DS - 2, ktiles - 1 - kt);
-    if (DS >= 4 && later >= 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * 2 * NI));
-    else if (DS >= 3 && later >= 1) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * NI));
-    else __builtin_amdgcn_s_waitcnt(0xF70);
-    __builtin_amdgcn_s_barrier();
-    if (kt + DS - 1 < ktiles) issue(kt + DS - 1);
-    const bf16* As_ = &S[kt % DS][0][0];
-    const bf16* Bs_ = &S[kt % DS][1][0];
+  for (int s0 = 0; s0 < DS - 1; ++s0) issue(s0, s0);
+  for (int64_t kb = 0; kb < ktiles; kb += DS) {
 #pragma unroll
-    for (int ks = 0; ks < DK / 32; ++ks) {
-      bf16x8 af[8], bfr[4];
+    for (int st = 0; st < DS; ++st) {
+      const int64_t kt = kb + st;
+      // opaque per iteration: keeps the compiler from hoisting base + voff
+      // into eight loop-invariant 64-bit pointers (it then spills them)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * dma_slot<CH>(wm + 16 * i + li, 4 * ks + lg));
+      for (int j = 0; j < NI; ++j) asm volatile("" : "+v"(voff[j]));
+      const int64_t later = min<int64_t>(DS - 2, ktiles - 1 - kt);
+      if (DS >= 4 && later >= 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * 2 * NI));
+      else if (DS >= 3 && later >= 1) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * NI));
+      else __builtin_amdgcn_s_waitcnt(0xF70);
+      __builtin_amdgcn_s_barrier();
+      if (kt + DS - 1 < ktiles) issue(kt + DS - 1, (st + DS - 1) % DS);
+      const bf16* As_ = &S[st][0][0];
+      const bf16* Bs_ = &S[st][1][0];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * dma_slot<CH>(wn + 16 * j + li, 4 * ks + lg));
+      for (int ks = 0; ks < DK / 32; ++ks) {
+        bf16x8 af[8], bfr[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int i = 0; i < 8; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * dma_slot<CH>(wm + 16 * i + li, 4 * ks + lg));
 #pragma unroll
-        for (int i = 0; i < 8; ++i) mma(acc[j][i], bfr[j], af[i]);
+        for (int j = 0; j < 4; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * dma_slot<CH>(wn + 16 * j + li, 4 * ks + lg));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) mma(acc[j][i], bfr[j], af[i]);
+      }
     }
   }
 
