@@ -193,6 +193,44 @@ def pairformer_layer_forward(
     return w.forward(s, z, mask, pair_mask, eps=eps)
 
 
+def pairformer_no_seq_layer_forward(
+    params,
+    z: torch.Tensor,
+    pair_mask: torch.Tensor,
+    eps: float = 1e-5,
+    chunk_size: int = 128,
+    triangle_attention_chunk: int | None = None,
+    triangle_attention_q_chunk: int | None = None,
+    transition_hidden_chunk: int | None = None,
+    matmul_precision: str = "highest",
+    triangle_backend: str = DEFAULT_BACKEND,
+    glu_backend: str = "xla",
+) -> torch.Tensor:
+    """Boltz-2 ``pairformer_no_seq_layer_forward`` (``B2K/msa.py:467-539``),
+    the MSA module's pair block: z += tri-mul outgoing, incoming, tri-attn
+    starting, ending (all with ``pair_mask``) and the unmasked pair
+    transition, each residual fused into its kernel. ``params`` is the
+    Boltz-2 dict with ``tri_mul_out``, ``tri_mul_in``, ``tri_att_start``,
+    ``tri_att_end`` and ``transition_z``; the chunk arguments are accepted for
+    signature parity (the kernels stream with a fixed workspace)."""
+    from foldjax_amd.pairformer import TriangleSublayers
+
+    resolve_matmul_precision(matmul_precision)
+    if triangle_backend not in ("xla", "pallas", "tokamax", "cueq", "hip"):
+        raise ValueError(f"Unsupported triangle_backend: {triangle_backend!r}")
+    if triangle_backend != "hip":
+        raise RuntimeError(_REFERENCE_ONLY.format(kind="triangle attention", name=triangle_backend))
+    dt, dev = z.dtype, z.device
+    tri = TriangleSublayers(
+        pack_trimul_boltz2(params["tri_mul_out"], dt, dev),
+        pack_trimul_boltz2(params["tri_mul_in"], dt, dev),
+        pack_triattn_boltz2(params["tri_att_start"], dt, dev),
+        pack_triattn_boltz2(params["tri_att_end"], dt, dev),
+    )
+    z = tri.forward(z, pair_mask)
+    return kernels.transition(z, pack_transition_boltz2(params["transition_z"], dt, dev), residual=z, eps=eps)
+
+
 def pairformer_module_forward(
     params,
     s: torch.Tensor,

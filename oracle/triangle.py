@@ -449,6 +449,20 @@ def boltz2_attention_pair_bias(p, s, z, mask, *, inf=1e6, eps=1e-5):
     return linear_torch(g * o, {"weight": p["proj_o"]["weight"]})
 
 
+def boltz2_pairformer_no_seq_layer(p, z, pair_mask, *, eps=1e-5):
+    """The pair half of a Boltz-2 layer, which is also the MSA module's
+    ``pairformer_no_seq_layer_forward`` (``B2K/msa.py:467-539``): z +=
+    tri_mul_out, tri_mul_in, tri_att_start, tri_att_end (all with the pair
+    mask), then the unmasked transition_z. Field dicts as in
+    ``boltz2_pairformer_layer``."""
+    heads = _f(p["tri_att_start"]["linear"]["weight"]).shape[0]
+    z = _f(z) + protenix_triangle_multiplication(z, pair_mask, p["tri_mul_out"], "outgoing")
+    z = z + protenix_triangle_multiplication(z, pair_mask, p["tri_mul_in"], "incoming")
+    z = z + protenix_triangle_attention(z, pair_mask, p["tri_att_start"], num_heads=heads, starting=True)
+    z = z + protenix_triangle_attention(z, pair_mask, p["tri_att_end"], num_heads=heads, starting=False)
+    return z + transition(z, p["transition_z"], eps=eps)
+
+
 def boltz2_pairformer_layer(p, s, z, mask, pair_mask, *, eps=1e-5):
     """One Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:100-206``):
     z += tri_mul_out, tri_mul_in, tri_att_start, tri_att_end, transition_z;
@@ -460,12 +474,7 @@ def boltz2_pairformer_layer(p, s, z, mask, pair_mask, *, eps=1e-5):
     (``layer_norm``, ``linear_a``, ``linear_b``, ``linear_out``), ``attention``
     (``pre_norm_s``, ``proj_*``). Returns ``(s, z)``.
     """
-    heads = _f(p["tri_att_start"]["linear"]["weight"]).shape[0]
-    z = _f(z) + protenix_triangle_multiplication(z, pair_mask, p["tri_mul_out"], "outgoing")
-    z = z + protenix_triangle_multiplication(z, pair_mask, p["tri_mul_in"], "incoming")
-    z = z + protenix_triangle_attention(z, pair_mask, p["tri_att_start"], num_heads=heads, starting=True)
-    z = z + protenix_triangle_attention(z, pair_mask, p["tri_att_end"], num_heads=heads, starting=False)
-    z = z + transition(z, p["transition_z"], eps=eps)
+    z = boltz2_pairformer_no_seq_layer(p, z, pair_mask, eps=eps)
     a = p["attention"]
     s_ln = layer_norm(s, a["pre_norm_s"]["weight"], a["pre_norm_s"]["bias"], eps)
     s = _f(s) + boltz2_attention_pair_bias(a, s_ln, z, mask, eps=eps)

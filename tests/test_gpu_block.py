@@ -133,6 +133,30 @@ def test_pairformer_module_two_layers():
     assert torch.equal(ps, gs) and torch.equal(pz, gz)
 
 
+def test_pairformer_no_seq_layer():
+    """The MSA module's pair block (``boltz2.pairformer_no_seq_layer_forward``)
+    against the oracle (bf16), and the pair half of a full layer gives the
+    same bits."""
+    dtype = DTYPES["bf16"]
+    n, n_real = 40, 35
+    say(f"pairformer no-seq layer n={n} bf16")
+    w = syn.pairformer_layer_weights(seed=31)
+    z = syn.pair_input(n, 128, seed=2, batch=1)
+    pm = syn.pair_mask(n, n_real)[None]
+    bp = P.pairformer_layer_to_boltz2(w)
+    params = {k: bp[k] for k in ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end", "transition_z")}
+    got = boltz2.pairformer_no_seq_layer_forward(params, device_tensor(z, dtype), device_tensor(pm, dtype))
+    torch.cuda.synchronize()
+    want = O.boltz2_pairformer_no_seq_layer(prep_tree(w, dtype), prep(z, dtype), pm)
+    v = slice(0, n_real)
+    assert_parity(to_np(got)[:, v, v], want[:, v, v], dtype, "no-seq layer z")
+    s = syn.single_input(n, 384, seed=3, batch=1)
+    tm = syn.token_mask(n, n_real)[None]
+    _, gz = boltz2.pairformer_layer_forward(bp, device_tensor(s, dtype), device_tensor(z, dtype),
+                                            device_tensor(tm, dtype), device_tensor(pm, dtype))
+    assert torch.equal(gz, got)
+
+
 def _of3_pair_block_oracle(z, p, pm, *, mask_transition, tri_mul_first):
     """The reference's ``pair_block`` composition on the oracle, with the
     ending node as a starting module between two transposes (as upstream)."""

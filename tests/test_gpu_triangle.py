@@ -169,6 +169,36 @@ def test_batch_axis_matches_per_item_bf16_n256():
             torch.testing.assert_close(att[i], kernels.triattn(zb[i], mb[i], wa, starting=starting), rtol=0, atol=0)
 
 
+def test_sample_axis_folds_like_batch():
+    """A leading sample axis in front of the batch (the confidence head's
+    pairformer; the reference folds it into one batch axis before the kernel,
+    ``_cueq.py:89-95``): x ``[S, B, N, N, c]`` with a mask ``[B, N, N]``
+    shared by the samples equals every ``[s, b]`` item run alone, bit for
+    bit, for tri-mul, tri-attn and the 6-D attention core."""
+    say("sample axis S=2 B=2 n=20 bf16")
+    n, dtype = 20, torch.bfloat16
+    z = device_tensor(syn.pair_input(n, seed=41, batch=4).reshape(2, 2, n, n, 128), dtype)
+    m = device_tensor(np.stack([mask_case(k, n) for k in ("tail", "random")]), dtype)
+    w = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(seed=42)), dtype, "cuda")
+    wa = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(seed=43)), dtype, "cuda")
+    out = kernels.trimul(z, m, w, "outgoing")
+    att = kernels.triattn(z, m, wa, starting=False)
+    for s in range(2):
+        for b in range(2):
+            assert torch.equal(out[s, b], kernels.trimul(z[s, b], m[b], w, "outgoing"))
+            assert torch.equal(att[s, b], kernels.triattn(z[s, b], m[b], wa, starting=False))
+    rng = np.random.default_rng(44)
+    h, d = 4, 32
+    q, k, v = (device_tensor(rng.standard_normal((2, 2, n, h, n, d)).astype(np.float32), dtype) for _ in range(3))
+    tb = device_tensor(rng.standard_normal((2, 1, h, n, n)).astype(np.float32), dtype)  # per batch, shared by samples
+    mb = device_tensor(1e9 * (np.stack([mask_case(k, n) for k in ("tail", "random")])[:, :, None, None, :] - 1), torch.float32)
+    core = kernels.triattn_core(q, k, v, tb, mb, scale=d ** -0.5)
+    for s in range(2):
+        for b in range(2):
+            one = kernels.triattn_core(q[s, b], k[s, b], v[s, b], tb[b], mb[b], scale=d ** -0.5)
+            assert torch.equal(core[s, b], one)
+
+
 def test_mask_none_equals_all_ones():
     say("mask None n=20")
     n, dtype = 20, torch.bfloat16
