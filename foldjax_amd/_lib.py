@@ -25,7 +25,7 @@ FJX_ERR_UNSUPPORTED = 2
 FJX_ERR_WORKSPACE = 3
 FJX_ERR_HIP = 4
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -75,6 +75,7 @@ class TransitionArgs(ctypes.Structure):
         ("x", _vp), ("norm_weight", _vp), ("norm_bias", _vp),
         ("w_a", _vp), ("w_b", _vp), ("w_o", _vp),
         ("row_mask", _vp), ("residual", _vp), ("out", _vp),
+        ("hidden", _i64), ("workspace", _vp), ("workspace_bytes", _sz),
     ]
 
 
@@ -100,6 +101,7 @@ SYMBOLS = {
     "fjx_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), _vp]),
     "fjx_triattn_core_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "fjx_triattn_core": (ctypes.c_int, [ctypes.POINTER(TriAttnCoreArgs), _vp]),
+    "fjx_transition_workspace_size": (_sz, [_i64, _i64, _i64, _i32]),
     "fjx_transition_fwd": (ctypes.c_int, [ctypes.POINTER(TransitionArgs), _vp]),
     "fjx_single_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "fjx_single_attention_fwd": (ctypes.c_int, [ctypes.POINTER(SingleAttentionArgs), _vp]),

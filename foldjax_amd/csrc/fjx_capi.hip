@@ -401,6 +401,243 @@ int transition_run(const fjx_transition_args* a, hipStream_t st) {
   return timed(id, st, "transition", [&] { launch_transition<T>(p, (int)a->c, st); });
 }
 
+// ------------------------------------------------- general-width paths
+// Widths the fused kernels are not built for (the Protenix template stack's
+// c_z = 64, wider tracks): row LayerNorms, GEMMs and layout passes around
+// the same contraction and flash kernels (fjx_generic.hip).
+bool fused_trimul(int64_t c_z, int64_t c_h) { return c_z == 128 && c_h == 128; }
+bool fused_triattn(int64_t c_z, int64_t heads, int64_t head_dim) {
+  return c_z == 128 && head_dim == 32 && heads * head_dim == 128;
+}
+bool fused_transition(int64_t c, int64_t hidden) { return (c == 128 || c == 384) && hidden == 4 * c; }
+int64_t transition_hidden(const fjx_transition_args* a) { return a->hidden > 0 ? a->hidden : 4 * a->c; }
+
+template <typename T>
+GemmParams<T, T> rows_gemm(const T* x, int64_t rows, int64_t k, const void* w, int64_t n_out, T* out, int64_t ldc) {
+  GemmParams<T, T> g = {};
+  g.a = x;
+  g.b = static_cast<const T*>(w);
+  g.c = out;
+  g.m = rows;
+  g.n = n_out;
+  g.k = k;
+  g.lda = k;
+  g.ldb = k;
+  g.ldc = ldc;
+  g.batches = 1;
+  return g;
+}
+
+struct GenTriMulWs {
+  size_t xn, pg, acm, bcm, ocm, g2, total;
+};
+GenTriMulWs gen_trimul_ws(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype) {
+  const size_t pos = (size_t)batch * n * n * esize(dtype);
+  GenTriMulWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  w.xn = take(pos * c_z);
+  w.pg = take(pos * 2 * c_h);  // G, then P = (x p_in^T) * G, then o position-major
+  w.acm = take(pos * c_h);     // a, then LN_out(o)
+  w.bcm = take(pos * c_h);
+  w.ocm = take(pos * c_h);
+  w.g2 = take(pos * c_z);
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+int trimul_generic_run(const fjx_trimul_args* a, hipStream_t st) {
+  const int64_t B = a->batch, n = a->n, nn = n * n, cz = a->c_z, ch = a->c_h, rows = B * nn;
+  const GenTriMulWs ws = gen_trimul_ws(B, n, cz, ch, a->dtype);
+  void* W = a->workspace;
+  T* xn = at<T>(W, ws.xn);
+  T* pg = at<T>(W, ws.pg);
+  T* acm = at<T>(W, ws.acm);
+  T* bcm = at<T>(W, ws.bcm);
+  T* ocm = at<T>(W, ws.ocm);
+  T* g2 = at<T>(W, ws.g2);
+  const int t = a->direction == FJX_INCOMING;
+  const T* mask = static_cast<const T*>(a->mask);
+
+  int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] {
+    launch_ln_grid<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_in_weight),
+                      static_cast<const T*>(a->norm_in_bias), xn, B, n, (int)cz, a->eps, 0, st);
+    GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, a->g_in_weight, 2 * ch, pg, 2 * ch);
+    g.act = 1;
+    launch_gemm<T, T>(g, st);
+    g = rows_gemm<T>(xn, rows, cz, a->p_in_weight, 2 * ch, pg, 2 * ch);
+    g.gate = pg;  // in place: each element reads its gate, then is overwritten
+    launch_gemm<T, T>(g, st);
+    launch_to_channel_major<T>(pg, 2 * ch, 0, (int)ch, mask, acm, B, n, t, st);
+    launch_to_channel_major<T>(pg, 2 * ch, (int)ch, (int)ch, mask, bcm, B, n, t, st);
+  });
+  if (rc) return rc;
+
+  rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] {
+    if constexpr (std::is_same<T, bf16>::value) {
+      launch_contract(acm, bcm, ocm, n, B * ch, st);
+    } else {
+      GemmParams<T, T> cp = {};
+      cp.a = acm;
+      cp.b = bcm;
+      cp.c = ocm;
+      cp.m = cp.n = cp.k = n;
+      cp.lda = cp.ldb = cp.ldc = n;
+      cp.sa = cp.sb = cp.sc = nn;
+      cp.batches = B * ch;
+      launch_gemm<T, T>(cp, st);
+    }
+  });
+  if (rc) return rc;
+
+  return timed(K_TRIMUL_EPILOGUE, st, "trimul_epilogue", [&] {
+    launch_to_position_major<T>(ocm, (int)ch, pg, B, nn, st);
+    launch_layernorm_rows<T>(pg, static_cast<const T*>(a->norm_out_weight), static_cast<const T*>(a->norm_out_bias),
+                             acm, rows, (int)ch, a->eps, st);
+    GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, a->g_out_weight, cz, g2, cz);
+    g.act = 1;
+    launch_gemm<T, T>(g, st);
+    g = rows_gemm<T>(acm, rows, ch, a->p_out_weight, cz, static_cast<T*>(a->out), cz);
+    g.gate = g2;
+    g.residual = static_cast<const T*>(a->residual);
+    launch_gemm<T, T>(g, st);
+  });
+}
+
+struct GenTriAttnWs {
+  size_t xn, proj, bias_pm, q, k, vt, bias, mb, o, y, total;
+};
+GenTriAttnWs gen_triattn_ws(int64_t batch, int64_t n, int64_t c_z, int64_t heads, int32_t dtype) {
+  const int64_t np = round64(n), hd = 32 * heads;
+  const size_t es = esize(dtype), pos = (size_t)batch * n * n * es;
+  GenTriAttnWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  w.xn = take(pos * c_z);
+  w.proj = take(pos * 4 * hd);  // q | k | v | sigmoid(g)
+  w.bias_pm = take(pos * heads);
+  w.q = take((size_t)batch * n * heads * np * 32 * es);
+  w.k = take((size_t)batch * n * heads * np * 32 * es);
+  w.vt = take((size_t)batch * n * heads * np * 32 * es);
+  w.bias = take((size_t)batch * heads * np * np * es);
+  w.mb = take((size_t)batch * n * np * sizeof(float));
+  w.o = take(pos * hd);
+  w.y = take(pos * c_z);
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
+  const int64_t B = a->batch, n = a->n, nn = n * n, cz = a->c_z, H = a->heads, hd = 32 * H, rows = B * nn;
+  const int64_t np = round64(n);
+  const GenTriAttnWs ws = gen_triattn_ws(B, n, cz, H, a->dtype);
+  void* W = a->workspace;
+  T* xn = at<T>(W, ws.xn);
+  T* proj = at<T>(W, ws.proj);
+  T* bpm = at<T>(W, ws.bias_pm);
+  const int t = a->starting ? 0 : 1;
+
+  int rc = timed(K_TRIATTN_PROLOGUE, st, "triattn_prologue", [&] {
+    launch_ln_grid<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_weight),
+                      static_cast<const T*>(a->norm_bias), xn, B, n, (int)cz, a->eps, t, st);
+    const void* wq[4] = {a->q_weight, a->k_weight, a->v_weight, a->g_weight};
+    for (int j = 0; j < 4; ++j) {
+      if (!wq[j]) continue;
+      GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, wq[j], hd, proj + j * hd, 4 * hd);
+      g.act = j == 3 ? 1 : 0;
+      launch_gemm<T, T>(g, st);
+    }
+    launch_gemm<T, T>(rows_gemm<T>(xn, rows, cz, a->bias_weight, H, bpm, H), st);
+    launch_split_qk<T>(proj, 4 * hd, 0, at<T>(W, ws.q), B * n, n, np, (int)H,
+                       (1.0f / sqrtf((float)a->head_dim)) * kLog2e, st);
+    launch_split_qk<T>(proj, 4 * hd, hd, at<T>(W, ws.k), B * n, n, np, (int)H, 1.0f, st);
+    launch_split_vt<T>(proj, 4 * hd, 2 * hd, at<T>(W, ws.vt), B * n, n, np, (int)hd, st);
+    launch_bias_planes<T>(bpm, H, 0, at<T>(W, ws.bias), B, n, np, (int)H, st);
+    launch_grid_mask_bias<T>(static_cast<const T*>(a->mask), at<float>(W, ws.mb), B, n, np, a->inf, t, st);
+  });
+  if (rc) return rc;
+
+  FlashParams<T> fp;
+  fp.q = at<T>(W, ws.q);
+  fp.k = at<T>(W, ws.k);
+  fp.vt = at<T>(W, ws.vt);
+  fp.bias = at<T>(W, ws.bias);
+  fp.mb = at<float>(W, ws.mb);
+  fp.out = at<T>(W, ws.o);
+  fp.n = n;
+  fp.np = np;
+  fp.heads = H;
+  fp.rows = n;
+  fp.o_stride_b = nn * hd;
+  fp.o_stride_row = n * hd;
+  fp.o_stride_head = 32;
+  fp.o_stride_q = hd;
+  fp.bias_stride_b = H * np * np;
+  rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, B, st); });
+  if (rc) return rc;
+
+  return timed(K_TRIATTN_EPILOGUE, st, "triattn_epilogue", [&] {
+    if (a->g_weight) launch_gate_rows<T>(fp.out, proj, 4 * hd, 3 * hd, rows, (int)hd, st);
+    T* y = at<T>(W, ws.y);
+    launch_gemm<T, T>(rows_gemm<T>(fp.out, rows, hd, a->o_weight, cz, y, cz), st);
+    launch_scatter_add<T>(y, nullptr, static_cast<const T*>(a->residual), static_cast<T*>(a->out), rows, n, (int)cz,
+                          t, st);
+  });
+}
+
+struct GenTransitionWs {
+  size_t xn, h, y, total;
+};
+GenTransitionWs gen_transition_ws(int64_t rows, int64_t c, int64_t hidden, int32_t dtype) {
+  const size_t es = esize(dtype);
+  GenTransitionWs w;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += align_up(bytes);
+    return at;
+  };
+  w.xn = take((size_t)rows * c * es);
+  w.h = take((size_t)rows * hidden * es);
+  w.y = take((size_t)rows * c * es);
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+int transition_generic_run(const fjx_transition_args* a, hipStream_t st) {
+  const int64_t rows = a->rows, c = a->c, hid = transition_hidden(a);
+  const GenTransitionWs ws = gen_transition_ws(rows, c, hid, a->dtype);
+  void* W = a->workspace;
+  T* xn = at<T>(W, ws.xn);
+  T* h = at<T>(W, ws.h);
+  T* y = at<T>(W, ws.y);
+  const int id = c == 384 ? K_SINGLE_TRANSITION : K_TRANSITION;
+  return timed(id, st, "transition", [&] {
+    launch_layernorm_rows<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_weight),
+                             static_cast<const T*>(a->norm_bias), xn, rows, (int)c, a->eps, st);
+    GemmParams<T, T> g = rows_gemm<T>(xn, rows, c, a->w_a, hid, h, hid);
+    g.act = 2;
+    launch_gemm<T, T>(g, st);
+    g = rows_gemm<T>(xn, rows, c, a->w_b, hid, h, hid);
+    g.gate = h;  // in place
+    launch_gemm<T, T>(g, st);
+    launch_gemm<T, T>(rows_gemm<T>(h, rows, hid, a->w_o, c, y, c), st);
+    launch_scatter_add<T>(y, static_cast<const T*>(a->row_mask), static_cast<const T*>(a->residual),
+                          static_cast<T*>(a->out), rows, 1, (int)c, 0, st);
+  });
+}
+
 // ------------------------------------------------ single-track attention
 struct SingleWs {
   size_t s_ln, qkvg, q, k, vt, bias, mb, o, go, total;
@@ -530,10 +767,8 @@ const char* fjx_last_error(void) { return g_err.c_str(); }
 int fjx_abi_version(void) { return FJX_ABI_VERSION; }
 
 size_t fjx_trimul_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype) {
-  (void)c_z;
-  (void)c_h;
-  if (batch < 1 || n < 1 || !dtype_ok(dtype)) return 0;
-  return trimul_ws(batch, n, dtype).total;
+  if (batch < 1 || n < 1 || c_z < 1 || c_h < 1 || !dtype_ok(dtype)) return 0;
+  return fused_trimul(c_z, c_h) ? trimul_ws(batch, n, dtype).total : gen_trimul_ws(batch, n, c_z, c_h, dtype).total;
 }
 
 int fjx_trimul_fwd(const fjx_trimul_args* a, hipStream_t st) {
@@ -543,8 +778,9 @@ int fjx_trimul_fwd(const fjx_trimul_args* a, hipStream_t st) {
   if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: unknown dtype %d", a->dtype);
   if (a->direction != FJX_OUTGOING && a->direction != FJX_INCOMING)
     return fail(FJX_ERR_INVALID, "Unsupported triangle multiplication direction: %d", a->direction);
-  if (a->c_z != 128 || a->c_h != 128)
-    return fail(FJX_ERR_UNSUPPORTED, "fjx_trimul_fwd: this build supports c_z == c_h == 128, got c_z=%lld c_h=%lld",
+  if (a->c_z < 8 || a->c_h < 8 || a->c_z % 8 || a->c_h % 8 || a->c_z > 1024 || a->c_h > 1024)
+    return fail(FJX_ERR_UNSUPPORTED,
+                "fjx_trimul_fwd: c_z and c_h must be multiples of 8 in [8, 1024], got c_z=%lld c_h=%lld",
                 (long long)a->c_z, (long long)a->c_h);
   if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_trimul_fwd: n or batch too large");
   if (!a->x || !a->out || !a->norm_in_weight || !a->norm_in_bias || !a->p_in_weight || !a->g_in_weight ||
@@ -553,19 +789,21 @@ int fjx_trimul_fwd(const fjx_trimul_args* a, hipStream_t st) {
   if (!aligned16({a->x, a->out, a->residual, a->norm_in_weight, a->norm_in_bias, a->p_in_weight, a->g_in_weight,
                   a->norm_out_weight, a->norm_out_bias, a->p_out_weight, a->g_out_weight}))
     return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: tensors must be 16-byte aligned");
-  const size_t need = trimul_ws(a->batch, a->n, a->dtype).total;
+  const bool fused = fused_trimul(a->c_z, a->c_h);
+  const size_t need = fjx_trimul_workspace_size(a->batch, a->n, a->c_z, a->c_h, a->dtype);
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_trimul_fwd: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);
+  if (!fused)
+    return a->dtype == FJX_DTYPE_BF16 ? trimul_generic_run<bf16>(a, st) : trimul_generic_run<float>(a, st);
   return a->dtype == FJX_DTYPE_BF16 ? trimul_run<bf16>(a, st) : trimul_run<float>(a, st);
 }
 
 size_t fjx_triattn_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t heads, int64_t head_dim,
                                   int32_t dtype) {
-  (void)c_z;
-  (void)head_dim;
-  if (batch < 1 || n < 1 || heads < 1 || !dtype_ok(dtype)) return 0;
-  return triattn_ws(batch, n, n, heads, dtype, true).total;
+  if (batch < 1 || n < 1 || c_z < 1 || heads < 1 || !dtype_ok(dtype)) return 0;
+  return fused_triattn(c_z, heads, head_dim) ? triattn_ws(batch, n, n, heads, dtype, true).total
+                                             : gen_triattn_ws(batch, n, c_z, heads, dtype).total;
 }
 
 int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
@@ -573,10 +811,10 @@ int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
   if (!a) return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: args is NULL");
   if (a->batch < 1 || a->n < 1) return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: batch and n must be >= 1");
   if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: unknown dtype %d", a->dtype);
-  if (a->c_z != 128 || a->head_dim != 32 || a->heads * a->head_dim != 128)
+  if (a->heads < 1 || a->head_dim != 32 || a->c_z < 8 || a->c_z % 8 || a->c_z > 1024 || a->heads > 32)
     return fail(FJX_ERR_UNSUPPORTED,
-                "fjx_triattn_fwd: this build supports c_z == 128, head_dim == 32, heads*head_dim == 128; got "
-                "c_z=%lld heads=%lld head_dim=%lld",
+                "fjx_triattn_fwd: this build supports head_dim == 32, 1 <= heads <= 32 and c_z a multiple of 8 in "
+                "[8, 1024]; got c_z=%lld heads=%lld head_dim=%lld",
                 (long long)a->c_z, (long long)a->heads, (long long)a->head_dim);
   if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_triattn_fwd: n or batch too large");
   if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->bias_weight || !a->q_weight ||
@@ -585,10 +823,13 @@ int fjx_triattn_fwd(const fjx_triattn_args* a, hipStream_t st) {
   if (!aligned16({a->x, a->out, a->residual, a->norm_weight, a->norm_bias, a->bias_weight, a->q_weight, a->k_weight,
                   a->v_weight, a->g_weight, a->o_weight}))
     return fail(FJX_ERR_INVALID, "fjx_triattn_fwd: tensors must be 16-byte aligned");
-  const size_t need = triattn_ws(a->batch, a->n, a->n, a->heads, a->dtype, true).total;
+  const bool fused = fused_triattn(a->c_z, a->heads, a->head_dim);
+  const size_t need = fjx_triattn_workspace_size(a->batch, a->n, a->c_z, a->heads, a->head_dim, a->dtype);
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_triattn_fwd: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);
+  if (!fused)
+    return a->dtype == FJX_DTYPE_BF16 ? triattn_generic_run<bf16>(a, st) : triattn_generic_run<float>(a, st);
   return a->dtype == FJX_DTYPE_BF16 ? triattn_run<bf16>(a, st) : triattn_run<float>(a, st);
 }
 
@@ -619,20 +860,36 @@ int fjx_triattn_core(const fjx_triattn_core_args* a, hipStream_t st) {
   return a->dtype == FJX_DTYPE_BF16 ? core_run<bf16>(a, st) : core_run<float>(a, st);
 }
 
+size_t fjx_transition_workspace_size(int64_t rows, int64_t c, int64_t hidden, int32_t dtype) {
+  if (rows < 1 || c < 1 || hidden < 0 || !dtype_ok(dtype)) return 0;
+  const int64_t hid = hidden > 0 ? hidden : 4 * c;
+  return fused_transition(c, hid) ? 0 : gen_transition_ws(rows, c, hid, dtype).total;
+}
+
 int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
   g_err.clear();
   if (!a) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: args is NULL");
   if (a->rows < 1) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: rows must be >= 1");
   if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: unknown dtype %d", a->dtype);
-  if (a->c != 128 && a->c != 384)
-    return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: this build supports c in {128, 384}, got %lld",
-                (long long)a->c);
+  if (a->hidden < 0) return fail(FJX_ERR_INVALID, "fjx_transition_fwd: hidden must be >= 0");
+  const int64_t hid = transition_hidden(a);
+  if (a->c < 8 || a->c % 8 || a->c > 1024 || hid % 8)
+    return fail(FJX_ERR_UNSUPPORTED,
+                "fjx_transition_fwd: c must be a multiple of 8 in [8, 1024] and hidden a multiple of 8; got c=%lld "
+                "hidden=%lld",
+                (long long)a->c, (long long)hid);
   if ((a->rows + 15) / 16 > 0x7fffffffLL) return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: too many rows");
   if (!a->x || !a->out || !a->norm_weight || !a->norm_bias || !a->w_a || !a->w_b || !a->w_o)
     return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a required pointer is NULL");
   if (!aligned16({a->x, a->out, a->residual, a->norm_weight, a->norm_bias, a->w_a, a->w_b, a->w_o}))
     return fail(FJX_ERR_INVALID, "fjx_transition_fwd: tensors must be 16-byte aligned");
-  return a->dtype == FJX_DTYPE_BF16 ? transition_run<bf16>(a, st) : transition_run<float>(a, st);
+  if (fused_transition(a->c, hid))
+    return a->dtype == FJX_DTYPE_BF16 ? transition_run<bf16>(a, st) : transition_run<float>(a, st);
+  const size_t need = fjx_transition_workspace_size(a->rows, a->c, hid, a->dtype);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail(FJX_ERR_WORKSPACE, "fjx_transition_fwd: workspace of %zu bytes needed, %zu given", need,
+                a->workspace_bytes);
+  return a->dtype == FJX_DTYPE_BF16 ? transition_generic_run<bf16>(a, st) : transition_generic_run<float>(a, st);
 }
 
 size_t fjx_single_attention_workspace_size(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype) {

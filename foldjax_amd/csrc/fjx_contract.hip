@@ -155,6 +155,7 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
         if (row >= M) continue;
         float v = acc[i][j][q] + bias;
         if (P.act == 1) v = fast_sigmoid(v);
+        else if (P.act == 2) v *= fast_sigmoid(v);  // silu
         const int64_t off = row * P.ldc + col;
         if (G) v *= to_f32(G[off]);
         if (R) v += to_f32(R[off]);

@@ -1,0 +1,310 @@
+// Layout and elementwise kernels of the general-width paths: the triangle
+// ops and the transition for channel widths the fused kernels do not take
+// (the fused ones are built for c_z = c_h = 128, H*D = 128). The C ABI layer
+// composes these with the row LayerNorm, the generic GEMM, the contraction
+// and the flash attention core into the same computation:
+//
+//   tri-mul:  xn = LN_in(x) -> G = sigmoid(xn g_in^T), P = (xn p_in^T) * G
+//             -> a, b = mask * P, channel-major in the virtual grid
+//             -> o[c] = a[c] b[c]^T -> LN_out(o) -> (.. p_out^T) * sigmoid(xn g_out^T)
+//   tri-attn: xn = LN(x) in the virtual grid -> q|k|v|g and the bias by GEMM
+//             -> padded head layouts -> flash core -> o * sigmoid(g) -> o w_o^T
+//   transition: LN -> silu(xn a^T) * (xn b^T) -> (..) o^T [* row mask]
+//
+// Positions of the virtual grid are v = r*n + s; for the incoming direction
+// and the ending node they read the original grid at s*n + r.
+#include "fjx_common.hpp"
+#include "fjx_kernels.hpp"
+
+namespace fjx {
+
+namespace {
+
+__device__ __forceinline__ int64_t orig_pos(int64_t v, int64_t n, int t) {
+  if (!t) return v;
+  const int64_t r = v / n;
+  return (v - r * n) * n + r;
+}
+
+dim3 stride_grid(int64_t total) {
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (blocks < 1) blocks = 1;
+  return dim3((unsigned)blocks);
+}
+
+// one wave per position: y[b][v][:] = LN(x[b][orig(v)][:]), c <= 1024
+template <typename T>
+__global__ __launch_bounds__(256) void ln_grid_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                      const T* __restrict__ b, T* __restrict__ y, int64_t rows,
+                                                      int64_t n, int c, float eps, int t) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int64_t nn = n * n;
+  const int64_t bb = row / nn;
+  const T* xr = x + (bb * nn + orig_pos(row - bb * nn, n, t)) * c;
+  float v[16];
+  float s = 0.f;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int ch = lane + 64 * u;
+    v[u] = ch < c ? to_f32(xr[ch]) : 0.f;
+    s += v[u];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += shfl_xor(s, o);
+  const float mean = s / c;
+  float q2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int ch = lane + 64 * u;
+    if (ch < c) q2 += (v[u] - mean) * (v[u] - mean);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) q2 += shfl_xor(q2, o);
+  const float rstd = __builtin_amdgcn_rsqf(q2 / c + eps);
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int ch = lane + 64 * u;
+    if (ch < c) y[row * c + ch] = from_f32<T>((v[u] - mean) * rstd * to_f32(w[ch]) + to_f32(b[ch]));
+  }
+}
+
+// dst[b][c][v] = src[b][orig(v)][c0 + c] * mask[b][orig(v)] (c < C), through
+// 64 x 64 LDS tiles so that both sides move whole rows
+template <typename T>
+__global__ __launch_bounds__(256) void to_channel_major_kernel(const T* __restrict__ src, int64_t ld, int c0, int C,
+                                                               const T* __restrict__ mask, T* __restrict__ dst,
+                                                               int64_t n, int t) {
+  __shared__ float tile[64][65];
+  const int64_t nn = n * n;
+  const int64_t vtiles = (nn + 63) / 64;
+  const int ctiles = (C + 63) / 64;
+  int64_t id = blockIdx.x;
+  const int ct = (int)(id % ctiles);
+  id /= ctiles;
+  const int64_t vt = id % vtiles;
+  const int64_t bb = id / vtiles;
+  const int64_t v0 = vt * 64;
+  const int cb = ct * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int pv = e >> 6, pc = e & 63;
+    const int64_t v = v0 + pv;
+    const int c = cb + pc;
+    float val = 0.f;
+    if (v < nn && c < C) {
+      const int64_t o = bb * nn + orig_pos(v, n, t);
+      val = to_f32(src[o * ld + c0 + c]);
+      if (mask) val *= to_f32(mask[o]);
+    }
+    tile[pv][pc] = val;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int pc = e >> 6, pv = e & 63;
+    const int64_t v = v0 + pv;
+    const int c = cb + pc;
+    if (v < nn && c < C) dst[(bb * C + c) * nn + v] = from_f32<T>(tile[pv][pc]);
+  }
+}
+
+// dst[b][v][c] = src[b][c][v]
+template <typename T>
+__global__ __launch_bounds__(256) void to_position_major_kernel(const T* __restrict__ src, int C, T* __restrict__ dst,
+                                                                int64_t nn) {
+  __shared__ float tile[64][65];
+  const int64_t vtiles = (nn + 63) / 64;
+  const int ctiles = (C + 63) / 64;
+  int64_t id = blockIdx.x;
+  const int ct = (int)(id % ctiles);
+  id /= ctiles;
+  const int64_t vt = id % vtiles;
+  const int64_t bb = id / vtiles;
+  const int64_t v0 = vt * 64;
+  const int cb = ct * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int pc = e >> 6, pv = e & 63;
+    const int64_t v = v0 + pv;
+    const int c = cb + pc;
+    tile[pc][pv] = (v < nn && c < C) ? to_f32(src[(bb * C + c) * nn + v]) : 0.f;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int pv = e >> 6, pc = e & 63;
+    const int64_t v = v0 + pv;
+    const int c = cb + pc;
+    if (v < nn && c < C) dst[(bb * nn + v) * C + c] = from_f32<T>(tile[pc][pv]);
+  }
+}
+
+// q/k of the flash core: dst[br][h][s][d] (s < np) = src[br*n + s][c0 + 32h + d] * mul, zero padded keys
+template <typename T>
+__global__ void split_qk_kernel(const T* __restrict__ src, int64_t ld, int64_t c0, T* __restrict__ dst, int64_t rows,
+                                int64_t n, int64_t np, int heads, float mul) {
+  const int64_t total = rows * heads * np * 32;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int d = (int)(idx % 32);
+    const int64_t s = (idx / 32) % np;
+    const int h = (int)((idx / (32 * np)) % heads);
+    const int64_t br = idx / (32 * np * heads);
+    dst[idx] = s < n ? from_f32<T>(to_f32(src[(br * n + s) * ld + c0 + 32 * h + d]) * mul) : from_f32<T>(0.f);
+  }
+}
+
+// v of the flash core, keys innermost: dst[br][hd][s] = src[br*n + s][c0 + hd]
+template <typename T>
+__global__ void split_vt_kernel(const T* __restrict__ src, int64_t ld, int64_t c0, T* __restrict__ dst, int64_t rows,
+                                int64_t n, int64_t np, int hd_total) {
+  const int64_t total = rows * hd_total * np;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t s = idx % np;
+    const int hd = (int)((idx / np) % hd_total);
+    const int64_t br = idx / (np * hd_total);
+    dst[idx] = s < n ? src[(br * n + s) * ld + c0 + hd] : from_f32<T>(0.f);
+  }
+}
+
+// triangle bias planes: dst[b][h][q][k] (np x np) = src[b][q*n + k][c0 + h] * log2 e, zeros outside
+template <typename T>
+__global__ void bias_planes_kernel(const T* __restrict__ src, int64_t ld, int64_t c0, T* __restrict__ dst,
+                                   int64_t batch, int64_t n, int64_t np, int heads) {
+  const int64_t total = batch * heads * np * np;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = idx % np;
+    const int64_t q = (idx / np) % np;
+    const int h = (int)((idx / (np * np)) % heads);
+    const int64_t bb = idx / (np * np * heads);
+    dst[idx] = (q < n && k < n) ? from_f32<T>(to_f32(src[(bb * n * n + q * n + k) * ld + c0 + h]) * kLog2e)
+                                : from_f32<T>(0.f);
+  }
+}
+
+// mask bias of row r: mb[b][r][k] = inf * (mask[b][orig(r*n + k)] - 1) * log2 e (0 without a mask),
+// -inf for the padded keys
+template <typename T>
+__global__ void grid_mask_bias_kernel(const T* __restrict__ mask, float* __restrict__ mb, int64_t batch, int64_t n,
+                                      int64_t np, float inf, int t) {
+  const int64_t total = batch * n * np;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = idx % np;
+    const int64_t r = (idx / np) % n;
+    const int64_t bb = idx / (np * n);
+    float v = -INFINITY;
+    if (k < n) v = mask ? inf * (to_f32(mask[bb * n * n + orig_pos(r * n + k, n, t)]) - 1.0f) * kLog2e : 0.f;
+    mb[idx] = v;
+  }
+}
+
+// o[i][j] *= g[i*ldg + c0 + j] for rows x width
+template <typename T>
+__global__ void gate_rows_kernel(T* __restrict__ o, const T* __restrict__ g, int64_t ldg, int64_t c0, int64_t rows,
+                                 int width) {
+  const int64_t total = rows * width;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = idx / width;
+    const int j = (int)(idx - i * width);
+    o[idx] = from_f32<T>(to_f32(o[idx]) * to_f32(g[i * ldg + c0 + j]));
+  }
+}
+
+// out[b][orig(v)][c] = T(y[b][v][c] * m) + residual[b][orig(v)][c], with m
+// the row mask at the output position (1 without one)
+template <typename T>
+__global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
+                                   const T* __restrict__ residual, T* __restrict__ out, int64_t rows, int64_t n,
+                                   int c, int t) {
+  const int64_t total = rows * c;
+  const int64_t nn = n * n;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = idx / c;
+    const int ch = (int)(idx - row * c);
+    const int64_t bb = row / nn;
+    const int64_t o = bb * nn + orig_pos(row - bb * nn, n, t);
+    float v = to_f32(y[idx]);
+    if (row_mask) v *= to_f32(row_mask[o]);
+    v = round_to<T>(v);
+    if (residual) v += to_f32(residual[o * c + ch]);
+    out[o * c + ch] = from_f32<T>(v);
+  }
+}
+
+}  // namespace
+
+template <typename T>
+void launch_ln_grid(const T* x, const T* w, const T* b, T* y, int64_t batch, int64_t n, int c, float eps, int t,
+                    hipStream_t st) {
+  const int64_t rows = batch * n * n;
+  hipLaunchKernelGGL(ln_grid_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows, n, c,
+                     eps, t);
+}
+template <typename T>
+void launch_to_channel_major(const T* src, int64_t ld, int c0, int C, const T* mask, T* dst, int64_t batch, int64_t n,
+                             int t, hipStream_t st) {
+  const int64_t blocks = batch * ((n * n + 63) / 64) * ((C + 63) / 64);
+  hipLaunchKernelGGL(to_channel_major_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, ld, c0, C, mask, dst,
+                     n, t);
+}
+template <typename T>
+void launch_to_position_major(const T* src, int C, T* dst, int64_t batch, int64_t nn, hipStream_t st) {
+  const int64_t blocks = batch * ((nn + 63) / 64) * ((C + 63) / 64);
+  hipLaunchKernelGGL(to_position_major_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, C, dst, nn);
+}
+template <typename T>
+void launch_split_qk(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int heads,
+                     float mul, hipStream_t st) {
+  hipLaunchKernelGGL(split_qk_kernel<T>, stride_grid(rows * heads * np * 32), dim3(256), 0, st, src, ld, c0, dst,
+                     rows, n, np, heads, mul);
+}
+template <typename T>
+void launch_split_vt(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int hd_total,
+                     hipStream_t st) {
+  hipLaunchKernelGGL(split_vt_kernel<T>, stride_grid(rows * hd_total * np), dim3(256), 0, st, src, ld, c0, dst, rows,
+                     n, np, hd_total);
+}
+template <typename T>
+void launch_bias_planes(const T* src, int64_t ld, int64_t c0, T* dst, int64_t batch, int64_t n, int64_t np, int heads,
+                        hipStream_t st) {
+  hipLaunchKernelGGL(bias_planes_kernel<T>, stride_grid(batch * heads * np * np), dim3(256), 0, st, src, ld, c0, dst,
+                     batch, n, np, heads);
+}
+template <typename T>
+void launch_grid_mask_bias(const T* mask, float* mb, int64_t batch, int64_t n, int64_t np, float inf, int t,
+                           hipStream_t st) {
+  hipLaunchKernelGGL(grid_mask_bias_kernel<T>, stride_grid(batch * n * np), dim3(256), 0, st, mask, mb, batch, n, np,
+                     inf, t);
+}
+template <typename T>
+void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, int width, hipStream_t st) {
+  hipLaunchKernelGGL(gate_rows_kernel<T>, stride_grid(rows * width), dim3(256), 0, st, o, g, ldg, c0, rows, width);
+}
+template <typename T>
+void launch_scatter_add(const T* y, const T* row_mask, const T* residual, T* out, int64_t rows, int64_t n, int c,
+                        int t, hipStream_t st) {
+  hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out, rows,
+                     n, c, t);
+}
+
+#define FJX_INST(T)                                                                                                \
+  template void launch_ln_grid<T>(const T*, const T*, const T*, T*, int64_t, int64_t, int, float, int, hipStream_t); \
+  template void launch_to_channel_major<T>(const T*, int64_t, int, int, const T*, T*, int64_t, int64_t, int,        \
+                                           hipStream_t);                                                           \
+  template void launch_to_position_major<T>(const T*, int, T*, int64_t, int64_t, hipStream_t);                    \
+  template void launch_split_qk<T>(const T*, int64_t, int64_t, T*, int64_t, int64_t, int64_t, int, float,           \
+                                   hipStream_t);                                                                   \
+  template void launch_split_vt<T>(const T*, int64_t, int64_t, T*, int64_t, int64_t, int64_t, int, hipStream_t);   \
+  template void launch_bias_planes<T>(const T*, int64_t, int64_t, T*, int64_t, int64_t, int64_t, int, hipStream_t); \
+  template void launch_grid_mask_bias<T>(const T*, float*, int64_t, int64_t, int64_t, float, int, hipStream_t);     \
+  template void launch_gate_rows<T>(T*, const T*, int64_t, int64_t, int64_t, int, hipStream_t);                      \
+  template void launch_scatter_add<T>(const T*, const T*, const T*, T*, int64_t, int64_t, int, int, hipStream_t);
+FJX_INST(float)
+FJX_INST(bf16)
+#undef FJX_INST
+
+}  // namespace fjx

@@ -86,7 +86,7 @@ struct GemmParams {
   int64_t sa, sb, sc;  // batch strides in elements (0 = shared)
   int64_t batches;
   const T* bias;       // [n] or null
-  int act;             // 0 none, 1 sigmoid
+  int act;             // 0 none, 1 sigmoid, 2 silu
   const TO* gate;      // indexed like c, or null
   const TO* residual;  // indexed like c, or null (may alias c)
 };
@@ -156,5 +156,33 @@ void launch_gate_unpad(const T* o, const T* g, int64_t ldg, T* out, int64_t rows
                        hipStream_t st);
 template <typename T>
 void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st);
+
+// general-width paths (fjx_generic.hip); positions v = r*n + s of the virtual
+// grid read the original grid at s*n + r when t = 1
+template <typename T>
+void launch_ln_grid(const T* x, const T* w, const T* b, T* y, int64_t batch, int64_t n, int c, float eps, int t,
+                    hipStream_t st);
+template <typename T>
+void launch_to_channel_major(const T* src, int64_t ld, int c0, int C, const T* mask, T* dst, int64_t batch, int64_t n,
+                             int t, hipStream_t st);
+template <typename T>
+void launch_to_position_major(const T* src, int C, T* dst, int64_t batch, int64_t nn, hipStream_t st);
+template <typename T>
+void launch_split_qk(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int heads,
+                     float mul, hipStream_t st);
+template <typename T>
+void launch_split_vt(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int hd_total,
+                     hipStream_t st);
+template <typename T>
+void launch_bias_planes(const T* src, int64_t ld, int64_t c0, T* dst, int64_t batch, int64_t n, int64_t np, int heads,
+                        hipStream_t st);
+template <typename T>
+void launch_grid_mask_bias(const T* mask, float* mb, int64_t batch, int64_t n, int64_t np, float inf, int t,
+                           hipStream_t st);
+template <typename T>
+void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, int width, hipStream_t st);
+template <typename T>
+void launch_scatter_add(const T* y, const T* row_mask, const T* residual, T* out, int64_t rows, int64_t n, int c,
+                        int t, hipStream_t st);
 
 }  // namespace fjx

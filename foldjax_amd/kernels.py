@@ -88,8 +88,9 @@ class TriAttnWeights:
 
 @dataclass(frozen=True)
 class TransitionWeights:
-    """Transition weights, PyTorch ``[out, in]``: ``w_a``/``w_b`` ``[4c, c]`` (silu
-    and linear branches), ``w_o`` ``[c, 4c]``."""
+    """Transition weights, PyTorch ``[out, in]``: ``w_a``/``w_b`` ``[hidden, c]``
+    (silu and linear branches), ``w_o`` ``[c, hidden]``; hidden is 4c in every
+    port."""
 
     norm_weight: torch.Tensor
     norm_bias: torch.Tensor
@@ -146,11 +147,15 @@ def transition(
     if row_mask is not None:
         rm = torch.broadcast_to(row_mask, x.shape[:-1]).to(dtype=x.dtype).contiguous()
     res = None if residual is None else residual.to(dtype=x.dtype).contiguous()
+    hidden = int(w.w_a.shape[0])
+    ws_bytes = lib.fjx_transition_workspace_size(rows, c, hidden, _code(x.dtype))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     a = _lib.TransitionArgs(
         rows=rows, c=c, dtype=_code(x.dtype), eps=float(eps),
         x=_ptr(xf), norm_weight=_ptr(w.norm_weight), norm_bias=_ptr(w.norm_bias),
         w_a=_ptr(w.w_a), w_b=_ptr(w.w_b), w_o=_ptr(w.w_o),
         row_mask=_ptr(rm), residual=_ptr(res), out=_ptr(out),
+        hidden=hidden, workspace=_ptr(ws), workspace_bytes=ws_bytes,
     )
     _check_weights(x, w)
     _lib.check(lib.fjx_transition_fwd(ctypes.byref(a), _stream(x)))

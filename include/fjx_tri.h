@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FJX_ABI_VERSION 1
+#define FJX_ABI_VERSION 2
 
 /* element types of activations, masks and weights */
 enum { FJX_DTYPE_F32 = 0, FJX_DTYPE_BF16 = 1 };
@@ -71,8 +71,11 @@ enum {
  * p_in/g_in are [2*c_h, c_z] with the a rows first. In BF16 mode the
  * contraction runs on bf16 MFMA with fp32 accumulation (the reference's
  * fp32-upcast contraction of bf16 values, B2T/triangle.py:95-97) and o is
- * rounded to bf16 before LN_out (B2T/triangle.py:124). Supported here:
- * c_z == c_h == 128.
+ * rounded to bf16 before LN_out (B2T/triangle.py:124). Fused kernels serve
+ * c_z == c_h == 128; other widths (c_z, c_h multiples of 8 up to 1024, e.g.
+ * the Protenix template stack's c_z = 64, c_h = 128, protenix/models/triangle/
+ * triangle.py:131-137) run a general path of row LayerNorms, GEMMs and the same
+ * contraction, with a larger workspace.
  */
 typedef struct fjx_trimul_args {
   int64_t batch;
@@ -115,8 +118,10 @@ int fjx_trimul_fwd(const fjx_trimul_args* args, hipStream_t stream);
  *   out       = (sigmoid(g) * o) w_o^T                 (+ residual)
  *
  * Weights are PyTorch [out, in]. The softmax runs in fp32 with exp2 and the
- * log2(e) factor folded into q and the biases. Supported here: c_z == 128,
- * heads * head_dim == 128, head_dim == 32.
+ * log2(e) factor folded into q and the biases. Fused kernels serve c_z == 128,
+ * heads * head_dim == 128, head_dim == 32; other widths (c_z a multiple of 8
+ * up to 1024, any heads, head_dim == 32) run a general path of row
+ * LayerNorms, GEMMs and the same flash core, with a larger workspace.
  */
 typedef struct fjx_triattn_args {
   int64_t batch;
@@ -182,11 +187,14 @@ int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
 /*
  * Transition (pair or single track): for every row of c channels
  *   out = (silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T  [* row_mask]  [+ residual]
- * with a 4c hidden width that never leaves the chip. Replaces
- * src/foldjax/models/boltz2/models/primitives/transition.py:39-122
+ * Replaces src/foldjax/models/boltz2/models/primitives/transition.py:39-122
  * (fc1 = w_a, fc2 = w_b, fc3 = w_o), protenix/models/primitives/primitives.py:117-146
  * and openfold3/models/primitives.py:133-150 (row_mask = the OpenFold3 mask).
- * Weights PyTorch [out, in]: w_a, w_b [4c, c]; w_o [c, 4c]. Supported: c in {128, 384}.
+ * Weights PyTorch [out, in]: w_a, w_b [hidden, c]; w_o [c, hidden]; hidden = 0
+ * means 4c. Fused kernels (the hidden activations never leave the chip) serve
+ * c in {128, 384} with hidden == 4c and need no workspace; other widths (c and
+ * hidden multiples of 8, c <= 1024) run a general path of GEMMs through the
+ * workspace of fjx_transition_workspace_size.
  */
 typedef struct fjx_transition_args {
   int64_t rows;
@@ -202,8 +210,12 @@ typedef struct fjx_transition_args {
   const void* row_mask;  /* [rows] or NULL */
   const void* residual;  /* [rows, c] or NULL; may equal out */
   void* out;             /* [rows, c] */
+  int64_t hidden;        /* 0 for 4c */
+  void* workspace;       /* general path only; may be NULL when the size is 0 */
+  size_t workspace_bytes;
 } fjx_transition_args;
 
+size_t fjx_transition_workspace_size(int64_t rows, int64_t c, int64_t hidden, int32_t dtype);
 int fjx_transition_fwd(const fjx_transition_args* args, hipStream_t stream);
 
 /*

@@ -82,6 +82,13 @@ def test_workspace_sizes_are_host_only(lib):
     assert lib.fjx_trimul_workspace_size(0, 8, 128, 128, 0) == 0
     assert lib.fjx_triattn_workspace_size(1, 384, 128, 4, 32, _lib.FJX_DTYPE_BF16) > 0
     assert lib.fjx_triattn_core_workspace_size(1, 3, 4, 70, 32, _lib.FJX_DTYPE_F32) > 0
+    # the general-width paths (e.g. the template stack's c_z = 64) take their own, larger workspace
+    fused = lib.fjx_trimul_workspace_size(1, 64, 128, 128, _lib.FJX_DTYPE_BF16)
+    assert lib.fjx_trimul_workspace_size(1, 64, 64, 128, _lib.FJX_DTYPE_BF16) > fused
+    assert lib.fjx_triattn_workspace_size(1, 64, 64, 4, 32, _lib.FJX_DTYPE_BF16) > 0
+    assert lib.fjx_transition_workspace_size(100, 128, 0, _lib.FJX_DTYPE_BF16) == 0  # fused: none
+    assert lib.fjx_transition_workspace_size(100, 384, 1536, _lib.FJX_DTYPE_BF16) == 0
+    assert lib.fjx_transition_workspace_size(100, 64, 0, _lib.FJX_DTYPE_BF16) >= 100 * (64 + 256 + 64) * 2
 
 
 def test_invalid_arguments_return_codes_without_launching(lib):
@@ -90,9 +97,9 @@ def test_invalid_arguments_return_codes_without_launching(lib):
     assert rc == _lib.FJX_ERR_INVALID
     assert "Unsupported triangle multiplication direction" in lib.fjx_last_error().decode()
 
-    a = _lib.TriMulArgs(batch=1, n=8, c_z=64, c_h=128, direction=0, dtype=0, eps=1e-5)
+    a = _lib.TriMulArgs(batch=1, n=8, c_z=60, c_h=128, direction=0, dtype=0, eps=1e-5)
     assert lib.fjx_trimul_fwd(ctypes.byref(a), None) == _lib.FJX_ERR_UNSUPPORTED
-    assert "c_z == c_h == 128" in lib.fjx_last_error().decode()
+    assert "multiples of 8" in lib.fjx_last_error().decode()
 
     a = _lib.TriMulArgs(batch=1, n=8, c_z=128, c_h=128, direction=0, dtype=0, eps=1e-5)
     assert lib.fjx_trimul_fwd(ctypes.byref(a), None) == _lib.FJX_ERR_INVALID  # null pointers
@@ -117,8 +124,10 @@ def test_invalid_arguments_return_codes_without_launching(lib):
     c = _lib.TriAttnCoreArgs(batch=1, rows=1, heads=1, n=4, head_dim=64, dtype=0)
     assert lib.fjx_triattn_core(ctypes.byref(c), None) == _lib.FJX_ERR_UNSUPPORTED
     assert lib.fjx_trimul_fwd(None, None) == _lib.FJX_ERR_INVALID
-    tr = _lib.TransitionArgs(rows=4, c=256, dtype=1)
+    tr = _lib.TransitionArgs(rows=4, c=100, dtype=1)
     assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_UNSUPPORTED
+    tr = _lib.TransitionArgs(rows=4, c=64, dtype=1, hidden=-1)
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_INVALID
     sa = _lib.SingleAttentionArgs(batch=1, n=4, c_s=384, c_z=128, heads=8, dtype=1)  # head_dim 48 > 32
     assert lib.fjx_single_attention_fwd(ctypes.byref(sa), None) == _lib.FJX_ERR_UNSUPPORTED
 

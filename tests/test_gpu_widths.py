@@ -1,0 +1,106 @@
+"""GPU parity of the general-width paths, the shapes the fused kernels are not
+built for: the Protenix template stack (c_z = 64 with c_h = 128 for tri-mul,
+``PXT/triangle.py:131-137``; c_z = 64 tri-attn), a c = 384 track (OpenDDE's
+c_z = c_h = 384) and transitions of other widths and expansions, against the
+CPU oracle on the same values (fp32: max-abs <= 1e-4; bf16: relative <= 2e-2)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from foldjax_amd import kernels, protenix
+from foldjax_amd import params as P
+from foldjax_amd import synthetic as syn
+from oracle import triangle as O
+from tests.gpu_util import assert_parity, device_tensor, mask_case, prep, prep_tree, say, to_np
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16}
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+@pytest.mark.parametrize("c_z,c_h,n,mask_kind", [(64, 128, 33, "tail"), (64, 128, 70, "random"),
+                                                 (384, 384, 20, "random")])
+def test_trimul_widths(dt, direction, c_z, c_h, n, mask_kind):
+    dtype = DTYPES[dt]
+    say(f"trimul widths c_z={c_z} c_h={c_h} n={n} {dt} {direction}")
+    z = syn.pair_input(n, c_z, seed=5)
+    m = mask_case(mask_kind, n)
+    w = syn.trimul_weights(c_z, c_h, seed=6)
+    got = protenix.triangle_multiplication(device_tensor(z, dtype), device_tensor(m, dtype),
+                                           P.trimul_to_protenix(w), direction)
+    torch.cuda.synchronize()
+    want = O.protenix_triangle_multiplication(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), direction)
+    assert got.shape == (n, n, c_z)
+    assert_parity(to_np(got), want, dtype, f"trimul c_z={c_z} c_h={c_h} {direction}")
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("c_z,heads,n", [(64, 4, 33), (64, 2, 70), (384, 8, 20)])
+def test_triattn_widths(dt, starting, c_z, heads, n):
+    dtype = DTYPES[dt]
+    say(f"triattn widths c_z={c_z} heads={heads} n={n} {dt} starting={starting}")
+    z = syn.pair_input(n, c_z, seed=7)
+    m = mask_case("tail", n)
+    w = syn.triattn_weights(c_z, heads, 32, seed=8)
+    got = protenix.triangle_attention(device_tensor(z, dtype), device_tensor(m, dtype), P.triattn_to_protenix(w),
+                                      num_heads=heads, starting=starting)
+    torch.cuda.synchronize()
+    want = O.protenix_triangle_attention(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), num_heads=heads,
+                                         starting=starting)
+    mv = m if starting else m.T
+    rows = mv.max(axis=1) > 0
+    g, w_ = (to_np(got)[rows], want[rows]) if starting else (to_np(got)[:, rows], want[:, rows])
+    assert_parity(g, w_, dtype, f"triattn c_z={c_z} heads={heads} starting={starting}")
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("c,expansion,rows,masked", [(64, 4, 300, False), (64, 2, 77, True), (256, 4, 130, True)])
+def test_transition_widths(dt, c, expansion, rows, masked):
+    dtype = DTYPES[dt]
+    say(f"transition widths c={c} x{expansion} rows={rows} {dt} masked={masked}")
+    rng = np.random.default_rng(c + rows)
+    x = rng.standard_normal((rows, c)).astype(np.float32)
+    w = syn.transition_weights(c, expansion, seed=9)
+    rm = (rng.random(rows) > 0.3).astype(np.float32) if masked else None
+    tw = P.pack_transition_torch({k: w[k] for k in ("layer_norm", "linear_a", "linear_b", "linear_out")}, dtype, "cuda")
+    xt = device_tensor(x, dtype)
+    got = kernels.transition(xt, tw, row_mask=None if rm is None else device_tensor(rm, dtype), residual=xt)
+    torch.cuda.synchronize()
+    xr = prep(x, dtype)
+    want = xr + O.transition(xr, prep_tree(w, dtype), mask=rm)
+    assert_parity(to_np(got), want, dtype, f"transition c={c} x{expansion}")
+
+
+def test_template_stack_pair_block_bf16():
+    """One pair block at the template stack's widths (c_z = 64, c_h = 128,
+    4 heads of 32, transition x4) through the general paths, each residual
+    added by the kernels, against the oracle composition."""
+    dtype = DTYPES["bf16"]
+    n, n_real, c_z = 40, 36, 64
+    say(f"template pair block c_z={c_z} n={n} bf16")
+    z = syn.pair_input(n, c_z, seed=12)
+    pm = syn.pair_mask(n, n_real)
+    tm = [syn.trimul_weights(c_z, 128, seed=13 + i) for i in range(2)]
+    ta = [syn.triattn_weights(c_z, 4, 32, seed=15 + i) for i in range(2)]
+    tr = syn.transition_weights(c_z, 4, seed=17)
+    zt, mt = device_tensor(z, dtype), device_tensor(pm, dtype)
+    zt = protenix.triangle_multiplication(zt, mt, P.trimul_to_protenix(tm[0]), "outgoing", residual=zt)
+    zt = protenix.triangle_multiplication(zt, mt, P.trimul_to_protenix(tm[1]), "incoming", residual=zt)
+    zt = protenix.triangle_attention(zt, mt, P.triattn_to_protenix(ta[0]), num_heads=4, starting=True, residual=zt)
+    zt = protenix.triangle_attention(zt, mt, P.triattn_to_protenix(ta[1]), num_heads=4, starting=False, residual=zt)
+    zt = protenix.transition(zt, {k: tr[k] for k in ("layer_norm", "linear_a", "linear_b", "linear_out")}, residual=zt)
+    torch.cuda.synchronize()
+    ze = prep(z, dtype)
+    ze = ze + O.protenix_triangle_multiplication(ze, pm, prep_tree(tm[0], dtype), "outgoing")
+    ze = ze + O.protenix_triangle_multiplication(ze, pm, prep_tree(tm[1], dtype), "incoming")
+    ze = ze + O.protenix_triangle_attention(ze, pm, prep_tree(ta[0], dtype), num_heads=4, starting=True)
+    ze = ze + O.protenix_triangle_attention(ze, pm, prep_tree(ta[1], dtype), num_heads=4, starting=False)
+    ze = ze + O.transition(ze, prep_tree(tr, dtype))
+    v = slice(0, n_real)
+    assert_parity(to_np(zt)[v, v], ze[v, v], dtype, "template pair block")
