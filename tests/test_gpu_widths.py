@@ -104,3 +104,26 @@ def test_template_stack_pair_block_bf16():
     ze = ze + O.transition(ze, prep_tree(tr, dtype))
     v = slice(0, n_real)
     assert_parity(to_np(zt)[v, v], ze[v, v], dtype, "template pair block")
+
+
+@pytest.mark.parametrize("c_z,c_h", [(128, 128), (64, 128)])
+@pytest.mark.parametrize("n", [1, 2])
+def test_tiny_n_fused_and_general(c_z, c_h, n):
+    """One and two tokens on the fused (c = 128) and the general paths: tri-mul
+    both directions, tri-attn both nodes, bf16, against the oracle."""
+    dtype = DTYPES["bf16"]
+    say(f"tiny n={n} c_z={c_z} c_h={c_h}")
+    z = syn.pair_input(n, c_z, seed=21)
+    m = np.ones((n, n), np.float32)
+    w = syn.trimul_weights(c_z, c_h, seed=22)
+    wa = syn.triattn_weights(c_z, 4, 32, seed=23)
+    for direction in ("outgoing", "incoming"):
+        got = protenix.triangle_multiplication(device_tensor(z, dtype), device_tensor(m, dtype),
+                                               P.trimul_to_protenix(w), direction)
+        want = O.protenix_triangle_multiplication(prep(z, dtype), m, prep_tree(w, dtype), direction)
+        assert_parity(to_np(got), want, dtype, f"tiny trimul {direction}")
+    for starting in (True, False):
+        got = protenix.triangle_attention(device_tensor(z, dtype), device_tensor(m, dtype), P.triattn_to_protenix(wa),
+                                          num_heads=4, starting=starting)
+        want = O.protenix_triangle_attention(prep(z, dtype), m, prep_tree(wa, dtype), num_heads=4, starting=starting)
+        assert_parity(to_np(got), want, dtype, f"tiny triattn starting={starting}")
