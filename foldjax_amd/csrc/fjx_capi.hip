@@ -396,9 +396,7 @@ int transition_run(const fjx_transition_args* a, hipStream_t st) {
   p.out = static_cast<T*>(a->out);
   p.rows = a->rows;
   p.eps = a->eps;
-  // the 128-channel pair track and the 384-channel single track are timed apart
-  const int id = a->c == 128 ? K_TRANSITION : K_SINGLE_TRANSITION;
-  return timed(id, st, "transition", [&] { launch_transition<T>(p, (int)a->c, st); });
+  return timed(K_TRANSITION, st, "transition", [&] { launch_transition<T>(p, (int)a->c, st); });
 }
 
 // ------------------------------------------------- general-width paths
@@ -409,7 +407,7 @@ bool fused_trimul(int64_t c_z, int64_t c_h) { return c_z == 128 && c_h == 128; }
 bool fused_triattn(int64_t c_z, int64_t heads, int64_t head_dim) {
   return c_z == 128 && head_dim == 32 && heads * head_dim == 128;
 }
-bool fused_transition(int64_t c, int64_t hidden) { return (c == 128 || c == 384) && hidden == 4 * c; }
+bool fused_transition(int64_t c, int64_t hidden) { return c == 128 && hidden == 4 * c; }
 int64_t transition_hidden(const fjx_transition_args* a) { return a->hidden > 0 ? a->hidden : 4 * a->c; }
 
 template <typename T>
@@ -622,6 +620,7 @@ int transition_generic_run(const fjx_transition_args* a, hipStream_t st) {
   T* xn = at<T>(W, ws.xn);
   T* h = at<T>(W, ws.h);
   T* y = at<T>(W, ws.y);
+  // the 384-channel single track is timed apart from the pair track
   const int id = c == 384 ? K_SINGLE_TRANSITION : K_TRANSITION;
   return timed(id, st, "transition", [&] {
     launch_layernorm_rows<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_weight),

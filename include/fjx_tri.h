@@ -191,10 +191,11 @@ int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
  * (fc1 = w_a, fc2 = w_b, fc3 = w_o), protenix/models/primitives/primitives.py:117-146
  * and openfold3/models/primitives.py:133-150 (row_mask = the OpenFold3 mask).
  * Weights PyTorch [out, in]: w_a, w_b [hidden, c]; w_o [c, hidden]; hidden = 0
- * means 4c. Fused kernels (the hidden activations never leave the chip) serve
- * c in {128, 384} with hidden == 4c and need no workspace; other widths (c and
- * hidden multiples of 8, c <= 1024) run a general path of GEMMs through the
- * workspace of fjx_transition_workspace_size.
+ * means 4c. A fused kernel (the hidden activations never leave the chip)
+ * serves c == 128 with hidden == 4c and needs no workspace; every other width
+ * (c and hidden multiples of 8, c <= 1024; the single track's c = 384
+ * included) runs a general path of GEMMs through the workspace of
+ * fjx_transition_workspace_size.
  */
 typedef struct fjx_transition_args {
   int64_t rows;

@@ -87,7 +87,7 @@ def test_workspace_sizes_are_host_only(lib):
     assert lib.fjx_trimul_workspace_size(1, 64, 64, 128, _lib.FJX_DTYPE_BF16) > fused
     assert lib.fjx_triattn_workspace_size(1, 64, 64, 4, 32, _lib.FJX_DTYPE_BF16) > 0
     assert lib.fjx_transition_workspace_size(100, 128, 0, _lib.FJX_DTYPE_BF16) == 0  # fused: none
-    assert lib.fjx_transition_workspace_size(100, 384, 1536, _lib.FJX_DTYPE_BF16) == 0
+    assert lib.fjx_transition_workspace_size(100, 384, 1536, _lib.FJX_DTYPE_BF16) > 0  # single track: general path
     assert lib.fjx_transition_workspace_size(100, 64, 0, _lib.FJX_DTYPE_BF16) >= 100 * (64 + 256 + 64) * 2
 
 
