@@ -186,8 +186,12 @@ TriMulWs trimul_ws(int64_t batch, int64_t n, int32_t dtype) {
 }
 
 struct TriAttnWs {
-  size_t q, k, vt, bias, mb, o, total;
+  size_t q, k, vt, bias, mb, o, flags, total;
 };
+// one flag per workgroup of the 128-query flash launch (4 rows x 128 queries)
+size_t flash_flags_bytes(int64_t batch, int64_t rows, int64_t heads, int64_t np) {
+  return align_up((size_t)batch * heads * ((rows + 3) / 4) * ((np + 127) / 128) * sizeof(unsigned));
+}
 TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int32_t dtype, bool with_o) {
   const int64_t np = round64(n);
   const size_t es = esize(dtype);
@@ -206,6 +210,8 @@ TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int3
   off += align_up((size_t)batch * rows * np * sizeof(float));
   w.o = off;
   if (with_o) off += align_up((size_t)batch * rows * n * heads * 32 * es);
+  w.flags = off;
+  off += flash_flags_bytes(batch, rows, heads, np);
   w.total = off;
   return w;
 }
@@ -302,7 +308,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   int rc = timed(K_TRIATTN_PROLOGUE, st, "triattn_prologue", [&] { launch_triattn_prologue<T>(pp, a->batch, st); });
   if (rc) return rc;
 
-  FlashParams<T> fp;
+  FlashParams<T> fp = {};
   fp.q = pp.q;
   fp.k = pp.k;
   fp.vt = pp.vt;
@@ -318,6 +324,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   fp.o_stride_head = 32;
   fp.o_stride_q = 128;
   fp.bias_stride_b = a->heads * np * np;
+  fp.fallback = at<unsigned>(W, ws.flags);
   rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
   if (rc) return rc;
 
@@ -362,7 +369,7 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   });
   if (rc) return rc;
 
-  FlashParams<T> fp;
+  FlashParams<T> fp = {};
   fp.q = q;
   fp.k = k;
   fp.vt = vt;
@@ -378,6 +385,7 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   fp.o_stride_head = n * 32;
   fp.o_stride_q = 32;
   fp.bias_stride_b = a->heads * np * np;
+  fp.fallback = at<unsigned>(W, ws.flags);
   return timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
 }
 
@@ -508,7 +516,7 @@ int trimul_generic_run(const fjx_trimul_args* a, hipStream_t st) {
 }
 
 struct GenTriAttnWs {
-  size_t xn, proj, bias_pm, q, k, vt, bias, mb, o, y, total;
+  size_t xn, proj, bias_pm, q, k, vt, bias, mb, o, y, flags, total;
 };
 GenTriAttnWs gen_triattn_ws(int64_t batch, int64_t n, int64_t c_z, int64_t heads, int32_t dtype) {
   const int64_t np = round64(n), hd = 32 * heads;
@@ -530,6 +538,7 @@ GenTriAttnWs gen_triattn_ws(int64_t batch, int64_t n, int64_t c_z, int64_t heads
   w.mb = take((size_t)batch * n * np * sizeof(float));
   w.o = take(pos * hd);
   w.y = take(pos * c_z);
+  w.flags = take(flash_flags_bytes(batch, n, heads, np));
   w.total = off;
   return w;
 }
@@ -565,7 +574,7 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
   });
   if (rc) return rc;
 
-  FlashParams<T> fp;
+  FlashParams<T> fp = {};
   fp.q = at<T>(W, ws.q);
   fp.k = at<T>(W, ws.k);
   fp.vt = at<T>(W, ws.vt);
@@ -581,6 +590,7 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
   fp.o_stride_head = 32;
   fp.o_stride_q = hd;
   fp.bias_stride_b = H * np * np;
+  fp.fallback = at<unsigned>(W, ws.flags);
   rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, B, st); });
   if (rc) return rc;
 
@@ -708,7 +718,7 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
   });
   if (rc) return rc;
 
-  FlashParams<T> fp;
+  FlashParams<T> fp = {};
   fp.q = at<T>(W, ws.q);
   fp.k = at<T>(W, ws.k);
   fp.vt = at<T>(W, ws.vt);

@@ -91,7 +91,7 @@ template <> __device__ __forceinline__ f32x8 ones8<float>(bool on) {
 // accumulator whose A operand is 1 only in rows 4(qt%4) .. +3, so lane group
 // g holds the sums of tile 4(qt/4) + g -- padded queries have zero scores,
 // so the zero-weighted rows add nothing)
-template <typename T, int ROWS, int NQT>
+template <typename T, int ROWS, int NQT, bool FAST = false>
 __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   typedef typename Frag<T>::type FragT;
   constexpr int QTL = 16 * NQT;
@@ -100,6 +100,11 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   __shared__ __attribute__((aligned(16))) float bias_s[2][QTL][kBiasLd];
   __shared__ __attribute__((aligned(16))) FragT q_s[kQLds ? ROWS : 1][4][64];  // [wave][qt][lane]: B fragments of Q
   __shared__ __attribute__((aligned(16))) float mb_s[2][ROWS][kKB];  // each row's mask bias, one key block
+
+  // the offset path after a FAST launch: only the workgroups it flagged
+  if constexpr (!FAST && NQT == 8) {
+    if (P.fallback && P.fallback[blockIdx.x] == 0u) return;
+  }
 
   const int64_t n = P.n;
   const int64_t np = P.np;
@@ -133,6 +138,23 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   const T* BIAS = P.bias + b * P.bias_stride_b + h * np * np;
 
   const int64_t nblk = np / kKB;
+
+  // offset-free pass: a row with every key masked (no mask bias above -1e8)
+  // would sum to 0. Its softmax is that of the unmasked scores (the mask is
+  // the same constant on every key and cancels), so such a row drops the
+  // masked keys' bias and keeps only the -inf of the padded keys.
+  bool full_row = false;
+  if constexpr (FAST) {
+    // 16-byte loads over the whole padded row (np is a multiple of 128; the
+    // padded keys hold -inf), four in flight per lane
+    bool any_valid = false;
+#pragma unroll 4
+    for (int64_t k0 = 4 * lane; k0 < np; k0 += 256) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(MB + k0);
+      any_valid |= (v[0] > -1.0e8f) | (v[1] > -1.0e8f) | (v[2] > -1.0e8f) | (v[3] > -1.0e8f);
+    }
+    full_row = __builtin_amdgcn_ballot_w64(any_valid) == 0;
+  }
 
   // Q stays in LDS (in fragment order: conflict-free 16-byte reads) and is
   // re-read per key block, which leaves registers for a second V buffer
@@ -232,7 +254,14 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
       // the test is wave-uniform, a scalar branch
       if (masked_blk) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s[kt] += *reinterpret_cast<const f32x4*>(&mb_s[buf][wave][col_of(kt, lg)]);
+        for (int kt = 0; kt < 4; ++kt) {
+          f32x4 mv = *reinterpret_cast<const f32x4*>(&mb_s[buf][wave][col_of(kt, lg)]);
+          if (FAST && full_row) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mv[r] = mv[r] < -1.0e30f ? mv[r] : 0.f;
+          }
+          s[kt] += mv;
+        }
       }
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) mma(s[kt], kf[kt], qf);
@@ -241,6 +270,15 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) kf[kt] = load8(K + (kn + key_of(kt, li)) * kD + 8 * lg);
       }
+      float pv[4][4];
+      if constexpr (FAST) {
+        // no offset: exp2 of the raw log2-unit score; overflow or underflow
+        // of a whole row is caught after the last block
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pv[kt][r] = __builtin_amdgcn_exp2f(s[kt][r]);
+      } else {
       // this lane's 16 scores: a max3 tree (5 + 2 + 1)
       const float t0 = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
       const float t1 = fmaxf(fmaxf(s[0][3], s[1][0]), s[1][1]);
@@ -265,11 +303,11 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
         m[qt] = mnew;
       }
       const float mnew = m[qt];
-      float pv[4][4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) pv[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] - mnew);
+      }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         const float f[8] = {pv[2 * c][0], pv[2 * c][1], pv[2 * c][2], pv[2 * c][3],
@@ -294,6 +332,28 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   }
 
   if (!row_ok) return;
+  if constexpr (FAST) {
+    // every softmax sum in [2^-100, inf) and every output finite, checked on
+    // the bit patterns (this file is compiled without NaN semantics);
+    // otherwise the workgroup is left to the offset path
+    bool bad = false;
+#pragma unroll
+    for (int qt = 0; qt < NQT; ++qt) {
+      float ls;
+      if constexpr (kQLds) ls = lsum[qt][0];
+      else ls = __shfl(lsum[qt >> 2][0], 16 * (qt & 3) + li, 64);
+      const unsigned u = __float_as_uint(ls);
+      bad |= !(u >= 0x0D800000u && u < 0x7F800000u);
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) bad |= (__float_as_uint(o[dt][qt][r]) & 0x7F800000u) == 0x7F800000u;
+    }
+    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+      if (lane == 0) P.fallback[blockIdx.x] = 1u;
+      return;
+    }
+  }
   T* OUT = P.out + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head;
 #pragma unroll
   for (int qt = 0; qt < NQT; ++qt) {
@@ -324,6 +384,23 @@ __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2
   flash_tri_body<bf16, kRows, 8>(P);
 }
 
+// The same 128-query kernel without a softmax offset: p = exp2(s) straight
+// from the log2-unit scores, so no running max, no subtraction and no rescale
+// branch per query tile. Softmax is invariant to the offset, and exp2 of any
+// score in [-126, 127] is a normal float whose bf16 rounding is the same
+// relative error as with an offset; a row whose scores leave that range (or a
+// row with every key masked, whose sums underflow to 0) shows up as a sum
+// below 2^-100 or a non-finite value after its last block, and its workgroup
+// is then recomputed by the offset kernel above.
+__global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_tri8_fast_kernel_bf16(FlashParams<bf16> P) {
+  flash_tri_body<bf16, kRows, 8, true>(P);
+}
+
+__global__ void zero_flags_kernel(unsigned* __restrict__ f, int64_t count) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < count; i += (int64_t)gridDim.x * blockDim.x)
+    f[i] = 0u;
+}
+
 // bf16: 3 waves per SIMD (168 VGPRs) measured faster than 2 without spills;
 // the fp32 variant would spill heavily under that cap and keeps 2.
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
@@ -351,6 +428,13 @@ void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st) {
   if constexpr (std::is_same<T, bf16>::value) {
     if (!single && p.np % 128 == 0) {
       const dim3 grid8((unsigned)(batch * p.heads * rg * (p.np / 128)));
+      if (p.fallback) {
+        // offset-free pass, then the offset kernel for the workgroups it flagged
+        const int64_t nb = ((int64_t)grid8.x + 255) / 256;
+        hipLaunchKernelGGL(zero_flags_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, p.fallback,
+                           (int64_t)grid8.x);
+        hipLaunchKernelGGL(flash_tri8_fast_kernel_bf16, grid8, dim3(64 * kRows), 0, st, p);
+      }
       hipLaunchKernelGGL(flash_tri8_kernel_bf16, grid8, dim3(64 * kRows), 0, st, p);
     } else {
       hipLaunchKernelGGL(single ? flash_single_kernel_bf16 : flash_tri_kernel_bf16, grid, dim3(64 * kRows), 0, st, p);
