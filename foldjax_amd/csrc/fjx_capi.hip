@@ -188,9 +188,9 @@ TriMulWs trimul_ws(int64_t batch, int64_t n, int32_t dtype) {
 struct TriAttnWs {
   size_t q, k, vt, bias, mb, o, flags, total;
 };
-// one flag per workgroup of the 128-query flash launch (4 rows x 128 queries)
+// one flag per workgroup of the flash launch (4 rows x 64 or 128 queries)
 size_t flash_flags_bytes(int64_t batch, int64_t rows, int64_t heads, int64_t np) {
-  return align_up((size_t)batch * heads * ((rows + 3) / 4) * ((np + 127) / 128) * sizeof(unsigned));
+  return align_up((size_t)batch * heads * ((rows + 3) / 4) * ((np + 63) / 64) * sizeof(unsigned));
 }
 TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int32_t dtype, bool with_o) {
   const int64_t np = round64(n);

@@ -102,7 +102,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   __shared__ __attribute__((aligned(16))) float mb_s[2][ROWS][kKB];  // each row's mask bias, one key block
 
   // the offset path after a FAST launch: only the workgroups it flagged
-  if constexpr (!FAST && NQT == 8) {
+  if constexpr (!FAST) {
     if (P.fallback && P.fallback[blockIdx.x] == 0u) return;
   }
 
@@ -407,6 +407,11 @@ __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3
 void flash_tri_kernel_bf16(FlashParams<bf16> P) {
   flash_tri_body<bf16, kRows, 4>(P);
 }
+// its offset-free pass (as flash_tri8_fast_kernel_bf16)
+__global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
+void flash_tri_fast_kernel_bf16(FlashParams<bf16> P) {
+  flash_tri_body<bf16, kRows, 4, true>(P);
+}
 __global__ __launch_bounds__(64 * kRows) void flash_tri_kernel_f32(FlashParams<float> P) {
   flash_tri_body<float, kRows, 4>(P);
 }
@@ -421,26 +426,33 @@ __global__ __launch_bounds__(64 * kRows) void flash_single_kernel_f32(FlashParam
 }
 
 template <typename T>
-void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st) {
-  const int64_t rg = (p.rows + kRows - 1) / kRows;
-  const dim3 grid((unsigned)(batch * p.heads * rg * (p.np / kQT)));
-  const bool single = p.rows == 1;
+void launch_flash(const FlashParams<T>& p_in, int64_t batch, hipStream_t st) {
+  const int64_t rg = (p_in.rows + kRows - 1) / kRows;
+  const dim3 grid((unsigned)(batch * p_in.heads * rg * (p_in.np / kQT)));
+  const bool single = p_in.rows == 1;
+  // the offset kernels skip unflagged workgroups whenever `fallback` is set,
+  // so it stays set only where an offset-free pass fills the flags first
+  FlashParams<T> plain = p_in;
+  plain.fallback = nullptr;
   if constexpr (std::is_same<T, bf16>::value) {
-    if (!single && p.np % 128 == 0) {
-      const dim3 grid8((unsigned)(batch * p.heads * rg * (p.np / 128)));
-      if (p.fallback) {
-        // offset-free pass, then the offset kernel for the workgroups it flagged
-        const int64_t nb = ((int64_t)grid8.x + 255) / 256;
-        hipLaunchKernelGGL(zero_flags_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, p.fallback,
-                           (int64_t)grid8.x);
-        hipLaunchKernelGGL(flash_tri8_fast_kernel_bf16, grid8, dim3(64 * kRows), 0, st, p);
-      }
-      hipLaunchKernelGGL(flash_tri8_kernel_bf16, grid8, dim3(64 * kRows), 0, st, p);
-    } else {
-      hipLaunchKernelGGL(single ? flash_single_kernel_bf16 : flash_tri_kernel_bf16, grid, dim3(64 * kRows), 0, st, p);
+    if (single) {
+      hipLaunchKernelGGL(flash_single_kernel_bf16, grid, dim3(64 * kRows), 0, st, plain);
+      return;
     }
+    const FlashParams<T>& p = p_in;
+    const bool q128 = p.np % 128 == 0;
+    const dim3 g = q128 ? dim3((unsigned)(batch * p.heads * rg * (p.np / 128))) : grid;
+    if (p.fallback) {
+      // offset-free pass, then the offset kernel for the workgroups it flagged
+      const int64_t nb = ((int64_t)g.x + 255) / 256;
+      hipLaunchKernelGGL(zero_flags_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, p.fallback,
+                         (int64_t)g.x);
+      hipLaunchKernelGGL(q128 ? flash_tri8_fast_kernel_bf16 : flash_tri_fast_kernel_bf16, g, dim3(64 * kRows), 0, st,
+                         p);
+    }
+    hipLaunchKernelGGL(q128 ? flash_tri8_kernel_bf16 : flash_tri_kernel_bf16, g, dim3(64 * kRows), 0, st, p);
   } else
-    hipLaunchKernelGGL(single ? flash_single_kernel_f32 : flash_tri_kernel_f32, grid, dim3(64 * kRows), 0, st, p);
+    hipLaunchKernelGGL(single ? flash_single_kernel_f32 : flash_tri_kernel_f32, grid, dim3(64 * kRows), 0, st, plain);
 }
 
 template void launch_flash<bf16>(const FlashParams<bf16>&, int64_t, hipStream_t);

@@ -123,8 +123,8 @@ struct FlashParams {
   int64_t o_stride_head;
   int64_t o_stride_q;
   int64_t bias_stride_b;  // 0 when one bias is shared by all batches
-  // the 128-query bf16 path without a softmax offset (see fjx_flash.hip): one
-  // flag per workgroup of that launch, or null for the offset path only
+  // the bf16 pair-track path without a softmax offset (see fjx_flash.hip):
+  // one flag per workgroup of that launch, or null for the offset path only
   unsigned* fallback;
 };
 
