@@ -25,7 +25,7 @@ FJX_ERR_UNSUPPORTED = 2
 FJX_ERR_WORKSPACE = 3
 FJX_ERR_HIP = 4
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -76,6 +76,8 @@ class TransitionArgs(ctypes.Structure):
         ("w_a", _vp), ("w_b", _vp), ("w_o", _vp),
         ("row_mask", _vp), ("residual", _vp), ("out", _vp),
         ("hidden", _i64), ("workspace", _vp), ("workspace_bytes", _sz),
+        ("pb_n", _i64), ("pb_heads", _i64), ("pb_eps", _f32),
+        ("pb_norm_weight", _vp), ("pb_norm_bias", _vp), ("pb_weight", _vp), ("pb_out", _vp),
     ]
 
 
@@ -90,6 +92,7 @@ class SingleAttentionArgs(ctypes.Structure):
         ("g_weight", _vp), ("o_weight", _vp),
         ("residual", _vp), ("out", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("pair_bias", _vp),
     ]
 
 
@@ -103,6 +106,7 @@ SYMBOLS = {
     "fjx_triattn_core": (ctypes.c_int, [ctypes.POINTER(TriAttnCoreArgs), _vp]),
     "fjx_transition_workspace_size": (_sz, [_i64, _i64, _i64, _i32]),
     "fjx_transition_fwd": (ctypes.c_int, [ctypes.POINTER(TransitionArgs), _vp]),
+    "fjx_pair_bias_size": (_sz, [_i64, _i64, _i64, _i32]),
     "fjx_single_attention_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "fjx_single_attention_fwd": (ctypes.c_int, [ctypes.POINTER(SingleAttentionArgs), _vp]),
     "fjx_last_error": (ctypes.c_char_p, []),

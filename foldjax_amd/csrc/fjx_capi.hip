@@ -391,8 +391,8 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
 
 // -------------------------------------------------------- transition body
 template <typename T>
-int transition_run(const fjx_transition_args* a, hipStream_t st) {
-  TransitionParams<T> p;
+int transition_run(const fjx_transition_args* a, bool pb_fused, hipStream_t st) {
+  TransitionParams<T> p = {};
   p.x = static_cast<const T*>(a->x);
   p.ln_w = static_cast<const T*>(a->norm_weight);
   p.ln_b = static_cast<const T*>(a->norm_bias);
@@ -404,7 +404,34 @@ int transition_run(const fjx_transition_args* a, hipStream_t st) {
   p.out = static_cast<T*>(a->out);
   p.rows = a->rows;
   p.eps = a->eps;
-  return timed(K_TRANSITION, st, "transition", [&] { launch_transition<T>(p, (int)a->c, st); });
+  if (pb_fused) {
+    p.pb_ln_w = static_cast<const T*>(a->pb_norm_weight);
+    p.pb_ln_b = static_cast<const T*>(a->pb_norm_bias);
+    p.pb_w = static_cast<const T*>(a->pb_weight);
+    p.pb_out = static_cast<T*>(a->pb_out);
+    p.pb_n = a->pb_n;
+    p.pb_np = round64(a->pb_n);
+    p.pb_heads = (int)a->pb_heads;
+    p.pb_eps = a->pb_eps;
+  }
+  return timed(K_TRANSITION, st, "transition", [&] {
+    if (pb_fused)
+      launch_pair_bias_border<T>(p.pb_out, a->rows / (a->pb_n * a->pb_n) * a->pb_heads, a->pb_n, p.pb_np, st);
+    launch_transition<T>(p, (int)a->c, st);
+  });
+}
+
+// the pair-bias output of a transition that could not fuse it: the same
+// projection as the single attention's own, over the transition's output
+template <typename T>
+int transition_pair_bias_pass(const fjx_transition_args* a, hipStream_t st) {
+  const int64_t batch = a->rows / (a->pb_n * a->pb_n);
+  return timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
+    launch_pair_bias<T>(static_cast<const T*>(a->out), static_cast<const T*>(a->pb_norm_weight),
+                        static_cast<const T*>(a->pb_norm_bias), static_cast<const T*>(a->pb_weight),
+                        static_cast<T*>(a->pb_out), batch, a->pb_n, round64(a->pb_n), (int)a->pb_heads, a->pb_eps,
+                        st);
+  });
 }
 
 // ------------------------------------------------- general-width paths
@@ -711,18 +738,20 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
     launch_key_mask<T>(static_cast<const T*>(a->mask), at<float>(W, ws.mb), B, n, np, a->inf, st);
   });
   if (rc) return rc;
-  rc = timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
-    launch_pair_bias<T>(static_cast<const T*>(a->z), static_cast<const T*>(a->z_norm_weight),
-                        static_cast<const T*>(a->z_norm_bias), static_cast<const T*>(a->z_weight), at<T>(W, ws.bias),
-                        B, n, np, (int)H, a->eps, st);
-  });
-  if (rc) return rc;
+  if (!a->pair_bias) {
+    rc = timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
+      launch_pair_bias<T>(static_cast<const T*>(a->z), static_cast<const T*>(a->z_norm_weight),
+                          static_cast<const T*>(a->z_norm_bias), static_cast<const T*>(a->z_weight),
+                          at<T>(W, ws.bias), B, n, np, (int)H, a->eps, st);
+    });
+    if (rc) return rc;
+  }
 
   FlashParams<T> fp = {};
   fp.q = at<T>(W, ws.q);
   fp.k = at<T>(W, ws.k);
   fp.vt = at<T>(W, ws.vt);
-  fp.bias = at<T>(W, ws.bias);
+  fp.bias = a->pair_bias ? static_cast<const T*>(a->pair_bias) : at<T>(W, ws.bias);
   fp.mb = at<float>(W, ws.mb);
   fp.out = at<T>(W, ws.o);
   fp.n = n;
@@ -892,13 +921,43 @@ int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
     return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a required pointer is NULL");
   if (!aligned16({a->x, a->out, a->residual, a->norm_weight, a->norm_bias, a->w_a, a->w_b, a->w_o}))
     return fail(FJX_ERR_INVALID, "fjx_transition_fwd: tensors must be 16-byte aligned");
-  if (fused_transition(a->c, hid))
-    return a->dtype == FJX_DTYPE_BF16 ? transition_run<bf16>(a, st) : transition_run<float>(a, st);
-  const size_t need = fjx_transition_workspace_size(a->rows, a->c, hid, a->dtype);
-  if (!a->workspace || a->workspace_bytes < need)
-    return fail(FJX_ERR_WORKSPACE, "fjx_transition_fwd: workspace of %zu bytes needed, %zu given", need,
-                a->workspace_bytes);
-  return a->dtype == FJX_DTYPE_BF16 ? transition_generic_run<bf16>(a, st) : transition_generic_run<float>(a, st);
+  if (a->pb_out) {
+    if (a->c != 128)
+      return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: the pair-bias output needs c == 128; got c=%lld",
+                  (long long)a->c);
+    if (a->pb_n < 1 || a->pb_n > 65535 || a->pb_heads < 1 || a->pb_heads > 1024 || a->rows % (a->pb_n * a->pb_n))
+      return fail(FJX_ERR_INVALID,
+                  "fjx_transition_fwd: the pair-bias output needs 1 <= pb_n <= 65535, 1 <= pb_heads <= 1024 and "
+                  "rows a multiple of pb_n^2; got rows=%lld pb_n=%lld pb_heads=%lld",
+                  (long long)a->rows, (long long)a->pb_n, (long long)a->pb_heads);
+    if (!grid_ok(a->pb_n, a->rows / (a->pb_n * a->pb_n)))
+      return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: the pair-bias batch is too large");
+    if (!a->pb_norm_weight || !a->pb_norm_bias || !a->pb_weight)
+      return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a pair-bias weight pointer is NULL");
+    if (!aligned16({a->pb_norm_weight, a->pb_norm_bias, a->pb_weight, a->pb_out}))
+      return fail(FJX_ERR_INVALID, "fjx_transition_fwd: tensors must be 16-byte aligned");
+  }
+  const bool bf = a->dtype == FJX_DTYPE_BF16;
+  int rc;
+  bool pb_fused = false;
+  if (fused_transition(a->c, hid)) {
+    pb_fused = a->pb_out && a->pb_heads <= 16;
+    rc = bf ? transition_run<bf16>(a, pb_fused, st) : transition_run<float>(a, pb_fused, st);
+  } else {
+    const size_t need = fjx_transition_workspace_size(a->rows, a->c, hid, a->dtype);
+    if (!a->workspace || a->workspace_bytes < need)
+      return fail(FJX_ERR_WORKSPACE, "fjx_transition_fwd: workspace of %zu bytes needed, %zu given", need,
+                  a->workspace_bytes);
+    rc = bf ? transition_generic_run<bf16>(a, st) : transition_generic_run<float>(a, st);
+  }
+  if (rc || !a->pb_out || pb_fused) return rc;
+  return bf ? transition_pair_bias_pass<bf16>(a, st) : transition_pair_bias_pass<float>(a, st);
+}
+
+size_t fjx_pair_bias_size(int64_t batch, int64_t n, int64_t heads, int32_t dtype) {
+  if (batch < 1 || n < 1 || heads < 1 || !dtype_ok(dtype)) return 0;
+  const int64_t np = round64(n);
+  return (size_t)batch * heads * np * np * esize(dtype);
 }
 
 size_t fjx_single_attention_workspace_size(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype) {
@@ -912,7 +971,7 @@ int fjx_single_attention_fwd(const fjx_single_attention_args* a, hipStream_t st)
   if (a->batch < 1 || a->n < 1 || a->heads < 1)
     return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: batch, n and heads must be >= 1");
   if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: unknown dtype %d", a->dtype);
-  if (a->c_z != 128 || a->c_s % a->heads != 0 || a->c_s / a->heads > 32 || a->c_s > 1024)
+  if ((!a->pair_bias && a->c_z != 128) || a->c_s % a->heads != 0 || a->c_s / a->heads > 32 || a->c_s > 1024)
     return fail(FJX_ERR_UNSUPPORTED,
                 "fjx_single_attention_fwd: this build supports c_z == 128, heads dividing c_s <= 1024 with "
                 "head_dim <= 32; got c_s=%lld c_z=%lld heads=%lld",
@@ -920,13 +979,12 @@ int fjx_single_attention_fwd(const fjx_single_attention_args* a, hipStream_t st)
   if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_single_attention_fwd: n or batch too large");
   if ((a->pre_norm_weight == nullptr) != (a->pre_norm_bias == nullptr))
     return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: pre_norm weight and bias must both be given or both NULL");
-  if (!a->s || !a->z || !a->out || !a->z_norm_weight ||
-      !a->z_norm_bias || !a->z_weight || !a->q_weight || !a->k_weight || !a->v_weight || !a->g_weight ||
-      !a->o_weight)
+  if (!a->s || !a->out || !a->q_weight || !a->k_weight || !a->v_weight || !a->g_weight || !a->o_weight ||
+      (!a->pair_bias && (!a->z || !a->z_norm_weight || !a->z_norm_bias || !a->z_weight)))
     return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: a required pointer is NULL");
   if (!aligned16({a->s, a->z, a->out, a->residual, a->pre_norm_weight, a->pre_norm_bias, a->z_norm_weight,
                   a->z_norm_bias, a->z_weight, a->q_weight, a->q_bias, a->k_weight, a->v_weight, a->g_weight,
-                  a->o_weight}))
+                  a->o_weight, a->pair_bias}))
     return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: tensors must be 16-byte aligned");
   const size_t need = single_ws(a->batch, a->n, a->c_s, a->heads, a->dtype).total;
   if (!a->workspace || a->workspace_bytes < need)

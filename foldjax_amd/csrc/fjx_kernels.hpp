@@ -104,6 +104,18 @@ struct TransitionParams {
   T* out;             // [rows][C]
   int64_t rows;
   float eps;
+  // optional pair-bias epilogue (pb_out null: off): rows are the positions
+  // (b, r, s) of [B, pb_n, pb_n]; pb_out[b][h][r][s] = log2(e) *
+  // LN_pb(out row) . pb_w[h] in the padded [B, pb_heads, pb_np, pb_np]
+  // layout the flash kernel reads; pb_heads <= 16
+  const T* pb_ln_w;
+  const T* pb_ln_b;
+  const T* pb_w;      // [pb_heads][C]
+  T* pb_out;
+  int64_t pb_n;
+  int64_t pb_np;
+  int pb_heads;
+  float pb_eps;
 };
 
 template <typename T>
@@ -152,6 +164,8 @@ void launch_split_heads(const T* qkv, int64_t ld, int64_t batch, int64_t n, int6
 template <typename T>
 void launch_pair_bias(const T* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
                       int64_t np, int heads, float eps, hipStream_t st);
+template <typename T>
+void launch_pair_bias_border(T* bias, int64_t planes, int64_t n, int64_t np, hipStream_t st);
 template <typename T>
 void launch_key_mask(const T* mask, float* mb, int64_t batch, int64_t n, int64_t np, float inf, hipStream_t st);
 template <typename T>

@@ -153,6 +153,30 @@ __global__ __launch_bounds__(512) void pair_bias_kernel(const T* __restrict__ z,
   }
 }
 
+// zeros of a prepared pair bias outside the [n, n] block of each padded
+// [np, np] plane: rows r < n, columns n .. np-1, then rows n .. np-1 whole
+// (the transition's fused epilogue writes only the real positions)
+template <typename T>
+__global__ void pair_bias_border_kernel(T* __restrict__ bias, int64_t planes, int64_t n, int64_t np) {
+  const int64_t w = np - n;
+  const int64_t per = n * w + w * np;
+  const int64_t total = planes * per;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t plane = idx / per;
+    int64_t j = idx - plane * per;
+    int64_t r, c;
+    if (j < n * w) {
+      r = j / w;
+      c = n + (j - r * w);
+    } else {
+      j -= n * w;
+      r = n + j / np;
+      c = j - (r - n) * np;
+    }
+    bias[(plane * np + r) * np + c] = from_f32<T>(0.f);
+  }
+}
 
 // mb[b][k] = log2(e) * (1 - mask[b,k]) * (-inf_const), -inf for padded keys
 template <typename T>
@@ -214,6 +238,12 @@ void launch_pair_bias(const T* z, const T* ln_w, const T* ln_b, const T* w, T* b
                      ntiles);
 }
 template <typename T>
+void launch_pair_bias_border(T* bias, int64_t planes, int64_t n, int64_t np, hipStream_t st) {
+  if (np == n) return;
+  hipLaunchKernelGGL(pair_bias_border_kernel<T>, grid_stride(planes * (n * (np - n) + (np - n) * np)), dim3(256), 0,
+                     st, bias, planes, n, np);
+}
+template <typename T>
 void launch_key_mask(const T* mask, float* mb, int64_t batch, int64_t n, int64_t np, float inf, hipStream_t st) {
   hipLaunchKernelGGL(key_mask_kernel<T>, grid_stride(batch * np), dim3(256), 0, st, mask, mb, batch, n, np, inf);
 }
@@ -230,6 +260,7 @@ void launch_gate_unpad(const T* o, const T* g, int64_t ldg, T* out, int64_t rows
                                       hipStream_t);                                                              \
   template void launch_pair_bias<T>(const T*, const T*, const T*, const T*, T*, int64_t, int64_t, int64_t, int,  \
                                     float, hipStream_t);                                                         \
+  template void launch_pair_bias_border<T>(T*, int64_t, int64_t, int64_t, hipStream_t);                        \
   template void launch_key_mask<T>(const T*, float*, int64_t, int64_t, int64_t, float, hipStream_t);             \
   template void launch_gate_unpad<T>(const T*, const T*, int64_t, T*, int64_t, int, int, hipStream_t);
 FJX_INST(bf16)

@@ -19,6 +19,57 @@ __device__ __forceinline__ float silu(float x) { return x * __builtin_amdgcn_rcp
 
 }  // namespace
 
+// The attention-with-pair-bias projection of the transition's output rows,
+// fused so that the pair tensor is not read again: the rows (as stored, in
+// T) are in xs; they are LayerNormed in place with the attention's pair norm
+// and multiplied by its [heads][128] weight. Wave w owns rows 16w .. 16w+15
+// of the tile, and a lane holds 4 consecutive rows (positions) of head
+// l % 16, stored as bias[b][h][r][s] * log2(e).
+template <typename T>
+__device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P, T (*xs)[tile::kLd],
+                                                   const tile::LnAffine& ln, const tile::WCol<T>& wf,
+                                                   int64_t m0, int nvalid) {
+  using namespace tile;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int p = t >> 2;
+  __syncthreads();
+  {
+    RowPart<T> yr;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) yr.f[q] = load8(&xs[p][row_chunk(q)]);
+    ln_quad<T>(yr, ln, P.pb_eps, &xs[p][0]);  // each thread rewrites only the chunks it read
+  }
+  __syncthreads();
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) mma(acc, load8(&xs[16 * wave + li][32 * ks + 8 * lg]), wf[ks]);
+  const int pos0 = 16 * wave + 4 * lg;
+  if (li >= P.pb_heads || pos0 >= nvalid) return;
+  const int64_t n = P.pb_n, nn = n * n, np = P.pb_np;
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = acc[q] * kLog2e;
+  if ((n & 3) == 0) {
+    // rows = B n^2 is then a multiple of 16, so nvalid is too, and the 4
+    // positions share (b, r) with s a multiple of 4 (aligned stores)
+    const int64_t m = m0 + pos0;
+    const int64_t b = m / nn, rem = m - b * nn, r = rem / n, c = rem - r * n;
+    store4f(P.pb_out + ((b * P.pb_heads + li) * np + r) * np + c, v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (pos0 + q >= nvalid) break;
+      const int64_t m = m0 + pos0 + q;
+      const int64_t b = m / nn, rem = m - b * nn, r = rem / n, c = rem - r * n;
+      P.pb_out[((b * P.pb_heads + li) * np + r) * np + c] = from_f32<T>(v[q]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Pair-track transition (C = 128, hidden 512): 128-row tiles, 512 threads.
 // Wave w owns hidden columns 16w .. 16w+15 of every 128-wide hidden chunk and
@@ -34,6 +85,7 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];  // LN(x)
   __shared__ __attribute__((aligned(16))) T hs[kTP][kLd];  // silu(a) * b, one hidden chunk
   __shared__ __attribute__((aligned(16))) LnAffine ln;
+  __shared__ __attribute__((aligned(16))) LnAffine pb_ln;  // the pair-bias epilogue's norm
 
   const int64_t m0 = (int64_t)blockIdx.x * kTP;
   const int nvalid = (int)min<int64_t>(kTP, P.rows - m0);
@@ -47,6 +99,7 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
     RowPart<T> xr;
     load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
     stage_ln<T>(P.ln_w, P.ln_b, ln);
+    if (P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
     __syncthreads();
     ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
   }
@@ -78,26 +131,60 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
     __syncthreads();  // hs is rewritten by the next chunk
   }
 
+  // the pair-bias weight (rows = heads, zero past pb_heads) is fetched ahead
+  // of the output stores so that its latency is not exposed after them
+  WCol<T> pb_wf;
+  if (P.pb_out) {
+    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int h = lane & 15;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      pb_wf[ks] = h < P.pb_heads ? load8(P.pb_w + (int64_t)h * kC + 32 * ks + 8 * (lane >> 4)) : pack8<T>(zero);
+  }
+
+  // every row tile's row mask and residual are loaded before the first
+  // store: a store counts against the same memory counter a load's use
+  // waits on, so loads between stores would each wait for the stores
+  // before (rows past the tile's end read the last valid row, unused), with
+  // no per-lane branch around them
+  float res[8][4], msk[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) {
+    msk[rt] = 1.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) res[rt][q] = 0.f;
+  }
+  if (P.residual) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) {
+      const int row = min(16 * rt + (lane & 15), nvalid - 1);
+      load4f(P.residual + (m0 + row) * kC + col + 4 * (lane >> 4), res[rt]);
+    }
+  }
+  if (P.row_mask) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt) msk[rt] = to_f32(P.row_mask[m0 + min(16 * rt + (lane & 15), nvalid - 1)]);
+  }
+
   // the update is rounded to T (the reference's projection output is), then
   // the residual is added
 #pragma unroll
   for (int rt = 0; rt < 8; ++rt) {
     const int row = 16 * rt + (lane & 15);
     if (row < nvalid) {
-      const float m = P.row_mask ? to_f32(P.row_mask[m0 + row]) : 1.0f;
       const int64_t off = (m0 + row) * kC + col + 4 * (lane >> 4);
       float y[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) y[q] = round_to<T>(out[rt][q] * m);
+      for (int q = 0; q < 4; ++q) y[q] = round_to<T>(out[rt][q] * msk[rt]);
       if (P.residual) {
-        float r[4];
-        load4f(P.residual + off, r);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) y[q] += r[q];
+        for (int q = 0; q < 4; ++q) y[q] += res[rt][q];
       }
       store4f(P.out + off, y);
+      if (P.pb_out) store4f(&xs[row][col + 4 * (lane >> 4)], y);  // xs is free after the last chunk
     }
   }
+  if (P.pb_out) pair_bias_epilogue<T>(P, xs, pb_ln, pb_wf, m0, nvalid);
 }
 
 // C = 128 only; other widths take the general path of the C ABI layer (row

@@ -134,15 +134,34 @@ def transition(
     row_mask: torch.Tensor | None = None,
     residual: torch.Tensor | None = None,
     eps: float = 1e-5,
-) -> torch.Tensor:
+    pair_bias_for: SingleAttentionWeights | None = None,
+    pair_bias_eps: float = 1e-5,
+):
     """``(silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T [* row_mask] [+ residual]``
-    over the last axis (``fjx_transition_fwd``)."""
+    over the last axis (``fjx_transition_fwd``).
+
+    ``pair_bias_for``: the weights of the single attention that reads this
+    pair transition's output next (``x`` is then ``[..., N, N, 128]``). The
+    call returns ``(out, pair_bias)``, ``pair_bias`` being that attention's
+    bias ``LN_z(out) w_z^T`` (eps ``pair_bias_eps``) prepared in the
+    library's ``[B, H, Np, Np]`` layout, for ``single_attention(...,
+    pair_bias=...)``; with 128 channels, a 4x hidden width and at most 16
+    heads it is computed in the transition's epilogue, so the pair tensor is
+    not read again."""
     _dev(x)
     c = int(x.shape[-1])
     rows = x.numel() // max(c, 1)
     xf = x.contiguous()
     lib = _lib.load()
     out = torch.empty_like(xf)
+    pb = None
+    pb_n = pb_heads = 0
+    if pair_bias_for is not None:
+        if x.dim() < 3 or x.shape[-3] != x.shape[-2]:
+            raise ValueError(f"a pair-bias output needs a pair tensor [..., N, N, C], got {tuple(x.shape)}")
+        pb_n, pb_heads = int(x.shape[-2]), pair_bias_for.heads
+        np_ = (pb_n + 63) // 64 * 64
+        pb = torch.empty((rows // (pb_n * pb_n), pb_heads, np_, np_), dtype=x.dtype, device=x.device)
     rm = None
     if row_mask is not None:
         rm = torch.broadcast_to(row_mask, x.shape[:-1]).to(dtype=x.dtype).contiguous()
@@ -157,34 +176,55 @@ def transition(
         row_mask=_ptr(rm), residual=_ptr(res), out=_ptr(out),
         hidden=hidden, workspace=_ptr(ws), workspace_bytes=ws_bytes,
     )
+    if pb is not None:
+        a.pb_n, a.pb_heads, a.pb_eps = pb_n, pb_heads, float(pair_bias_eps)
+        a.pb_norm_weight = _ptr(pair_bias_for.z_norm_weight)
+        a.pb_norm_bias = _ptr(pair_bias_for.z_norm_bias)
+        a.pb_weight = _ptr(pair_bias_for.z_weight)
+        a.pb_out = _ptr(pb)
+        _check_weights(x, pair_bias_for)
     _check_weights(x, w)
     _lib.check(lib.fjx_transition_fwd(ctypes.byref(a), _stream(x)))
-    return out
+    return out if pb is None else (out, pb)
 
 
 def single_attention(
     s: torch.Tensor,
-    z: torch.Tensor,
+    z: torch.Tensor | None,
     mask: torch.Tensor | None,
     w: SingleAttentionWeights,
     *,
     inf: float = 1e6,
     eps: float = 1e-5,
     residual: torch.Tensor | None = None,
+    pair_bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Single-track attention with pair bias (``fjx_single_attention_fwd``).
     ``s`` ``[B, N, c_s]`` (or ``[N, c_s]``), ``z`` ``[B, N, N, c_z]``, ``mask``
-    ``[B, N]`` token mask. Returns the update, or ``residual + update``."""
+    ``[B, N]`` token mask. Returns the update, or ``residual + update``.
+    ``pair_bias``: the bias ``transition(..., pair_bias_for=w)`` prepared from
+    this ``z``; ``z`` is then not read (and may be None)."""
     _dev(s)
     squeeze = s.dim() == 2
     sb = s.unsqueeze(0) if squeeze else s
-    zb = z.unsqueeze(0) if z.dim() == 3 else z
     batch, n, c_s = (int(v) for v in sb.shape)
-    c_z = int(zb.shape[-1])
-    if tuple(zb.shape[:3]) != (batch, n, n):
-        raise ValueError(f"z must be [{batch}, {n}, {n}, c_z], got {tuple(z.shape)}")
+    zb = None
+    c_z = 0
+    if z is not None:
+        zb = z.unsqueeze(0) if z.dim() == 3 else z
+        c_z = int(zb.shape[-1])
+        if tuple(zb.shape[:3]) != (batch, n, n):
+            raise ValueError(f"z must be [{batch}, {n}, {n}, c_z], got {tuple(z.shape)}")
+        zb = zb.to(dtype=s.dtype).contiguous()
+    if pair_bias is not None:
+        np_ = (n + 63) // 64 * 64
+        if (tuple(pair_bias.shape) != (batch, w.heads, np_, np_) or pair_bias.dtype != s.dtype
+                or pair_bias.device != s.device or not pair_bias.is_contiguous()):
+            raise ValueError(f"pair_bias must be the prepared [{batch}, {w.heads}, {np_}, {np_}] {s.dtype} bias, "
+                             f"got {tuple(pair_bias.shape)} {pair_bias.dtype}")
+    elif zb is None:
+        raise ValueError("single_attention needs z or a prepared pair_bias")
     sb = sb.contiguous()
-    zb = zb.to(dtype=s.dtype).contiguous()
     mb = None
     if mask is not None:
         mb = torch.broadcast_to(mask, (batch, n)).to(dtype=s.dtype).contiguous()
@@ -204,6 +244,7 @@ def single_attention(
         q_weight=_ptr(w.q_weight), q_bias=_ptr(w.q_bias), k_weight=_ptr(w.k_weight), v_weight=_ptr(w.v_weight),
         g_weight=_ptr(w.g_weight), o_weight=_ptr(w.o_weight),
         residual=_ptr(res), out=_ptr(out), workspace=_ptr(ws), workspace_bytes=ws_bytes,
+        pair_bias=_ptr(pair_bias),
     )
     _check_weights(s, w)
     _lib.check(lib.fjx_single_attention_fwd(ctypes.byref(a), _stream(s)))

@@ -55,10 +55,13 @@ class PairformerLayerWeights:
     def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor | None, pair_mask: torch.Tensor | None,
                 eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
         """``B2K/pairformer.py:133-205``: z += tri-mul out, in, tri-attn start,
-        end, transition; s += attention(LN(s), z, mask); s += transition_s."""
+        end, transition; s += attention(LN(s), z, mask); s += transition_s.
+        The attention's pair bias LN_z(z) w_z^T comes out of the pair
+        transition's epilogue, so z is not read a further time."""
         z = self.triangle.forward(z, pair_mask)
-        z = kernels.transition(z, self.transition_z, residual=z, eps=eps)
-        s = kernels.single_attention(s, z, mask, self.attention, residual=s, eps=eps)
+        z, bias = kernels.transition(z, self.transition_z, residual=z, eps=eps, pair_bias_for=self.attention,
+                                     pair_bias_eps=eps)
+        s = kernels.single_attention(s, None, mask, self.attention, residual=s, eps=eps, pair_bias=bias)
         s = kernels.transition(s, self.transition_s, residual=s, eps=eps)
         return s, z
 

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FJX_ABI_VERSION 2
+#define FJX_ABI_VERSION 3
 
 /* element types of activations, masks and weights */
 enum { FJX_DTYPE_F32 = 0, FJX_DTYPE_BF16 = 1 };
@@ -196,6 +196,18 @@ int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
  * (c and hidden multiples of 8, c <= 1024; the single track's c = 384
  * included) runs a general path of GEMMs through the workspace of
  * fjx_transition_workspace_size.
+ *
+ * Optional pair-bias output (pb_out non-NULL; c == 128): the pair block's
+ * transition is followed by the single attention with pair bias, whose bias
+ * LN_z(z) w_z^T reads the whole pair tensor again
+ * (src/foldjax/models/boltz2/models/trunk_blocks/pairformer.py:173-201).
+ * With pb_out set, the rows are taken as the positions (b, i, j) of
+ * [rows / pb_n^2, pb_n, pb_n] and the transition also writes that bias of its
+ * own output (pb_norm_*, pb_weight [pb_heads, c], pb_eps: the attention's
+ * z_norm_*, z_weight and eps) into pb_out, fjx_pair_bias_size bytes in a
+ * library-internal layout that fjx_single_attention_fwd takes as pair_bias.
+ * Fused into the transition's epilogue when c == 128, hidden == 4c and
+ * pb_heads <= 16; computed from out by a separate pass otherwise.
  */
 typedef struct fjx_transition_args {
   int64_t rows;
@@ -214,9 +226,18 @@ typedef struct fjx_transition_args {
   int64_t hidden;        /* 0 for 4c */
   void* workspace;       /* general path only; may be NULL when the size is 0 */
   size_t workspace_bytes;
+  int64_t pb_n;          /* pair-bias output, see above; ignored when pb_out is NULL */
+  int64_t pb_heads;
+  float pb_eps;
+  const void* pb_norm_weight;  /* [c] */
+  const void* pb_norm_bias;
+  const void* pb_weight;       /* [pb_heads, c] */
+  void* pb_out;                /* fjx_pair_bias_size(rows / pb_n^2, pb_n, pb_heads, dtype) bytes, or NULL */
 } fjx_transition_args;
 
 size_t fjx_transition_workspace_size(int64_t rows, int64_t c, int64_t hidden, int32_t dtype);
+/* Bytes of a prepared pair bias (the pb_out / pair_bias buffer). */
+size_t fjx_pair_bias_size(int64_t batch, int64_t n, int64_t heads, int32_t dtype);
 int fjx_transition_fwd(const fjx_transition_args* args, hipStream_t stream);
 
 /*
@@ -258,6 +279,8 @@ typedef struct fjx_single_attention_args {
   void* out;            /* [batch, n, c_s]; may equal s when residual == s */
   void* workspace;
   size_t workspace_bytes;
+  const void* pair_bias; /* a bias prepared by fjx_transition_fwd's pb_out for this z, or NULL;
+                            when given, z, z_norm_* and z_weight are not read and may be NULL */
 } fjx_single_attention_args;
 
 size_t fjx_single_attention_workspace_size(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype);

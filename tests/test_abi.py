@@ -89,6 +89,10 @@ def test_workspace_sizes_are_host_only(lib):
     assert lib.fjx_transition_workspace_size(100, 128, 0, _lib.FJX_DTYPE_BF16) == 0  # fused: none
     assert lib.fjx_transition_workspace_size(100, 384, 1536, _lib.FJX_DTYPE_BF16) > 0  # single track: general path
     assert lib.fjx_transition_workspace_size(100, 64, 0, _lib.FJX_DTYPE_BF16) >= 100 * (64 + 256 + 64) * 2
+    # the prepared pair bias: [batch, heads, Np, Np], Np = n rounded up to 64
+    assert lib.fjx_pair_bias_size(2, 1000, 16, _lib.FJX_DTYPE_BF16) == 2 * 16 * 1024 * 1024 * 2
+    assert lib.fjx_pair_bias_size(1, 64, 4, _lib.FJX_DTYPE_F32) == 4 * 64 * 64 * 4
+    assert lib.fjx_pair_bias_size(1, 0, 4, _lib.FJX_DTYPE_F32) == 0
 
 
 def test_invalid_arguments_return_codes_without_launching(lib):
@@ -130,6 +134,37 @@ def test_invalid_arguments_return_codes_without_launching(lib):
     assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_INVALID
     sa = _lib.SingleAttentionArgs(batch=1, n=4, c_s=384, c_z=128, heads=8, dtype=1)  # head_dim 48 > 32
     assert lib.fjx_single_attention_fwd(ctypes.byref(sa), None) == _lib.FJX_ERR_UNSUPPORTED
+
+
+def test_pair_bias_arguments_are_checked_before_launch(lib):
+    """The transition's pair-bias output and the single attention's prepared
+    pair bias are validated on the host (fake, never dereferenced pointers)."""
+    fake = 0x1000
+    base = dict(dtype=1, eps=1e-5, x=fake, norm_weight=fake, norm_bias=fake, w_a=fake, w_b=fake, w_o=fake,
+                out=fake, pb_out=fake, pb_norm_weight=fake, pb_norm_bias=fake, pb_weight=fake)
+    tr = _lib.TransitionArgs(rows=18, c=64, pb_n=3, pb_heads=16, workspace=fake, workspace_bytes=1 << 40, **base)
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_UNSUPPORTED
+    assert "c == 128" in lib.fjx_last_error().decode()
+    tr = _lib.TransitionArgs(rows=10, c=128, pb_n=3, pb_heads=16, **base)  # 10 is not a multiple of 3^2
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_INVALID
+    assert "multiple of pb_n^2" in lib.fjx_last_error().decode()
+    tr = _lib.TransitionArgs(rows=18, c=128, pb_n=3, pb_heads=0, **base)
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_INVALID
+    tr = _lib.TransitionArgs(rows=18, c=128, pb_n=3, pb_heads=16, **dict(base, pb_weight=None))
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_INVALID
+    assert "pair-bias weight" in lib.fjx_last_error().decode()
+    tr = _lib.TransitionArgs(rows=18, c=128, pb_n=3, pb_heads=16, **dict(base, pb_out=fake + 4))
+    assert lib.fjx_transition_fwd(ctypes.byref(tr), None) == _lib.FJX_ERR_INVALID
+    assert "16-byte aligned" in lib.fjx_last_error().decode()
+
+    # with a prepared pair bias, z and its weights are not required: the call
+    # gets as far as the workspace check
+    sa = _lib.SingleAttentionArgs(batch=1, n=4, c_s=384, c_z=0, heads=16, dtype=1, s=fake, out=fake,
+                                  q_weight=fake, k_weight=fake, v_weight=fake, g_weight=fake, o_weight=fake,
+                                  pair_bias=fake, workspace=fake, workspace_bytes=16)
+    assert lib.fjx_single_attention_fwd(ctypes.byref(sa), None) == _lib.FJX_ERR_WORKSPACE
+    sa.pair_bias = None  # then z is required again
+    assert lib.fjx_single_attention_fwd(ctypes.byref(sa), None) == _lib.FJX_ERR_UNSUPPORTED  # c_z == 0
 
 
 def test_check_maps_codes_to_exceptions(lib):

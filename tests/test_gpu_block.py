@@ -82,6 +82,49 @@ def test_single_attention_parity(dt, n, n_real):
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("batch,n,heads,expansion", [
+    (1, 64, 16, 4),  # fused into the transition epilogue, no padding
+    (1, 37, 16, 4),  # fused, n % 4 != 0, padded border
+    (2, 40, 12, 4),  # fused, two batch entries, padded border
+    (1, 20, 24, 4),  # more than 16 heads: a separate pass after the fused transition
+    (1, 24, 16, 2),  # a 2x hidden width: general transition path, then the pass
+])
+def test_transition_pair_bias_output(dt, batch, n, heads, expansion):
+    """The pair transition's pair-bias output: its own output unchanged, the
+    prepared bias equal to log2(e) LN_z(out) w_z^T of that output inside
+    [n, n] and zero on the padded border, and the single attention fed the
+    prepared bias agreeing with the one that builds its own from z."""
+    dtype = DTYPES[dt]
+    say(f"transition pair-bias output batch={batch} n={n} heads={heads} x{expansion} {dt}")
+    z = syn.pair_input(n, 128, seed=41, batch=batch)
+    s = syn.single_input(n, 384, seed=42, batch=batch)
+    mask = np.stack([syn.token_mask(n, n - 3 * b) for b in range(batch)])
+    tr = syn.transition_weights(128, expansion, seed=44)
+    tw = P.pack_transition_torch({k: tr[k] for k in ("layer_norm", "linear_a", "linear_b", "linear_out")}, dtype, "cuda")
+    w = syn.single_attention_weights(heads=heads, seed=43)
+    att, pre = P.single_attention_to_boltz2(w)
+    packed = P.pack_single_attention_boltz2(att, dtype, "cuda", pre_norm=pre)
+    zt = device_tensor(z, dtype)
+    plain = kernels.transition(zt, tw, residual=zt)
+    out, pb = kernels.transition(zt, tw, residual=zt, pair_bias_for=packed)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    np_ = (n + 63) // 64 * 64
+    assert tuple(pb.shape) == (batch, heads, np_, np_)
+    pbn = to_np(pb)
+    assert not pbn[:, :, n:, :].any() and not pbn[:, :, :, n:].any()
+    o = to_np(out)
+    ln = O.layer_norm(o, prep(w["proj_z_norm"]["weight"], dtype), prep(w["proj_z_norm"]["bias"], dtype))
+    want = np.transpose(O.linear_torch(ln, {"weight": prep(w["proj_z"]["weight"], dtype)}), (0, 3, 1, 2))
+    assert_parity(pbn[:, :, :n, :n], want * np.log2(np.e), dtype, "prepared pair bias")
+    st, mt = device_tensor(s, dtype), device_tensor(mask, dtype)
+    ref = kernels.single_attention(st, out, mt, packed, residual=st)
+    got = kernels.single_attention(st, None, mt, packed, residual=st, pair_bias=pb)
+    torch.cuda.synchronize()
+    assert_parity(to_np(got), to_np(ref), dtype, "single attention with the prepared bias")
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
 def test_pairformer_layer_parity(dt):
     dtype = DTYPES[dt]
     n, n_real = 48, 44
