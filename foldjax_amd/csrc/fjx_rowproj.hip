@@ -283,8 +283,12 @@ constexpr int kTE = 64;
 // 32w .. 32w+31 of both products for the 64 positions, holding the g_out and
 // p_out slabs of those channels; the two LayerNormed tiles sit side by side
 // in LDS so the gate and the projection of a row tile combine at once.
+// kResX: the residual is x itself (read back from the tile's raw copy in
+// LDS). A compile-time choice: one pointer that may address LDS or global
+// memory compiles to a generic load, which waits for every global access in
+// flight -- the previous row tile's store and the next tile's prefetch.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool kResX>
 __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpilogueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xg[kTE][kLd];    // LN_in(x)
   __shared__ __attribute__((aligned(16))) T xp[kTE][kLd];    // LN_out(o)
@@ -299,7 +303,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
   const int lane = t & 63;
   const int col0 = 32 * wave;
   const int p = t >> 2;  // LayerNorm position of this thread
-  const bool res_x = P.residual == P.x;
+  constexpr bool res_x = kResX;
   const bool vec8 = (n % 8) == 0;
 
   WSlab<T> wg, wp;
@@ -382,7 +386,8 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
           for (int q = 0; q < 4; ++q) y[4 * ct + q] = ap[ct][q] * round_to<T>(fast_sigmoid(ag[ct][q]));
         if (P.residual) {
           float rv[8];
-          to_f32x8(load8(res_x ? &xraw[pp][c] : P.residual + off), rv);
+          if constexpr (res_x) to_f32x8(load8(&xraw[pp][c]), rv);
+          else to_f32x8(load8(P.residual + off), rv);
 #pragma unroll
           for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
@@ -398,9 +403,10 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 //   out[orig] = T(o[r,s] * sigmoid(LN(x[orig]) w_g^T)) w_o^T (+ residual[orig])
 // with o position-major [B][N*N][128] and orig = (r, s) or (s, r). 256
 // threads: wave w owns output channels 32w .. 32w+31 of both products for the
-// 64 positions, holding the w_g and w_o slabs.
+// 64 positions, holding the w_g and w_o slabs. kResX as for the tri-mul
+// epilogue.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool kResX>
 __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpilogueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTE][kLd];    // LN(x)
   __shared__ __attribute__((aligned(16))) T xo[kTE][kLd];    // gated o
@@ -416,7 +422,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
   const int col0 = 32 * wave;
   const int p = t >> 2;
   const bool gated = P.w_g != nullptr;
-  const bool res_x = P.residual == P.x;
+  constexpr bool res_x = kResX;
   const bool need_x = gated || res_x;
 
   // paired slabs: lane group g works on the 8 consecutive channels
@@ -496,7 +502,8 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
           for (int q = 0; q < 4; ++q) y[4 * ct + q] = acc[ct][q];
         if (P.residual) {
           float rv[8];
-          to_f32x8(load8(res_x ? &xraw[pp][c] : P.residual + off), rv);
+          if constexpr (res_x) to_f32x8(load8(&xraw[pp][c]), rv);
+          else to_f32x8(load8(P.residual + off), rv);
 #pragma unroll
           for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
@@ -525,14 +532,28 @@ void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, h
 template <typename T>
 void launch_trimul_epilogue(const TriMulEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
-  const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T>);
-  hipLaunchKernelGGL(trimul_epilogue_kernel<T>, dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p, ntiles);
+  if (p.residual && p.residual == p.x) {
+    const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T, true>);
+    hipLaunchKernelGGL((trimul_epilogue_kernel<T, true>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
+                       ntiles);
+  } else {
+    const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T, false>);
+    hipLaunchKernelGGL((trimul_epilogue_kernel<T, false>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
+                       ntiles);
+  }
 }
 template <typename T>
 void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
-  const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T>);
-  hipLaunchKernelGGL(triattn_epilogue_kernel<T>, dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p, ntiles);
+  if (p.residual && p.residual == p.x) {
+    const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T, true>);
+    hipLaunchKernelGGL((triattn_epilogue_kernel<T, true>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
+                       ntiles);
+  } else {
+    const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T, false>);
+    hipLaunchKernelGGL((triattn_epilogue_kernel<T, false>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
+                       ntiles);
+  }
 }
 
 #define FJX_INST(T)                                                                                 \
