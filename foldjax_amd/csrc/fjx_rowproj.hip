@@ -78,15 +78,22 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
   load_wslab<T>(P.w_g + (int64_t)half * kC * kC, col0, wg);
   stage_ln<T>(P.ln_w, P.ln_b, ln);
 
+  // the fetched position's mask value stays raw until it is used: a
+  // conversion in the fetch would wait there for every load in flight,
+  // the row prefetch included
   RowPart<T> xr;
-  float mk = 0.f;
+  T mraw = from_f32<T>(0.f);
+  bool mvalid = false;
   auto fetch = [&](int64_t tile) {
     const TileRS tl = tile_at(tile, ntx, n);
     const int s = tl.s0 + p;
     const bool valid = s < n;
-    const int64_t pos = (int64_t)tl.b * nn + (P.transpose ? (int64_t)s * n + tl.r : (int64_t)tl.r * n + s);
-    load_row_part<T>(valid ? P.x + pos * kC : nullptr, xr);
-    mk = valid ? (P.mask ? to_f32(P.mask[pos]) : 1.0f) : 0.f;
+    auto pos_of = [&](int ss) {
+      return (int64_t)tl.b * nn + (P.transpose ? (int64_t)ss * n + tl.r : (int64_t)tl.r * n + ss);
+    };
+    load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
+    mvalid = valid;
+    if (P.mask) mraw = P.mask[pos_of(valid ? s : tl.s0)];
   };
 
   int64_t tile = blockIdx.x;
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     const TileRS tl = tile_at(tile, ntx, n);
     const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
     ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
-    if ((t & 3) == 0) mrow[p] = mk;
+    if ((t & 3) == 0) mrow[p] = mvalid ? (P.mask ? to_f32(mraw) : 1.0f) : 0.f;
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
@@ -175,15 +182,20 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   }
   stage_ln<T>(P.ln_w, P.ln_b, ln);
 
+  // the mask value stays raw until it is used (as in the tri-mul prologue)
   RowPart<T> xr;
-  float mbv = -INFINITY;
+  T mraw = from_f32<T>(0.f);
+  bool mvalid = false;
   auto fetch = [&](int64_t tile) {
     const TileRS tl = tile_at(tile, ntx, n);
     const int s = tl.s0 + p;
     const bool valid = s < n;
-    const int64_t pos = (int64_t)tl.b * nn + (P.transpose ? (int64_t)s * n + tl.r : (int64_t)tl.r * n + s);
-    load_row_part<T>(valid ? P.x + pos * kC : nullptr, xr);
-    mbv = valid ? P.inf * ((P.mask ? to_f32(P.mask[pos]) : 1.0f) - 1.0f) * kLog2e : -INFINITY;
+    auto pos_of = [&](int ss) {
+      return (int64_t)tl.b * nn + (P.transpose ? (int64_t)ss * n + tl.r : (int64_t)tl.r * n + ss);
+    };
+    load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
+    mvalid = valid;
+    if (P.mask) mraw = P.mask[pos_of(valid ? s : tl.s0)];
   };
 
   int64_t tile = blockIdx.x;
@@ -194,7 +206,10 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
     const int nstore = (int)min<int64_t>(kTP, np - tl.s0);  // incl. zero padding; a multiple of 64
     const int nreal = (int)max<int64_t>(0, min<int64_t>(kTP, n - tl.s0));
     ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
-    if ((t & 3) == 0 && p < nstore) P.mb[((int64_t)tl.b * n + tl.r) * np + tl.s0 + p] = mbv;
+    if ((t & 3) == 0 && p < nstore) {
+      const float mv = P.mask ? to_f32(mraw) : 1.0f;
+      P.mb[((int64_t)tl.b * n + tl.r) * np + tl.s0 + p] = mvalid ? P.inf * (mv - 1.0f) * kLog2e : -INFINITY;
+    }
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
