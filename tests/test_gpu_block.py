@@ -124,6 +124,32 @@ def test_transition_pair_bias_output(dt, batch, n, heads, expansion):
     assert_parity(to_np(got), to_np(ref), dtype, "single attention with the prepared bias")
 
 
+def test_pair_bias_argument_errors():
+    """Misuse of the prepared pair bias is refused on the host: a transition
+    input that is not a pair tensor, a bias of the wrong shape or dtype, and
+    a single attention given neither z nor a prepared bias."""
+    dtype = torch.bfloat16
+    n = 24
+    tr = syn.transition_weights(128, 4, seed=44)
+    tw = P.pack_transition_torch({k: tr[k] for k in ("layer_norm", "linear_a", "linear_b", "linear_out")}, dtype, "cuda")
+    w = syn.single_attention_weights(heads=16, seed=43)
+    att, pre = P.single_attention_to_boltz2(w)
+    packed = P.pack_single_attention_boltz2(att, dtype, "cuda", pre_norm=pre)
+    rows = device_tensor(syn.pair_input(n, 128, seed=1)[0], dtype)  # [n, 128]: not a pair tensor
+    with pytest.raises(ValueError, match="pair tensor"):
+        kernels.transition(rows, tw, pair_bias_for=packed)
+    z = device_tensor(syn.pair_input(n, 128, seed=1, batch=1), dtype)
+    s = device_tensor(syn.single_input(n, 384, seed=2, batch=1), dtype)
+    _, pb = kernels.transition(z, tw, residual=z, pair_bias_for=packed)
+    with pytest.raises(ValueError, match="prepared"):
+        kernels.single_attention(s, None, None, packed, pair_bias=pb[:, :8].contiguous())
+    with pytest.raises(ValueError, match="prepared"):
+        kernels.single_attention(s, None, None, packed, pair_bias=pb.float())
+    with pytest.raises(ValueError, match="needs z or a prepared pair_bias"):
+        kernels.single_attention(s, None, None, packed)
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 def test_pairformer_layer_parity(dt):
     dtype = DTYPES[dt]
