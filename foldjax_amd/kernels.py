@@ -48,6 +48,20 @@ def _prep(t: torch.Tensor | None, dtype: torch.dtype, device) -> torch.Tensor | 
     return t.to(device=device, dtype=dtype).contiguous()
 
 
+def _same_device(x: torch.Tensor, **operands) -> None:
+    """Every operand must live on ``x``'s device: a host tensor's pointer
+    handed to a kernel would be read as device memory."""
+    for name, t in operands.items():
+        if t is not None and t.device != x.device:
+            raise ValueError(f"{name} is on {t.device} but the input is on {x.device}; "
+                             "every operand must be on the input's device")
+
+
+def _need_shape(name: str, t: torch.Tensor | None, shape) -> None:
+    if t is not None and tuple(t.shape) != tuple(int(v) for v in shape):
+        raise ValueError(f"{name} must have shape {tuple(int(v) for v in shape)}, got {tuple(t.shape)}")
+
+
 @dataclass(frozen=True)
 class TriMulWeights:
     """Tri-mul weights in the ABI layout (PyTorch ``[out, in]``, a rows first)."""
@@ -63,6 +77,15 @@ class TriMulWeights:
 
     def to(self, dtype: torch.dtype, device) -> "TriMulWeights":
         return TriMulWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+
+    def check(self, c_z: int) -> int:
+        """Shapes against the pair width ``c_z``; returns ``c_h``."""
+        c_h = int(self.norm_out_weight.shape[0])
+        for name, shape in (("norm_in_weight", (c_z,)), ("norm_in_bias", (c_z,)), ("p_in_weight", (2 * c_h, c_z)),
+                            ("g_in_weight", (2 * c_h, c_z)), ("norm_out_bias", (c_h,)), ("p_out_weight", (c_z, c_h)),
+                            ("g_out_weight", (c_z, c_z))):
+            _need_shape(f"tri-mul weight {name}", getattr(self, name), shape)
+        return c_h
 
 
 @dataclass(frozen=True)
@@ -85,6 +108,17 @@ class TriAttnWeights:
     def to(self, dtype: torch.dtype, device) -> "TriAttnWeights":
         return TriAttnWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
 
+    def check(self, c_z: int) -> int:
+        """Shapes against the pair width ``c_z``; returns ``heads * head_dim``."""
+        hd = int(self.q_weight.shape[0])
+        if hd % self.heads:
+            raise ValueError(f"q projection width {hd} is not divisible by {self.heads} heads")
+        for name, shape in (("norm_weight", (c_z,)), ("norm_bias", (c_z,)), ("bias_weight", (self.heads, c_z)),
+                            ("q_weight", (hd, c_z)), ("k_weight", (hd, c_z)), ("v_weight", (hd, c_z)),
+                            ("g_weight", (hd, c_z)), ("o_weight", (c_z, hd))):
+            _need_shape(f"tri-attn weight {name}", getattr(self, name), shape)
+        return hd
+
 
 @dataclass(frozen=True)
 class TransitionWeights:
@@ -100,6 +134,14 @@ class TransitionWeights:
 
     def to(self, dtype: torch.dtype, device) -> "TransitionWeights":
         return TransitionWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+
+    def check(self, c: int) -> int:
+        """Shapes against the width ``c``; returns the hidden width."""
+        hidden = int(self.w_a.shape[0])
+        for name, shape in (("norm_weight", (c,)), ("norm_bias", (c,)), ("w_a", (hidden, c)), ("w_b", (hidden, c)),
+                            ("w_o", (c, hidden))):
+            _need_shape(f"transition weight {name}", getattr(self, name), shape)
+        return hidden
 
 
 @dataclass(frozen=True)
@@ -126,6 +168,17 @@ class SingleAttentionWeights:
     def to(self, dtype: torch.dtype, device) -> "SingleAttentionWeights":
         return SingleAttentionWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
 
+    def check(self, c_s: int, c_z: int | None) -> None:
+        """Shapes against the single width ``c_s`` and (when z is read) the
+        pair width ``c_z``."""
+        for name in ("q_weight", "k_weight", "v_weight", "g_weight", "o_weight"):
+            _need_shape(f"single attention weight {name}", getattr(self, name), (c_s, c_s))
+        for name in ("q_bias", "pre_norm_weight", "pre_norm_bias"):
+            _need_shape(f"single attention weight {name}", getattr(self, name), (c_s,))
+        if c_z is not None:
+            for name, shape in (("z_norm_weight", (c_z,)), ("z_norm_bias", (c_z,)), ("z_weight", (self.heads, c_z))):
+                _need_shape(f"single attention weight {name}", getattr(self, name), shape)
+
 
 def transition(
     x: torch.Tensor,
@@ -148,8 +201,17 @@ def transition(
     pair_bias=...)``; with 128 channels, a 4x hidden width and at most 16
     heads it is computed in the transition's epilogue, so the pair tensor is
     not read again."""
-    _dev(x)
     c = int(x.shape[-1])
+    w.check(c)
+    _same_device(x, row_mask=row_mask, residual=residual)
+    if residual is not None:
+        _need_shape("residual", residual, x.shape)
+    if pair_bias_for is not None:
+        _same_device(x, pair_bias_for=pair_bias_for.z_weight)
+        _need_shape("pair-bias weight z_norm_weight", pair_bias_for.z_norm_weight, (c,))
+        _need_shape("pair-bias weight z_norm_bias", pair_bias_for.z_norm_bias, (c,))
+        _need_shape("pair-bias weight z_weight", pair_bias_for.z_weight, (pair_bias_for.heads, c))
+    _dev(x)
     rows = x.numel() // max(c, 1)
     xf = x.contiguous()
     lib = _lib.load()
@@ -204,6 +266,10 @@ def single_attention(
     ``[B, N]`` token mask. Returns the update, or ``residual + update``.
     ``pair_bias``: the bias ``transition(..., pair_bias_for=w)`` prepared from
     this ``z``; ``z`` is then not read (and may be None)."""
+    _same_device(s, z=z, mask=mask, residual=residual, pair_bias=pair_bias)
+    if residual is not None:
+        _need_shape("residual", residual, s.shape)
+    w.check(int(s.shape[-1]), None if z is None else int(z.shape[-1]))
     _dev(s)
     squeeze = s.dim() == 2
     sb = s.unsqueeze(0) if squeeze else s
@@ -254,6 +320,7 @@ def single_attention(
 def _flatten_pair(x: torch.Tensor, mask: torch.Tensor | None):
     if x.dim() < 3:
         raise ValueError(f"pair tensor must be [..., N, N, C], got shape {tuple(x.shape)}")
+    _same_device(x, mask=mask)
     n, n2, c = x.shape[-3:]
     if n != n2:
         raise ValueError(f"pair tensor must be square in its two pair axes, got {tuple(x.shape)}")
@@ -280,11 +347,14 @@ def trimul(
 ) -> torch.Tensor:
     """Triangle multiplicative update (``fjx_trimul_fwd``); returns the update,
     or ``residual + update`` when ``residual`` is given."""
-    _dev(x)
     if direction not in ("outgoing", "incoming"):
         raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
+    _same_device(x, residual=residual)
+    if residual is not None:
+        _need_shape("residual", residual, x.shape)
+    c_h = w.check(int(x.shape[-1]))
     xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
-    c_h = int(w.norm_out_weight.shape[0])
+    _dev(x)
     lib = _lib.load()
     code = _code(x.dtype)
     out = torch.empty_like(xf)
@@ -318,12 +388,13 @@ def triattn(
     residual: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Triangle attention, starting or ending node (``fjx_triattn_fwd``)."""
-    _dev(x)
-    xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
+    _same_device(x, residual=residual)
+    if residual is not None:
+        _need_shape("residual", residual, x.shape)
+    hd = w.check(int(x.shape[-1]))
     heads = w.heads
-    hd = int(w.q_weight.shape[0])
-    if hd % heads:
-        raise ValueError(f"q projection width {hd} is not divisible by {heads} heads")
+    xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
+    _dev(x)
     lib = _lib.load()
     code = _code(x.dtype)
     out = torch.empty_like(xf)
@@ -360,6 +431,14 @@ def triattn_core(
     ``mask_bias`` ``[..., I, 1, 1, J]`` (or None); ``scale`` applied inside.
     Leading axes are broadcast and folded into one batch axis.
     """
+    _same_device(q, k=k, v=v, tri_bias=tri_bias, mask_bias=mask_bias)
+    if q.dim() < 4 or k.shape[-4:] != q.shape[-4:] or v.shape[-4:] != q.shape[-4:]:
+        raise ValueError(f"q, k, v must share [..., I, H, J, D], got {tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
+    if tri_bias.dim() < 4 or tuple(tri_bias.shape[-3:]) != (q.shape[-3], q.shape[-2], q.shape[-2]):
+        raise ValueError(f"tri_bias must be [..., 1, H, J, J] for q {tuple(q.shape)}, got {tuple(tri_bias.shape)}")
+    if mask_bias is not None and (mask_bias.dim() < 4 or tuple(mask_bias.shape[-4:]) not in
+                                  ((q.shape[-4], 1, 1, q.shape[-2]), (1, 1, 1, q.shape[-2]))):
+        raise ValueError(f"mask_bias must be [..., I, 1, 1, J] for q {tuple(q.shape)}, got {tuple(mask_bias.shape)}")
     _dev(q)
     lead = torch.broadcast_shapes(q.shape[:-4], tri_bias.shape[:-4],
                                   () if mask_bias is None else mask_bias.shape[:-4])

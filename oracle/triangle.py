@@ -480,3 +480,134 @@ def boltz2_pairformer_layer(p, s, z, mask, pair_mask, *, eps=1e-5):
     s = _f(s) + boltz2_attention_pair_bias(a, s_ln, z, mask, eps=eps)
     s = s + transition(s, p["transition_s"], eps=eps)
     return s, z
+
+
+# ---------------------------------------------------------------------------
+# Sampled output positions at full size (configs 3-5)
+# ---------------------------------------------------------------------------
+#
+# At N = 1024 .. 3072 the full float64 restatements above need tens of GB.
+# Each output position of a triangle sublayer depends on only a few lines of
+# the pair tensor, so the same formulas are restated here per position:
+# ``z`` and ``mask`` are anything indexable as ``z[i]`` (row i, ``[N, C]``) and
+# ``z[:, j]`` (column j), e.g. a numpy array or a test-side view of a device
+# tensor; every line is converted to float64. Pinned against the full
+# functions on small shapes (tests/test_oracle.py).
+
+
+def _line(z, idx, transposed):
+    return _f(z[:, idx] if transposed else z[idx])
+
+
+def triangle_multiplication_at(z, mask, params, direction, positions, eps=1e-5):
+    """Protenix/OpenFold3-form tri-mul update (torch-layout field names) at
+    ``positions`` ``[(i, j), ...]`` of a ``[N, N, C]`` pair tensor.
+
+    The formula of ``protenix_triangle_multiplication`` (``PXT/triangle.py:166-228``):
+    outgoing ``o[i,j] = sum_k a[i,k] b[j,k]`` reads rows i and j of z and the
+    mask, incoming ``o[i,j] = sum_k a[k,i] b[k,j]`` reads columns i and j, with
+    ``a = m * sigmoid(LN(z) A_g^T) * (LN(z) A_p^T)`` (b likewise); then
+    ``LN_out(o) W_z^T * sigmoid(LN(z[i,j]) W_g^T)``. Returns ``[len(positions), C]``.
+    """
+    t = direction == "incoming"
+    if direction not in ("outgoing", "incoming"):
+        raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
+    ln_in = _ln_params(_get(params, "layer_norm_in"))
+    cache = {}
+
+    def proj(idx):
+        if idx not in cache:
+            zl = _line(z, idx, t)
+            m = np.ones(zl.shape[0]) if mask is None else _line(mask, idx, t)
+            zn = layer_norm(zl, *ln_in, eps=eps)
+            a = m[:, None] * sigmoid(linear_torch(zn, _get(params, "linear_a_g"))) * linear_torch(
+                zn, _get(params, "linear_a_p"))
+            b = m[:, None] * sigmoid(linear_torch(zn, _get(params, "linear_b_g"))) * linear_torch(
+                zn, _get(params, "linear_b_p"))
+            cache[idx] = (a, b, zl)
+        return cache[idx]
+
+    out = []
+    for i, j in positions:
+        a_i, _, zl_i = proj(i)
+        _, b_j, zl_j = proj(j)
+        o = (a_i * b_j).sum(axis=0)
+        o = layer_norm(o, *_ln_params(_get(params, "layer_norm_out")), eps=eps)
+        y = linear_torch(o, _get(params, "linear_z"))
+        x_ij = zl_j[i] if t else zl_i[j]  # z[i, j]: row i at column j, or column j at row i
+        xn = layer_norm(x_ij, *ln_in, eps=eps)
+        out.append(y * sigmoid(linear_torch(xn, _get(params, "linear_g"))))
+    return np.stack(out)
+
+
+def triangle_attention_at(z, mask, params, *, num_heads, starting, positions, inf=1e9, eps=1e-5):
+    """Protenix-form tri-attn update (``linear`` / ``attention`` field names) at
+    ``positions`` ``[(i, q), ...]`` of the attention grid.
+
+    The formula of ``protenix_triangle_attention`` (``PXT/triangle.py:509-535,
+    732-847``) for one attention row i and one query q: keys, values, the
+    mask bias ``inf * (m[i, k] - 1)`` come from line i of the grid, the query
+    and gate from its entry q, and the triangle bias ``LN(x)[q, k] . w_b`` from
+    line q. Starting node: the grid is z (lines are rows), and the result is
+    the update at ``[i, q]``; ending node: the grid is z transposed (lines are
+    columns), and the result is the update at ``[q, i]``. Returns
+    ``[len(positions), C]``.
+    """
+    t = not starting
+    ln = _ln_params(_get(params, "layer_norm"))
+    att = _get(params, "attention")
+    cache = {}
+
+    def line(idx):
+        if idx not in cache:
+            cache[idx] = layer_norm(_line(z, idx, t), *ln, eps=eps)
+        return cache[idx]
+
+    out = []
+    for i, q in positions:
+        xi = line(i)  # [N, C]
+        n = xi.shape[0]
+        m = np.ones(n) if mask is None else _line(mask, i, t)
+        k = linear_torch(xi, _get(att, "linear_k")).reshape(n, num_heads, -1)
+        v = linear_torch(xi, _get(att, "linear_v")).reshape(n, num_heads, -1)
+        d = k.shape[-1]
+        qv = linear_torch(xi[q], _get(att, "linear_q")).reshape(num_heads, d) * (float(d) ** -0.5)
+        bias = linear_torch(line(q), _get(params, "linear"))  # [N(k), H]
+        s = np.einsum("hd,khd->hk", qv, k) + (inf * (m - 1.0))[None, :] + bias.T
+        o = np.einsum("hk,khd->hd", softmax(s, axis=-1), v)
+        if _get(att, "linear_g") is not None:
+            o = o * sigmoid(linear_torch(xi[q], _get(att, "linear_g"))).reshape(num_heads, d)
+        out.append(linear_torch(o.reshape(-1), _get(att, "linear_o")))
+    return np.stack(out)
+
+
+def boltz2_attention_pair_bias_at(p, s, z, mask, queries, *, inf=1e6, eps=1e-5):
+    """``boltz2_attention_pair_bias`` (``B2P/attention.py:44-115``) for one batch
+    item at the query rows ``queries``: ``s`` ``[N, c_s]`` normalised single
+    representation, ``z`` indexable by row (row i gives the bias row
+    ``LN_z(z[i, :]) W_z^T``), ``mask`` ``[N]``. Returns ``[len(queries), c_s]``."""
+    s = _f(s)
+    mask = _f(mask)
+    n, c_s = s.shape
+    heads = _f(p["proj_z"]["weight"]).shape[0]
+    d = c_s // heads
+    k = linear_torch(s, {"weight": p["proj_k"]["weight"]}).reshape(n, heads, d)
+    v = linear_torch(s, {"weight": p["proj_v"]["weight"]}).reshape(n, heads, d)
+    out = []
+    for i in queries:
+        q = linear_torch(s[i], p["proj_q"]).reshape(heads, d)
+        g = sigmoid(linear_torch(s[i], {"weight": p["proj_g"]["weight"]}))
+        bias = linear_torch(layer_norm(_f(z[i]), p["proj_z_norm"]["weight"], p["proj_z_norm"]["bias"], eps),
+                            {"weight": p["proj_z"]["weight"]})  # [N(j), H]
+        sc = np.einsum("hd,jhd->hj", q, k) / np.sqrt(d) + bias.T + ((1.0 - mask) * -inf)[None, :]
+        o = np.einsum("hj,jhd->hd", softmax(sc, axis=-1), v).reshape(-1)
+        out.append(linear_torch(g * o, {"weight": p["proj_o"]["weight"]}))
+    return np.stack(out)
+
+
+def pair_bias_at(p, z, positions, *, eps=1e-5):
+    """The single attention's pair bias ``LN_z(z[i, j]) W_z^T`` (``B2P/attention.py:69-75``)
+    at ``positions`` ``[(i, j), ...]``; returns ``[len(positions), H]``."""
+    rows = np.stack([_f(z[i])[j] for i, j in positions])
+    return linear_torch(layer_norm(rows, p["proj_z_norm"]["weight"], p["proj_z_norm"]["bias"], eps),
+                        {"weight": p["proj_z"]["weight"]})

@@ -108,3 +108,67 @@ def test_bf16_round_matches_torch():
     x = np.random.default_rng(0).standard_normal(10000).astype(np.float32) * 100
     want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(syn.bf16_round(x), want)
+
+
+def _meta(t: torch.Tensor) -> torch.Tensor:
+    """The same shape on another device (``meta``): a stand-in for an operand
+    left on the wrong device, which must be refused before any launch."""
+    return torch.empty(t.shape, dtype=t.dtype, device="meta")
+
+
+def test_kernels_refuse_operands_on_another_device():
+    z = _z(8)
+    tm = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights()), torch.float32, "cpu")
+    ta = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights()), torch.float32, "cpu")
+    tr = P.pack_transition_torch(syn.transition_weights(), torch.float32, "cpu")
+    m = torch.ones(8, 8)
+    with pytest.raises(ValueError, match="mask is on meta"):
+        kernels.trimul(z, _meta(m), tm, "outgoing")
+    with pytest.raises(ValueError, match="residual is on meta"):
+        kernels.trimul(z, m, tm, "outgoing", residual=_meta(z))
+    with pytest.raises(ValueError, match="mask is on meta"):
+        kernels.triattn(z, _meta(m), ta)
+    with pytest.raises(ValueError, match="residual is on meta"):
+        kernels.triattn(z, m, ta, residual=_meta(z))
+    q = torch.zeros(1, 8, 4, 8, 32)
+    tb = torch.zeros(1, 1, 4, 8, 8)
+    for name, args in (("k", (q, _meta(q), q, tb, None)), ("v", (q, q, _meta(q), tb, None)),
+                       ("tri_bias", (q, q, q, _meta(tb), None)),
+                       ("mask_bias", (q, q, q, tb, _meta(torch.zeros(1, 8, 1, 1, 8))))):
+        with pytest.raises(ValueError, match=f"{name} is on meta"):
+            kernels.triattn_core(*args, scale=1.0)
+    with pytest.raises(ValueError, match="row_mask is on meta"):
+        kernels.transition(z, tr, row_mask=_meta(m))
+
+
+def test_kernels_refuse_mismatched_shapes():
+    z = _z(8)
+    m = torch.ones(8, 8)
+    w64 = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(64, 128)), torch.float32, "cpu")
+    with pytest.raises(ValueError, match="tri-mul weight norm_in_weight must have shape"):
+        kernels.trimul(z, m, w64, "outgoing")  # packed for c_z = 64, called with 128
+    tm = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights()), torch.float32, "cpu")
+    with pytest.raises(ValueError, match="residual must have shape"):
+        kernels.trimul(z, m, tm, "outgoing", residual=_z(4))
+    ta64 = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(64, 4, 16)), torch.float32, "cpu")
+    with pytest.raises(ValueError, match="tri-attn weight"):
+        kernels.triattn(z, m, ta64)
+    q = torch.zeros(1, 8, 4, 8, 32)
+    with pytest.raises(ValueError, match="q, k, v must share"):
+        kernels.triattn_core(q, torch.zeros(1, 8, 4, 9, 32), q, torch.zeros(1, 1, 4, 8, 8), None, scale=1.0)
+    with pytest.raises(ValueError, match="tri_bias must be"):
+        kernels.triattn_core(q, q, q, torch.zeros(1, 1, 4, 8, 9), None, scale=1.0)
+    with pytest.raises(ValueError, match="mask_bias must be"):
+        kernels.triattn_core(q, q, q, torch.zeros(1, 1, 4, 8, 8), torch.zeros(1, 8, 1, 1, 7), scale=1.0)
+    tr = P.pack_transition_torch({"layer_norm": {"weight": np.ones(96), "bias": np.zeros(96)},
+                                  "linear_a": {"weight": np.zeros((384, 96))}, "linear_b": {"weight": np.zeros((384, 96))},
+                                  "linear_out": {"weight": np.zeros((96, 384))}}, torch.float32, "cpu")
+    with pytest.raises(ValueError, match="transition weight norm_weight must have shape"):
+        kernels.transition(z, tr)
+    sa = P.pack_single_attention_boltz2(P.single_attention_to_boltz2(syn.single_attention_weights())[0],
+                                        torch.float32, "cpu")
+    with pytest.raises(ValueError, match="single attention weight q_weight must have shape"):
+        kernels.single_attention(torch.zeros(1, 8, 256), torch.zeros(1, 8, 8, 128), None, sa)
+    with pytest.raises(ValueError, match="residual must have shape"):
+        kernels.single_attention(torch.zeros(1, 8, 384), torch.zeros(1, 8, 8, 128), None, sa,
+                                 residual=torch.zeros(1, 7, 384))

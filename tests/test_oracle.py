@@ -309,3 +309,77 @@ def test_pairformer_layer_padding_isolation():
     got_s, got_z = O.boltz2_pairformer_layer(w, sp, zp, tm, syn.pair_mask(n + pad, n)[None])
     np.testing.assert_allclose(got_s[:, :n], want_s, rtol=1e-8, atol=1e-8)
     np.testing.assert_allclose(got_z[:, :n, :n], want_z, rtol=1e-8, atol=1e-8)
+
+
+# ------------------------------------- sampled positions (full-size checks)
+
+
+def _all_positions(n):
+    return [(i, j) for i in range(n) for j in range(n)]
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_at_matches_full_oracle(direction):
+    """The per-position restatement equals the full tri-mul at every position,
+    with a random mask, and at n = 3 equals the brute-force loops."""
+    rng = np.random.default_rng(30)
+    n, c = 9, 8
+    z = rng.standard_normal((n, n, c))
+    mask = (rng.random((n, n)) > 0.3).astype(np.float64)
+    tm = syn.trimul_weights(c, c, seed=30)
+    full = O.protenix_triangle_multiplication(z, mask, tm, direction)
+    pos = _all_positions(n)
+    got = O.triangle_multiplication_at(z, mask, tm, direction, pos)
+    np.testing.assert_allclose(got, np.stack([full[i, j] for i, j in pos]), rtol=1e-11, atol=1e-11)
+    zs, ms, tms, _ = _small(seed=31)
+    want = np.array(B.trimul(zs.tolist(), ms.tolist(), B.tolist(tms), direction == "outgoing"))
+    got = O.triangle_multiplication_at(zs, ms, tms, direction, _all_positions(3))
+    np.testing.assert_allclose(got, want.reshape(9, -1), rtol=1e-11, atol=1e-11)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_triattn_at_matches_full_oracle(starting):
+    rng = np.random.default_rng(32)
+    n, c = 8, 8
+    z = rng.standard_normal((n, n, c))
+    mask = (rng.random((n, n)) > 0.3).astype(np.float64)
+    mask[3, :] = 0.0  # a fully masked line
+    ta = syn.triattn_weights(c, 2, 4, seed=32)
+    full = O.protenix_triangle_attention(z, mask, ta, num_heads=2, starting=starting)
+    pos = _all_positions(n)
+    got = O.triangle_attention_at(z, mask, ta, num_heads=2, starting=starting, positions=pos)
+    # (i, q) of the attention grid is [i, q] of the output (starting) or [q, i] (ending)
+    want = np.stack([full[i, q] if starting else full[q, i] for i, q in pos])
+    np.testing.assert_allclose(got, want, rtol=1e-10, atol=1e-10)
+
+
+def test_attention_pair_bias_at_matches_full_oracle():
+    rng = np.random.default_rng(33)
+    n, c_s, c_z, h = 9, 24, 8, 4
+    s = rng.standard_normal((1, n, c_s))
+    z = rng.standard_normal((1, n, n, c_z))
+    mask = (rng.random((1, n)) > 0.3).astype(np.float64)
+    mask[:, 0] = 1.0
+    p = syn.single_attention_weights(c_s, c_z, h, seed=33)
+    full = O.boltz2_attention_pair_bias(p, s, z, mask)[0]
+    got = O.boltz2_attention_pair_bias_at(p, s[0], z[0], mask[0], list(range(n)))
+    np.testing.assert_allclose(got, full, rtol=1e-10, atol=1e-10)
+    pos = [(0, 0), (3, 7), (8, 2)]
+    pb = O.pair_bias_at(p, z[0], pos)
+    zl = O.layer_norm(z[0], p["proj_z_norm"]["weight"], p["proj_z_norm"]["bias"])
+    for r, (i, j) in enumerate(pos):
+        np.testing.assert_allclose(pb[r], zl[i, j] @ np.asarray(p["proj_z"]["weight"], np.float64).T, rtol=1e-12)
+
+
+def test_planted_swapped_position_is_caught():
+    """Reading z[j, i] instead of z[i, j] for the output gate is caught by the
+    comparison with the full oracle."""
+    rng = np.random.default_rng(34)
+    n, c = 6, 8
+    z = rng.standard_normal((n, n, c))
+    tm = syn.trimul_weights(c, c, seed=34)
+    full = O.protenix_triangle_multiplication(z, None, tm, "outgoing")
+    got = O.triangle_multiplication_at(np.swapaxes(z, 0, 1).copy(), None, tm, "incoming", [(1, 4)])
+    # incoming on z^T reads the same a/b lines as outgoing on z, but its gate
+    # is z^T[1, 4] = z[4, 1]: the planted swap must differ from z's answer
+    assert np.max(np.abs(got[0] - full[1, 4])) > 1e-3
