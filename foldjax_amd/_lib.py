@@ -25,7 +25,8 @@ FJX_ERR_UNSUPPORTED = 2
 FJX_ERR_WORKSPACE = 3
 FJX_ERR_HIP = 4
 
-ABI_VERSION = 3
+ABI_VERSION = 4
+NOALLOC_SCRATCH_BYTES = 256 << 20
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -100,6 +101,7 @@ class SingleAttentionArgs(ctypes.Structure):
 SYMBOLS = {
     "fjx_trimul_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i32]),
     "fjx_trimul_fwd": (ctypes.c_int, [ctypes.POINTER(TriMulArgs), _vp]),
+    "fjx_trimul_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(TriMulArgs), _vp]),
     "fjx_triattn_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "fjx_triattn_fwd": (ctypes.c_int, [ctypes.POINTER(TriAttnArgs), _vp]),
     "fjx_triattn_core_workspace_size": (_sz, [_i64, _i64, _i64, _i64, _i64, _i32]),

@@ -17,6 +17,9 @@ using namespace fjx;
 namespace {
 
 thread_local std::string g_err;
+// set while an allocation-free entry point runs: no timing events are taken
+// (creating one is a driver allocation)
+thread_local bool g_no_events = false;
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -96,7 +99,7 @@ int timed(int id, hipStream_t st, const char* what, F&& launch) {
   hipEvent_t a = nullptr, b = nullptr;
   {
     std::lock_guard<std::mutex> lk(p.mu);
-    if (p.on) {
+    if (p.on && !g_no_events) {
       a = take_event(p);
       b = take_event(p);
     }
@@ -797,6 +800,32 @@ bool aligned16(std::initializer_list<const void*> ps) {
   return true;
 }
 
+// every check of fjx_trimul_fwd except the workspace's; `fn` names the entry point in messages
+int trimul_check(const fjx_trimul_args* a, const char* fn) {
+  if (!a) return fail(FJX_ERR_INVALID, "%s: args is NULL", fn);
+  if (a->batch < 1 || a->n < 1) return fail(FJX_ERR_INVALID, "%s: batch and n must be >= 1", fn);
+  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "%s: unknown dtype %d", fn, a->dtype);
+  if (a->direction != FJX_OUTGOING && a->direction != FJX_INCOMING)
+    return fail(FJX_ERR_INVALID, "Unsupported triangle multiplication direction: %d", a->direction);
+  if (a->c_z < 8 || a->c_h < 8 || a->c_z % 8 || a->c_h % 8 || a->c_z > 1024 || a->c_h > 1024)
+    return fail(FJX_ERR_UNSUPPORTED, "%s: c_z and c_h must be multiples of 8 in [8, 1024], got c_z=%lld c_h=%lld",
+                fn, (long long)a->c_z, (long long)a->c_h);
+  if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "%s: n or batch too large", fn);
+  if (!a->x || !a->out || !a->norm_in_weight || !a->norm_in_bias || !a->p_in_weight || !a->g_in_weight ||
+      !a->norm_out_weight || !a->norm_out_bias || !a->p_out_weight || !a->g_out_weight)
+    return fail(FJX_ERR_INVALID, "%s: a required pointer is NULL", fn);
+  if (!aligned16({a->x, a->out, a->residual, a->norm_in_weight, a->norm_in_bias, a->p_in_weight, a->g_in_weight,
+                  a->norm_out_weight, a->norm_out_bias, a->p_out_weight, a->g_out_weight}))
+    return fail(FJX_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
+  return FJX_OK;
+}
+
+int trimul_dispatch(const fjx_trimul_args* a, hipStream_t st) {
+  if (!fused_trimul(a->c_z, a->c_h))
+    return a->dtype == FJX_DTYPE_BF16 ? trimul_generic_run<bf16>(a, st) : trimul_generic_run<float>(a, st);
+  return a->dtype == FJX_DTYPE_BF16 ? trimul_run<bf16>(a, st) : trimul_run<float>(a, st);
+}
+
 }  // namespace
 
 extern "C" {
@@ -809,33 +838,17 @@ size_t fjx_trimul_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t 
   return fused_trimul(c_z, c_h) ? trimul_ws(batch, n, dtype).total : gen_trimul_ws(batch, n, c_z, c_h, dtype).total;
 }
 
+
 int fjx_trimul_fwd(const fjx_trimul_args* a, hipStream_t st) {
   g_err.clear();
-  if (!a) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: args is NULL");
-  if (a->batch < 1 || a->n < 1) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: batch and n must be >= 1");
-  if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: unknown dtype %d", a->dtype);
-  if (a->direction != FJX_OUTGOING && a->direction != FJX_INCOMING)
-    return fail(FJX_ERR_INVALID, "Unsupported triangle multiplication direction: %d", a->direction);
-  if (a->c_z < 8 || a->c_h < 8 || a->c_z % 8 || a->c_h % 8 || a->c_z > 1024 || a->c_h > 1024)
-    return fail(FJX_ERR_UNSUPPORTED,
-                "fjx_trimul_fwd: c_z and c_h must be multiples of 8 in [8, 1024], got c_z=%lld c_h=%lld",
-                (long long)a->c_z, (long long)a->c_h);
-  if (!grid_ok(a->n, a->batch)) return fail(FJX_ERR_UNSUPPORTED, "fjx_trimul_fwd: n or batch too large");
-  if (!a->x || !a->out || !a->norm_in_weight || !a->norm_in_bias || !a->p_in_weight || !a->g_in_weight ||
-      !a->norm_out_weight || !a->norm_out_bias || !a->p_out_weight || !a->g_out_weight)
-    return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: a required pointer is NULL");
-  if (!aligned16({a->x, a->out, a->residual, a->norm_in_weight, a->norm_in_bias, a->p_in_weight, a->g_in_weight,
-                  a->norm_out_weight, a->norm_out_bias, a->p_out_weight, a->g_out_weight}))
-    return fail(FJX_ERR_INVALID, "fjx_trimul_fwd: tensors must be 16-byte aligned");
-  const bool fused = fused_trimul(a->c_z, a->c_h);
+  if (int rc = trimul_check(a, "fjx_trimul_fwd")) return rc;
   const size_t need = fjx_trimul_workspace_size(a->batch, a->n, a->c_z, a->c_h, a->dtype);
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_trimul_fwd: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);
-  if (!fused)
-    return a->dtype == FJX_DTYPE_BF16 ? trimul_generic_run<bf16>(a, st) : trimul_generic_run<float>(a, st);
-  return a->dtype == FJX_DTYPE_BF16 ? trimul_run<bf16>(a, st) : trimul_run<float>(a, st);
+  return trimul_dispatch(a, st);
 }
+
 
 size_t fjx_triattn_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t heads, int64_t head_dim,
                                   int32_t dtype) {
@@ -1046,3 +1059,29 @@ int fjx_prof_read(int id, double* total_ms, int64_t* launches) {
 }
 
 }  // extern "C"
+
+namespace fjx {
+// fjx_trimul_fwd on a caller-supplied device scratch (fjx_noalloc.hip): the
+// same checks and kernels, the workspace fields of `a` ignored, no timing
+// events, nothing allocated
+__attribute__((visibility("hidden"))) int trimul_fwd_on_scratch(const fjx_trimul_args* a, hipStream_t st,
+                                                               void* scratch, size_t scratch_bytes, const char* fn) {
+  g_err.clear();
+  if (int rc = trimul_check(a, fn)) return rc;
+  const size_t need = fjx_trimul_workspace_size(a->batch, a->n, a->c_z, a->c_h, a->dtype);
+  if (need > scratch_bytes)
+    return fail(FJX_ERR_WORKSPACE,
+                "%s: this shape needs %zu bytes of scratch, the library's static scratch holds %zu "
+                "(use fjx_trimul_fwd with a workspace)",
+                fn, need, scratch_bytes);
+  fjx_trimul_args b = *a;
+  b.workspace = scratch;
+  b.workspace_bytes = scratch_bytes;
+  g_no_events = true;
+  const int rc = trimul_dispatch(&b, st);
+  g_no_events = false;
+  return rc;
+}
+
+__attribute__((visibility("hidden"))) int set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+}  // namespace fjx

@@ -344,9 +344,16 @@ def trimul(
     direction: str,
     eps: float = 1e-5,
     residual: torch.Tensor | None = None,
+    *,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """Triangle multiplicative update (``fjx_trimul_fwd``); returns the update,
-    or ``residual + update`` when ``residual`` is given."""
+    or ``residual + update`` when ``residual`` is given.
+
+    ``no_alloc``: run ``fjx_trimul_fwd_noalloc`` instead, whose workspace is
+    the library's static per-GPU scratch (shapes up to
+    ``_lib.NOALLOC_SCRATCH_BYTES`` of workspace; calls on one GPU must not
+    overlap). Only the output is allocated here."""
     if direction not in ("outgoing", "incoming"):
         raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
     _same_device(x, residual=residual)
@@ -359,8 +366,8 @@ def trimul(
     code = _code(x.dtype)
     out = torch.empty_like(xf)
     res = None if residual is None else residual.to(dtype=x.dtype).contiguous().reshape(batch, n, n, c)
-    ws_bytes = lib.fjx_trimul_workspace_size(batch, n, c, c_h, code)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    ws_bytes = 0 if no_alloc else lib.fjx_trimul_workspace_size(batch, n, c, c_h, code)
+    ws = None if no_alloc else torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     a = _lib.TriMulArgs(
         batch=batch, n=n, c_z=c, c_h=c_h,
         direction=_lib.FJX_OUTGOING if direction == "outgoing" else _lib.FJX_INCOMING,
@@ -374,7 +381,8 @@ def trimul(
         workspace=_ptr(ws), workspace_bytes=ws_bytes,
     )
     _check_weights(x, w)
-    _lib.check(lib.fjx_trimul_fwd(ctypes.byref(a), _stream(x)))
+    entry = lib.fjx_trimul_fwd_noalloc if no_alloc else lib.fjx_trimul_fwd
+    _lib.check(entry(ctypes.byref(a), _stream(x)))
     return out.reshape(tuple(lead) + (n, n, c))
 
 

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define FJX_ABI_VERSION 3
+#define FJX_ABI_VERSION 4
 
 /* element types of activations, masks and weights */
 enum { FJX_DTYPE_F32 = 0, FJX_DTYPE_BF16 = 1 };
@@ -103,6 +103,28 @@ typedef struct fjx_trimul_args {
 
 size_t fjx_trimul_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype);
 int fjx_trimul_fwd(const fjx_trimul_args* args, hipStream_t stream);
+
+/*
+ * fjx_trimul_fwd without any device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, checks, kernels and results as fjx_trimul_fwd, except that
+ * args->workspace and args->workspace_bytes are ignored: the workspace is a
+ * static device array of the library, FJX_NOALLOC_SCRATCH_BYTES per GPU,
+ * reserved when the library's code is loaded on a GPU and held until the
+ * process ends. A shape whose fjx_trimul_workspace_size exceeds it is
+ * refused with FJX_ERR_WORKSPACE (bf16 with c_z == c_h == 128: batch * n^2
+ * up to 349525, i.e. n <= 591 at batch 1; fp32: n <= 418). The stream must
+ * belong to the current device (FJX_ERR_INVALID otherwise).
+ *
+ * Every call on one GPU uses that GPU's single array: calls that overlap on
+ * one GPU (other streams, other threads) race and must be serialised by the
+ * caller. No part of the array needs clearing between calls: each call writes
+ * every byte it reads before reading it.
+ */
+#define FJX_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+int fjx_trimul_fwd_noalloc(const fjx_trimul_args* args, hipStream_t stream);
 
 /*
  * Triangle attention around the starting (Algorithm 14) or ending
