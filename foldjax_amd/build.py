@@ -45,6 +45,9 @@ def _hipcc() -> str:
 FILE_FLAGS = {
     "fjx_flash.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "fjx_rowproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    # scores in VGPRs (compiler MFMAs); the output accumulators are pinned to
+    # AGPRs by inline asm in the kernel itself
+    "fjx_flash_pipe.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

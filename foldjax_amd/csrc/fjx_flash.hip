@@ -447,8 +447,10 @@ void launch_flash(const FlashParams<T>& p_in, int64_t batch, hipStream_t st) {
       const int64_t nb = ((int64_t)g.x + 255) / 256;
       hipLaunchKernelGGL(zero_flags_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, p.fallback,
                          (int64_t)g.x);
-      hipLaunchKernelGGL(q128 ? flash_tri8_fast_kernel_bf16 : flash_tri_fast_kernel_bf16, g, dim3(64 * kRows), 0, st,
-                         p);
+      // the pipelined pass flags in the 128-query grid of the offset kernel
+      if (!(q128 && launch_flash_pipe(p, batch, st)))
+        hipLaunchKernelGGL(q128 ? flash_tri8_fast_kernel_bf16 : flash_tri_fast_kernel_bf16, g, dim3(64 * kRows), 0,
+                           st, p);
     }
     hipLaunchKernelGGL(q128 ? flash_tri8_kernel_bf16 : flash_tri_kernel_bf16, g, dim3(64 * kRows), 0, st, p);
   } else

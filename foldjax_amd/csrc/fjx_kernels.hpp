@@ -36,6 +36,7 @@ struct TriAttnPrologueParams {
   T* k;
   T* vt;            // [B][N][128][Np]
   T* bias;          // [B][4][Np][Np]
+  float* biasf;     // null, or the same bias in fp32 (for the pipelined flash kernel)
   float* mb;        // [B][N][Np]
   int64_t n;
   int64_t np;
@@ -124,6 +125,7 @@ struct FlashParams {
   const T* k;        // [B][N][H][Np][32]
   const T* vt;       // [B][N][H*32][Np]
   const T* bias;     // [B][H][Np][Np], already times log2 e
+  const float* biasf;  // null, or the same bias in fp32: the pipelined bf16 kernel stages it by LDS DMA
   const float* mb;   // [B][N][Np], already times log2 e; -inf for padded keys
   T* out;            // out[b][i][q][h*32+d] via the strides below
   int64_t n;
@@ -173,6 +175,9 @@ void launch_gate_unpad(const T* o, const T* g, int64_t ldg, T* out, int64_t rows
                        hipStream_t st);
 template <typename T>
 void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st);
+// the pipelined offset-free pass (fjx_flash_pipe.hip); false when the shape
+// or the parameters do not suit it (then nothing is launched)
+bool launch_flash_pipe(const FlashParams<bf16>& p, int64_t batch, hipStream_t st);
 
 // general-width paths (fjx_generic.hip); positions v = r*n + s of the virtual
 // grid read the original grid at s*n + r when t = 1
