@@ -25,7 +25,7 @@ FJX_ERR_UNSUPPORTED = 2
 FJX_ERR_WORKSPACE = 3
 FJX_ERR_HIP = 4
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 NOALLOC_SCRATCH_BYTES = 256 << 20
 
 _vp = ctypes.c_void_p
@@ -46,6 +46,7 @@ class TriMulArgs(ctypes.Structure):
         ("p_out_weight", _vp), ("g_out_weight", _vp),
         ("residual", _vp), ("out", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("out_mask", _vp),
     ]
 
 
@@ -58,6 +59,7 @@ class TriAttnArgs(ctypes.Structure):
         ("q_weight", _vp), ("k_weight", _vp), ("v_weight", _vp), ("g_weight", _vp), ("o_weight", _vp),
         ("residual", _vp), ("out", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
+        ("out_mask", _vp),
     ]
 
 
@@ -79,6 +81,7 @@ class TransitionArgs(ctypes.Structure):
         ("hidden", _i64), ("workspace", _vp), ("workspace_bytes", _sz),
         ("pb_n", _i64), ("pb_heads", _i64), ("pb_eps", _f32),
         ("pb_norm_weight", _vp), ("pb_norm_bias", _vp), ("pb_weight", _vp), ("pb_out", _vp),
+        ("out_mask", _vp),
     ]
 
 
@@ -94,6 +97,8 @@ class SingleAttentionArgs(ctypes.Structure):
         ("residual", _vp), ("out", _vp),
         ("workspace", _vp), ("workspace_bytes", _sz),
         ("pair_bias", _vp),
+        ("z_dtype", _i32), ("out_mask", _vp),
+        ("extra_bias", _vp), ("extra_bias_stride_b", _i64), ("extra_bias_stride_h", _i64),
     ]
 
 

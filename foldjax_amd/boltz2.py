@@ -183,7 +183,8 @@ def pairformer_layer_forward(
     Boltz-2 layer dict, or a ``foldjax_amd.pairformer.PairformerLayerWeights``."""
     from foldjax_amd.pairformer import PairformerLayerWeights
 
-    w = params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_boltz2(params, z.dtype, z.device)
+    w = params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_boltz2(
+        params, z.dtype, z.device, single_dtype=s.dtype)
     # selector validation as the reference's entry points do it
     resolve_matmul_precision(matmul_precision)
     if triangle_backend not in ("xla", "pallas", "tokamax", "cueq", "hip"):
@@ -231,6 +232,25 @@ def pairformer_no_seq_layer_forward(
     return kernels.transition(z, pack_transition_boltz2(params["transition_z"], dt, dev), residual=z, eps=eps)
 
 
+def stack_layer_params(layer_list, dtype: torch.dtype | None = None, device=None, single_dtype=None):
+    """``B2P/_scan_utils.py:18-27``: the layers' weights on a leading layer
+    axis (``foldjax_amd.stacking.StackedLayers``), packed once. Layers given
+    as Boltz-2 dicts are packed in ``dtype`` on ``device`` (the single track
+    in ``single_dtype``, default ``dtype``)."""
+    from foldjax_amd.pairformer import PairformerLayerWeights
+    from foldjax_amd.stacking import StackedLayers, stacked_or_stack
+
+    if not layer_list:
+        raise ValueError("stack_layer_params requires at least one layer")
+    if isinstance(layer_list, StackedLayers):
+        return layer_list
+    return stacked_or_stack([
+        lay if isinstance(lay, PairformerLayerWeights)
+        else PairformerLayerWeights.from_boltz2(lay, dtype, device, single_dtype=single_dtype)
+        for lay in layer_list
+    ])
+
+
 def pairformer_module_forward(
     params,
     s: torch.Tensor,
@@ -251,12 +271,16 @@ def pairformer_module_forward(
     """Boltz-2 ``pairformer_module_forward`` (``B2K/pairformer.py:30-97``):
     the layers of ``params["layers"]`` applied in order, each one
     ``pairformer_layer_forward``. A layer entry is the Boltz-2 layer dict or a
-    pre-packed ``PairformerLayerWeights`` (packing once and passing the packed
-    layers avoids re-laying out the weights on every call). ``use_scan`` and
-    the chunk arguments are accepted for signature parity: the reference uses
-    them to bound XLA's memory, while every layer here streams through fused
-    kernels with a fixed workspace, so both settings run the same loop."""
+    pre-packed ``PairformerLayerWeights``; ``params["layers"]`` may also be a
+    ``StackedLayers`` (``stack_layer_params``). With ``use_scan`` the layers
+    are packed and stacked once, as the reference stacks them for its scan;
+    without it each layer is used as given. The chunk arguments are accepted
+    for signature parity: the reference uses them to bound XLA's memory,
+    while every layer here streams through fused kernels with a fixed
+    workspace."""
     layers = params["layers"]
+    if use_scan:
+        layers = stack_layer_params(layers, z.dtype, z.device, single_dtype=s.dtype)
     for layer in layers:
         s, z = pairformer_layer_forward(
             layer,
@@ -275,4 +299,3 @@ def pairformer_module_forward(
             glu_backend=glu_backend,
         )
     return s, z
-

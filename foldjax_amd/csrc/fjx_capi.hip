@@ -280,6 +280,7 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   ep.w_pout = static_cast<const T*>(a->p_out_weight);
   ep.w_gout = static_cast<const T*>(a->g_out_weight);
   ep.residual = static_cast<const T*>(a->residual);
+  ep.out_mask = static_cast<const T*>(a->out_mask);
   ep.out = static_cast<T*>(a->out);
   ep.n = a->n;
   ep.eps = a->eps;
@@ -347,6 +348,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   ep.w_g = static_cast<const T*>(a->g_weight);
   ep.w_o = static_cast<const T*>(a->o_weight);
   ep.residual = static_cast<const T*>(a->residual);
+  ep.out_mask = static_cast<const T*>(a->out_mask);
   ep.out = static_cast<T*>(a->out);
   ep.n = n;
   ep.eps = a->eps;
@@ -414,6 +416,7 @@ int transition_run(const fjx_transition_args* a, bool pb_fused, hipStream_t st) 
   p.w_o = static_cast<const T*>(a->w_o);
   p.row_mask = static_cast<const T*>(a->row_mask);
   p.residual = static_cast<const T*>(a->residual);
+  p.out_mask = static_cast<const T*>(a->out_mask);
   p.out = static_cast<T*>(a->out);
   p.rows = a->rows;
   p.eps = a->eps;
@@ -440,7 +443,7 @@ template <typename T>
 int transition_pair_bias_pass(const fjx_transition_args* a, hipStream_t st) {
   const int64_t batch = a->rows / (a->pb_n * a->pb_n);
   return timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
-    launch_pair_bias<T>(static_cast<const T*>(a->out), static_cast<const T*>(a->pb_norm_weight),
+    launch_pair_bias<T, T>(static_cast<const T*>(a->out), static_cast<const T*>(a->pb_norm_weight),
                         static_cast<const T*>(a->pb_norm_bias), static_cast<const T*>(a->pb_weight),
                         static_cast<T*>(a->pb_out), batch, a->pb_n, round64(a->pb_n), (int)a->pb_heads, a->pb_eps,
                         st);
@@ -551,6 +554,7 @@ int trimul_generic_run(const fjx_trimul_args* a, hipStream_t st) {
     g = rows_gemm<T>(acm, rows, ch, a->p_out_weight, cz, static_cast<T*>(a->out), cz);
     g.gate = g2;
     g.residual = static_cast<const T*>(a->residual);
+    g.row_gate = static_cast<const T*>(a->out_mask);
     launch_gemm<T, T>(g, st);
   });
 }
@@ -638,8 +642,8 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
     if (a->g_weight) launch_gate_rows<T>(fp.out, proj, 4 * hd, 3 * hd, rows, (int)hd, st);
     T* y = at<T>(W, ws.y);
     launch_gemm<T, T>(rows_gemm<T>(fp.out, rows, hd, a->o_weight, cz, y, cz), st);
-    launch_scatter_add<T>(y, nullptr, static_cast<const T*>(a->residual), static_cast<T*>(a->out), rows, n, (int)cz,
-                          t, st);
+    launch_scatter_add<T>(y, nullptr, static_cast<const T*>(a->residual), static_cast<const T*>(a->out_mask),
+                          static_cast<T*>(a->out), rows, n, (int)cz, t, st);
   });
 }
 
@@ -683,7 +687,7 @@ int transition_generic_run(const fjx_transition_args* a, hipStream_t st) {
     launch_gemm<T, T>(g, st);
     launch_gemm<T, T>(rows_gemm<T>(h, rows, hid, a->w_o, c, y, c), st);
     launch_scatter_add<T>(y, static_cast<const T*>(a->row_mask), static_cast<const T*>(a->residual),
-                          static_cast<T*>(a->out), rows, 1, (int)c, 0, st);
+                          static_cast<const T*>(a->out_mask), static_cast<T*>(a->out), rows, 1, (int)c, 0, st);
   });
 }
 
@@ -714,7 +718,8 @@ SingleWs single_ws(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t
   return w;
 }
 
-template <typename T>
+// T: s, the weights and the attention; TZ: the pair tensor z
+template <typename T, typename TZ>
 int single_run(const fjx_single_attention_args* a, hipStream_t st) {
   const int64_t B = a->batch, n = a->n, cs = a->c_s, H = a->heads;
   const int64_t np = round64(n);
@@ -751,11 +756,16 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
     launch_key_mask<T>(static_cast<const T*>(a->mask), at<float>(W, ws.mb), B, n, np, a->inf, st);
   });
   if (rc) return rc;
-  if (!a->pair_bias) {
+  if (!a->pair_bias || a->extra_bias) {
     rc = timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
-      launch_pair_bias<T>(static_cast<const T*>(a->z), static_cast<const T*>(a->z_norm_weight),
-                          static_cast<const T*>(a->z_norm_bias), static_cast<const T*>(a->z_weight),
-                          at<T>(W, ws.bias), B, n, np, (int)H, a->eps, st);
+      if (!a->pair_bias)
+        launch_pair_bias<TZ, T>(static_cast<const TZ*>(a->z), static_cast<const T*>(a->z_norm_weight),
+                                static_cast<const T*>(a->z_norm_bias), static_cast<const T*>(a->z_weight),
+                                at<T>(W, ws.bias), B, n, np, (int)H, a->eps, st);
+      if (a->extra_bias)
+        launch_add_extra_bias<T>(static_cast<const T*>(a->pair_bias), at<T>(W, ws.bias),
+                                 static_cast<const T*>(a->extra_bias), a->extra_bias_stride_b, a->extra_bias_stride_h,
+                                 B, (int)H, n, np, st);
     });
     if (rc) return rc;
   }
@@ -764,7 +774,7 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
   fp.q = at<T>(W, ws.q);
   fp.k = at<T>(W, ws.k);
   fp.vt = at<T>(W, ws.vt);
-  fp.bias = a->pair_bias ? static_cast<const T*>(a->pair_bias) : at<T>(W, ws.bias);
+  fp.bias = a->pair_bias && !a->extra_bias ? static_cast<const T*>(a->pair_bias) : at<T>(W, ws.bias);
   fp.mb = at<float>(W, ws.mb);
   fp.out = at<T>(W, ws.o);
   fp.n = n;
@@ -794,6 +804,7 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
     g.ldc = cs;
     g.batches = 1;
     g.residual = static_cast<const T*>(a->residual);
+    g.row_gate = static_cast<const T*>(a->out_mask);
     launch_gemm<T, T>(g, st);
   });
 }
@@ -994,6 +1005,9 @@ int fjx_single_attention_fwd(const fjx_single_attention_args* a, hipStream_t st)
   if (a->batch < 1 || a->n < 1 || a->heads < 1)
     return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: batch, n and heads must be >= 1");
   if (!dtype_ok(a->dtype)) return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: unknown dtype %d", a->dtype);
+  if (!dtype_ok(a->z_dtype)) return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: unknown z_dtype %d", a->z_dtype);
+  if (a->extra_bias && (a->extra_bias_stride_b < 0 || a->extra_bias_stride_h < 0))
+    return fail(FJX_ERR_INVALID, "fjx_single_attention_fwd: extra_bias strides must be >= 0");
   if ((!a->pair_bias && a->c_z != 128) || a->c_s % a->heads != 0 || a->c_s / a->heads > 32 || a->c_s > 1024)
     return fail(FJX_ERR_UNSUPPORTED,
                 "fjx_single_attention_fwd: this build supports c_z == 128, heads dividing c_s <= 1024 with "
@@ -1013,7 +1027,9 @@ int fjx_single_attention_fwd(const fjx_single_attention_args* a, hipStream_t st)
   if (!a->workspace || a->workspace_bytes < need)
     return fail(FJX_ERR_WORKSPACE, "fjx_single_attention_fwd: workspace of %zu bytes needed, %zu given", need,
                 a->workspace_bytes);
-  return a->dtype == FJX_DTYPE_BF16 ? single_run<bf16>(a, st) : single_run<float>(a, st);
+  const bool bf = a->dtype == FJX_DTYPE_BF16, zbf = a->z_dtype == FJX_DTYPE_BF16;
+  if (bf) return zbf ? single_run<bf16, bf16>(a, st) : single_run<bf16, float>(a, st);
+  return zbf ? single_run<float, bf16>(a, st) : single_run<float, float>(a, st);
 }
 
 int fjx_prof_enable(int on) {

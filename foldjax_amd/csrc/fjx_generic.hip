@@ -213,12 +213,12 @@ __global__ void gate_rows_kernel(T* __restrict__ o, const T* __restrict__ g, int
   }
 }
 
-// out[b][orig(v)][c] = T(y[b][v][c] * m) + residual[b][orig(v)][c], with m
-// the row mask at the output position (1 without one)
+// out[b][orig(v)][c] = (T(y[b][v][c] * m) + residual[b][orig(v)][c]) * (g != 0),
+// with m the row mask and g the output mask at the output position (1 without)
 template <typename T>
 __global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
-                                   const T* __restrict__ residual, T* __restrict__ out, int64_t rows, int64_t n,
-                                   int c, int t) {
+                                   const T* __restrict__ residual, const T* __restrict__ out_mask,
+                                   T* __restrict__ out, int64_t rows, int64_t n, int c, int t) {
   const int64_t total = rows * c;
   const int64_t nn = n * n;
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
@@ -231,6 +231,7 @@ __global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict_
     if (row_mask) v *= to_f32(row_mask[o]);
     v = round_to<T>(v);
     if (residual) v += to_f32(residual[o * c + ch]);
+    if (out_mask && to_f32(out_mask[o]) == 0.f) v *= 0.f;
     out[o * c + ch] = from_f32<T>(v);
   }
 }
@@ -285,10 +286,10 @@ void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, i
   hipLaunchKernelGGL(gate_rows_kernel<T>, stride_grid(rows * width), dim3(256), 0, st, o, g, ldg, c0, rows, width);
 }
 template <typename T>
-void launch_scatter_add(const T* y, const T* row_mask, const T* residual, T* out, int64_t rows, int64_t n, int c,
-                        int t, hipStream_t st) {
-  hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out, rows,
-                     n, c, t);
+void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
+                        int64_t n, int c, int t, hipStream_t st) {
+  hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out_mask,
+                     out, rows, n, c, t);
 }
 
 #define FJX_INST(T)                                                                                                \
@@ -302,7 +303,8 @@ void launch_scatter_add(const T* y, const T* row_mask, const T* residual, T* out
   template void launch_bias_planes<T>(const T*, int64_t, int64_t, T*, int64_t, int64_t, int64_t, int, hipStream_t); \
   template void launch_grid_mask_bias<T>(const T*, float*, int64_t, int64_t, int64_t, float, int, hipStream_t);     \
   template void launch_gate_rows<T>(T*, const T*, int64_t, int64_t, int64_t, int, hipStream_t);                      \
-  template void launch_scatter_add<T>(const T*, const T*, const T*, T*, int64_t, int64_t, int, int, hipStream_t);
+  template void launch_scatter_add<T>(const T*, const T*, const T*, const T*, T*, int64_t, int64_t, int, int,     \
+                                      hipStream_t);
 FJX_INST(float)
 FJX_INST(bf16)
 #undef FJX_INST

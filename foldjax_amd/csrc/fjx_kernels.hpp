@@ -57,6 +57,7 @@ struct TriMulEpilogueParams {
   const T* w_pout;    // [128][128]
   const T* w_gout;    // [128][128]
   const T* residual;  // [B][N][N][128] or null (may alias out)
+  const T* out_mask;  // [B][N][N] or null: positions where it is 0 are written as 0
   T* out;
   int64_t n;
   float eps;
@@ -71,6 +72,7 @@ struct TriAttnEpilogueParams {
   const T* w_g;       // [128][128] or null (ungated)
   const T* w_o;       // [128][128]
   const T* residual;  // original grid, or null (may alias out)
+  const T* out_mask;  // original grid [B][N][N], or null: positions where it is 0 are written as 0
   T* out;             // original grid
   int64_t n;
   float eps;
@@ -90,6 +92,7 @@ struct GemmParams {
   int act;             // 0 none, 1 sigmoid, 2 silu
   const TO* gate;      // indexed like c, or null
   const TO* residual;  // indexed like c, or null (may alias c)
+  const TO* row_gate;  // [m] per output row, or null: rows where it is 0 are written as 0 (after the residual)
 };
 
 template <typename T>
@@ -102,6 +105,7 @@ struct TransitionParams {
   const T* w_o;       // [C][4C]
   const T* row_mask;  // [rows] or null
   const T* residual;  // [rows][C] or null (may alias out)
+  const T* out_mask;  // [rows] or null: rows where it is 0 are written as 0 (after the residual)
   T* out;             // [rows][C]
   int64_t rows;
   float eps;
@@ -163,9 +167,16 @@ void launch_layernorm_rows(const T* x, const T* w, const T* b, T* y, int64_t row
 template <typename T>
 void launch_split_heads(const T* qkv, int64_t ld, int64_t batch, int64_t n, int64_t np, int heads, int dh,
                         float q_mul, T* q, T* k, T* vt, hipStream_t st);
-template <typename T>
-void launch_pair_bias(const T* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
+// z (and its norm and weight) in TZ, the bias in T: the Boltz-2 single track
+// runs in fp32 over a bf16 pair tensor
+template <typename TZ, typename T>
+void launch_pair_bias(const TZ* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
                       int64_t np, int heads, float eps, hipStream_t st);
+// bias[b][h][q][k] (+)= log2(e) * extra[b * sb + h * sh + q * n + k] for q, k < n;
+// src (a prepared bias of the same layout) is read when given, else bias itself
+template <typename T>
+void launch_add_extra_bias(const T* src, T* bias, const T* extra, int64_t sb, int64_t sh, int64_t batch, int heads,
+                           int64_t n, int64_t np, hipStream_t st);
 template <typename T>
 void launch_pair_bias_border(T* bias, int64_t planes, int64_t n, int64_t np, hipStream_t st);
 template <typename T>
@@ -204,7 +215,7 @@ void launch_grid_mask_bias(const T* mask, float* mb, int64_t batch, int64_t n, i
 template <typename T>
 void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, int width, hipStream_t st);
 template <typename T>
-void launch_scatter_add(const T* y, const T* row_mask, const T* residual, T* out, int64_t rows, int64_t n, int c,
-                        int t, hipStream_t st);
+void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
+                        int64_t n, int c, int t, hipStream_t st);
 
 }  // namespace fjx

@@ -418,6 +418,11 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 #pragma unroll
           for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
+        if (P.out_mask) {
+          const float g = to_f32(P.out_mask[pos0 + pp]) != 0.f ? 1.f : 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[e] *= g;
+        }
         store8(P.out + off, pack8<T>(y));
       }
     }
@@ -533,6 +538,11 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
           else to_f32x8(load8(P.residual + off), rv);
 #pragma unroll
           for (int e = 0; e < 8; ++e) y[e] += rv[e];
+        }
+        if (P.out_mask) {
+          const float g = to_f32(P.out_mask[orig_of(tl, pp)]) != 0.f ? 1.f : 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[e] *= g;
         }
         store8(P.out + off, pack8<T>(y));
       }

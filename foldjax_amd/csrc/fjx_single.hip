@@ -81,8 +81,11 @@ __global__ void split_heads_kernel(const T* __restrict__ qkv, int64_t ld, int64_
 // weight, 16 heads per MFMA column tile, and each lane stores 4 consecutive
 // keys of one head. The next tile's z rows are loaded before the current one
 // is multiplied; the weight is held in registers when heads <= 16.
-template <typename T>
-__global__ __launch_bounds__(512) void pair_bias_kernel(const T* __restrict__ z, const T* __restrict__ ln_w,
+// z may be narrower than the bias (TZ = bf16, T = float: the fp32 single
+// track of Boltz-2 over a bf16 pair tensor); the LayerNorm runs in fp32 and
+// its output is stored in T, so the projection then runs at T's precision.
+template <typename TZ, typename T>
+__global__ __launch_bounds__(512) void pair_bias_kernel(const TZ* __restrict__ z, const T* __restrict__ ln_w,
                                                         const T* __restrict__ ln_b, const T* __restrict__ w,
                                                         T* __restrict__ bias, int64_t n, int64_t np, int heads,
                                                         float eps, int64_t ntiles) {
@@ -109,12 +112,12 @@ __global__ __launch_bounds__(512) void pair_bias_kernel(const T* __restrict__ z,
   load_heads(0, w0);
   stage_ln<T>(ln_w, ln_b, ln);
 
-  RowPart<T> xr;
+  RowPart<TZ> xr;
   auto fetch = [&](int64_t tile) {
     const TileRS tl = tile_at(tile, ntx, np);
     const int64_t kk = tl.s0 + p;
     const bool valid = tl.r < n && kk < n;
-    load_row_part<T>(valid ? z + (((int64_t)tl.b * n + tl.r) * n + kk) * kC : nullptr, xr);
+    load_row_part<TZ>(valid ? z + (((int64_t)tl.b * n + tl.r) * n + kk) * kC : nullptr, xr);
   };
 
   int64_t tile = blockIdx.x;
@@ -124,7 +127,7 @@ __global__ __launch_bounds__(512) void pair_bias_kernel(const T* __restrict__ z,
     const TileRS tl = tile_at(tile, ntx, np);
     const int nstore = (int)min<int64_t>(kTP, np - tl.s0);  // a multiple of 64
     const int nreal = tl.r < n ? (int)max<int64_t>(0, min<int64_t>(kTP, n - tl.s0)) : 0;
-    ln_quad<T>(xr, ln, eps, &xs[p][0]);
+    ln_quad<TZ>(xr, ln, eps, &xs[p][0]);
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
@@ -175,6 +178,26 @@ __global__ void pair_bias_border_kernel(T* __restrict__ bias, int64_t planes, in
       c = j - (r - n) * np;
     }
     bias[(plane * np + r) * np + c] = from_f32<T>(0.f);
+  }
+}
+
+// an additive attention bias given by the caller (Protenix's extra_attn_bias),
+// broadcast over batch (sb = 0) and heads (sh = 0), added in fp32 to the
+// projected bias: bias = src + log2(e) * extra over the real [n, n] block.
+// src is a prepared bias (read-only) or bias itself.
+template <typename T>
+__global__ void add_extra_bias_kernel(const T* __restrict__ src, T* __restrict__ bias, const T* __restrict__ extra,
+                                      int64_t sb, int64_t sh, int64_t batch, int heads, int64_t n, int64_t np) {
+  const int64_t total = batch * heads * n * n;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t k = idx % n;
+    const int64_t q = (idx / n) % n;
+    const int64_t h = (idx / (n * n)) % heads;
+    const int64_t b = idx / (n * n * heads);
+    const int64_t at = ((b * heads + h) * np + q) * np + k;
+    const float e = to_f32(extra[b * sb + h * sh + q * n + k]);
+    bias[at] = from_f32<T>(to_f32(src[at]) + e * kLog2e);
   }
 }
 
@@ -229,13 +252,20 @@ void launch_split_heads(const T* qkv, int64_t ld, int64_t batch, int64_t n, int6
   hipLaunchKernelGGL(split_heads_kernel<T>, grid_stride(batch * heads * np * 32), dim3(256), 0, st, qkv, ld, batch, n,
                      np, heads, dh, q_mul, q, k, vt);
 }
-template <typename T>
-void launch_pair_bias(const T* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
+template <typename TZ, typename T>
+void launch_pair_bias(const TZ* z, const T* ln_w, const T* ln_b, const T* w, T* bias, int64_t batch, int64_t n,
                       int64_t np, int heads, float eps, hipStream_t st) {
   const int64_t ntiles = (np + tile::kTP - 1) / tile::kTP * np * batch;
-  const unsigned grid = tile::persistent_grid(reinterpret_cast<const void*>(&pair_bias_kernel<T>), 512, ntiles);
-  hipLaunchKernelGGL(pair_bias_kernel<T>, dim3(grid), dim3(512), 0, st, z, ln_w, ln_b, w, bias, n, np, heads, eps,
-                     ntiles);
+  const unsigned grid =
+      tile::persistent_grid(reinterpret_cast<const void*>(&pair_bias_kernel<TZ, T>), 512, ntiles);
+  hipLaunchKernelGGL((pair_bias_kernel<TZ, T>), dim3(grid), dim3(512), 0, st, z, ln_w, ln_b, w, bias, n, np, heads,
+                     eps, ntiles);
+}
+template <typename T>
+void launch_add_extra_bias(const T* src, T* bias, const T* extra, int64_t sb, int64_t sh, int64_t batch, int heads,
+                           int64_t n, int64_t np, hipStream_t st) {
+  hipLaunchKernelGGL(add_extra_bias_kernel<T>, grid_stride(batch * heads * n * n), dim3(256), 0, st, src ? src : bias,
+                     bias, extra, sb, sh, batch, heads, n, np);
 }
 template <typename T>
 void launch_pair_bias_border(T* bias, int64_t planes, int64_t n, int64_t np, hipStream_t st) {
@@ -258,13 +288,19 @@ void launch_gate_unpad(const T* o, const T* g, int64_t ldg, T* out, int64_t rows
   template void launch_layernorm_rows<T>(const T*, const T*, const T*, T*, int64_t, int, float, hipStream_t);   \
   template void launch_split_heads<T>(const T*, int64_t, int64_t, int64_t, int64_t, int, int, float, T*, T*, T*, \
                                       hipStream_t);                                                              \
-  template void launch_pair_bias<T>(const T*, const T*, const T*, const T*, T*, int64_t, int64_t, int64_t, int,  \
-                                    float, hipStream_t);                                                         \
+  template void launch_pair_bias<T, T>(const T*, const T*, const T*, const T*, T*, int64_t, int64_t, int64_t, int, \
+                                       float, hipStream_t);                                                      \
+  template void launch_add_extra_bias<T>(const T*, T*, const T*, int64_t, int64_t, int64_t, int, int64_t, int64_t,  \
+                                         hipStream_t);                                                           \
   template void launch_pair_bias_border<T>(T*, int64_t, int64_t, int64_t, hipStream_t);                        \
   template void launch_key_mask<T>(const T*, float*, int64_t, int64_t, int64_t, float, hipStream_t);             \
   template void launch_gate_unpad<T>(const T*, const T*, int64_t, T*, int64_t, int, int, hipStream_t);
 FJX_INST(bf16)
 FJX_INST(float)
 #undef FJX_INST
+template void launch_pair_bias<bf16, float>(const bf16*, const float*, const float*, const float*, float*, int64_t,
+                                            int64_t, int64_t, int, float, hipStream_t);
+template void launch_pair_bias<float, bf16>(const float*, const bf16*, const bf16*, const bf16*, bf16*, int64_t,
+                                            int64_t, int64_t, int, float, hipStream_t);
 
 }  // namespace fjx

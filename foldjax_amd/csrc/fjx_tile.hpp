@@ -60,9 +60,9 @@ __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restric
 }
 
 // LayerNorm of 128 channels held by 4 consecutive threads (the chunks of
-// load_row_part), written to the same channels of dst_row as T
-template <typename T>
-__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, T* __restrict__ dst_row) {
+// load_row_part), written to the same channels of dst_row as TO
+template <typename T, typename TO>
+__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row) {
   float v[32];
 #pragma unroll
   for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
@@ -98,7 +98,7 @@ __device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, 
       o[e] = fmaf(fmaf(v[8 * q + e], rstd, shift), w0[e], b0[e]);
       o[4 + e] = fmaf(fmaf(v[8 * q + 4 + e], rstd, shift), w1[e], b1[e]);
     }
-    store8(dst_row + c, pack8<T>(o));
+    store8(dst_row + c, pack8<TO>(o));
   }
 }
 

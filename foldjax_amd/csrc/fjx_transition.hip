@@ -1,4 +1,4 @@
-// Fused transition: y = (silu(LN(x) Wa^T) * (LN(x) Wb^T)) Wo^T [* row_mask] [+ residual]
+// Fused transition: y = ((silu(LN(x) Wa^T) * (LN(x) Wb^T)) Wo^T [* row_mask] [+ residual]) [* (out_mask != 0)]
 // for rows of C = 128 channels with a 4C hidden width (Boltz-2 transition_forward,
 // Protenix transition, OpenFold3 swiglu_transition).
 //
@@ -165,6 +165,14 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) msk[rt] = to_f32(P.row_mask[m0 + min(16 * rt + (lane & 15), nvalid - 1)]);
   }
+  float gate[8];
+#pragma unroll
+  for (int rt = 0; rt < 8; ++rt) gate[rt] = 1.0f;
+  if (P.out_mask) {
+#pragma unroll
+    for (int rt = 0; rt < 8; ++rt)
+      gate[rt] = to_f32(P.out_mask[m0 + min(16 * rt + (lane & 15), nvalid - 1)]) != 0.f ? 1.f : 0.f;
+  }
 
   // the update is rounded to T (the reference's projection output is), then
   // the residual is added
@@ -180,6 +188,8 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
 #pragma unroll
         for (int q = 0; q < 4; ++q) y[q] += res[rt][q];
       }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) y[q] *= gate[rt];
       store4f(P.out + off, y);
       if (P.pb_out) store4f(&xs[row][col + 4 * (lane >> 4)], y);  // xs is free after the last chunk
     }

@@ -62,6 +62,18 @@ def _need_shape(name: str, t: torch.Tensor | None, shape) -> None:
         raise ValueError(f"{name} must have shape {tuple(int(v) for v in shape)}, got {tuple(t.shape)}")
 
 
+def _rows_of(m: torch.Tensor | None, shape, dtype: torch.dtype, name: str) -> torch.Tensor | None:
+    """A per-row (per-position) mask broadcast to ``shape`` in ``dtype``,
+    contiguous, as the kernels index it."""
+    if m is None:
+        return None
+    try:
+        m = torch.broadcast_to(m, tuple(shape))
+    except RuntimeError:
+        raise ValueError(f"{name} of shape {tuple(m.shape)} does not broadcast to {tuple(shape)}") from None
+    return m.to(dtype=dtype).contiguous()
+
+
 @dataclass(frozen=True)
 class TriMulWeights:
     """Tri-mul weights in the ABI layout (PyTorch ``[out, in]``, a rows first)."""
@@ -189,9 +201,11 @@ def transition(
     eps: float = 1e-5,
     pair_bias_for: SingleAttentionWeights | None = None,
     pair_bias_eps: float = 1e-5,
+    out_mask: torch.Tensor | None = None,
 ):
-    """``(silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T [* row_mask] [+ residual]``
-    over the last axis (``fjx_transition_fwd``).
+    """``((silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T [* row_mask] [+ residual])
+    [* (out_mask != 0)]`` over the last axis (``fjx_transition_fwd``);
+    ``row_mask`` and ``out_mask`` broadcast to ``x.shape[:-1]``.
 
     ``pair_bias_for``: the weights of the single attention that reads this
     pair transition's output next (``x`` is then ``[..., N, N, 128]``). The
@@ -203,7 +217,7 @@ def transition(
     not read again."""
     c = int(x.shape[-1])
     w.check(c)
-    _same_device(x, row_mask=row_mask, residual=residual)
+    _same_device(x, row_mask=row_mask, residual=residual, out_mask=out_mask)
     if residual is not None:
         _need_shape("residual", residual, x.shape)
     if pair_bias_for is not None:
@@ -224,9 +238,8 @@ def transition(
         pb_n, pb_heads = int(x.shape[-2]), pair_bias_for.heads
         np_ = (pb_n + 63) // 64 * 64
         pb = torch.empty((rows // (pb_n * pb_n), pb_heads, np_, np_), dtype=x.dtype, device=x.device)
-    rm = None
-    if row_mask is not None:
-        rm = torch.broadcast_to(row_mask, x.shape[:-1]).to(dtype=x.dtype).contiguous()
+    rm = _rows_of(row_mask, x.shape[:-1], x.dtype, "row_mask")
+    om = _rows_of(out_mask, x.shape[:-1], x.dtype, "out_mask")
     res = None if residual is None else residual.to(dtype=x.dtype).contiguous()
     hidden = int(w.w_a.shape[0])
     ws_bytes = lib.fjx_transition_workspace_size(rows, c, hidden, _code(x.dtype))
@@ -236,7 +249,7 @@ def transition(
         x=_ptr(xf), norm_weight=_ptr(w.norm_weight), norm_bias=_ptr(w.norm_bias),
         w_a=_ptr(w.w_a), w_b=_ptr(w.w_b), w_o=_ptr(w.w_o),
         row_mask=_ptr(rm), residual=_ptr(res), out=_ptr(out),
-        hidden=hidden, workspace=_ptr(ws), workspace_bytes=ws_bytes,
+        hidden=hidden, workspace=_ptr(ws), workspace_bytes=ws_bytes, out_mask=_ptr(om),
     )
     if pb is not None:
         a.pb_n, a.pb_heads, a.pb_eps = pb_n, pb_heads, float(pair_bias_eps)
@@ -260,17 +273,25 @@ def single_attention(
     eps: float = 1e-5,
     residual: torch.Tensor | None = None,
     pair_bias: torch.Tensor | None = None,
+    out_mask: torch.Tensor | None = None,
+    extra_bias: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Single-track attention with pair bias (``fjx_single_attention_fwd``).
     ``s`` ``[B, N, c_s]`` (or ``[N, c_s]``), ``z`` ``[B, N, N, c_z]``, ``mask``
-    ``[B, N]`` token mask. Returns the update, or ``residual + update``.
-    ``pair_bias``: the bias ``transition(..., pair_bias_for=w)`` prepared from
-    this ``z``; ``z`` is then not read (and may be None)."""
-    _same_device(s, z=z, mask=mask, residual=residual, pair_bias=pair_bias)
+    ``[B, N]`` token mask. Returns the update, or ``residual + update``, times
+    ``out_mask != 0`` per row when ``out_mask`` (``[B, N]``) is given.
+    ``s`` and the weights share one dtype; ``z`` may be float32 or bfloat16
+    independently (the Boltz-2 single track runs in float32 over a bfloat16
+    pair tensor). ``pair_bias``: the bias ``transition(..., pair_bias_for=w)``
+    prepared from this ``z`` in ``s``'s dtype; ``z`` is then not read (and may
+    be None). ``extra_bias``: an additive bias broadcasting to ``[B, H, N, N]``
+    from a 4-D tensor whose last two axes are ``[N, N]`` (Protenix's
+    ``extra_attn_bias``)."""
+    _same_device(s, z=z, mask=mask, residual=residual, pair_bias=pair_bias, out_mask=out_mask,
+                 extra_bias=extra_bias)
     if residual is not None:
         _need_shape("residual", residual, s.shape)
     w.check(int(s.shape[-1]), None if z is None else int(z.shape[-1]))
-    _dev(s)
     squeeze = s.dim() == 2
     sb = s.unsqueeze(0) if squeeze else s
     batch, n, c_s = (int(v) for v in sb.shape)
@@ -281,7 +302,8 @@ def single_attention(
         c_z = int(zb.shape[-1])
         if tuple(zb.shape[:3]) != (batch, n, n):
             raise ValueError(f"z must be [{batch}, {n}, {n}, c_z], got {tuple(z.shape)}")
-        zb = zb.to(dtype=s.dtype).contiguous()
+        _code(zb.dtype)
+        zb = zb.contiguous()
     if pair_bias is not None:
         np_ = (n + 63) // 64 * 64
         if (tuple(pair_bias.shape) != (batch, w.heads, np_, np_) or pair_bias.dtype != s.dtype
@@ -291,9 +313,22 @@ def single_attention(
     elif zb is None:
         raise ValueError("single_attention needs z or a prepared pair_bias")
     sb = sb.contiguous()
-    mb = None
-    if mask is not None:
-        mb = torch.broadcast_to(mask, (batch, n)).to(dtype=s.dtype).contiguous()
+    mb = _rows_of(mask, (batch, n), s.dtype, "mask")
+    om = _rows_of(out_mask, (batch, n), s.dtype, "out_mask")
+    eb, eb_sb, eb_sh = None, 0, 0
+    if extra_bias is not None:
+        if extra_bias.dim() != 4 or tuple(extra_bias.shape[-2:]) != (n, n):
+            raise ValueError(f"extra_bias must be a 4-D tensor [B or 1, H or 1, {n}, {n}], got {tuple(extra_bias.shape)}")
+        eb = extra_bias.to(dtype=s.dtype)
+        if eb.stride(-1) != 1 or eb.stride(-2) != n:
+            eb = eb.contiguous()
+        try:
+            eb = torch.broadcast_to(eb, (batch, w.heads, n, n))
+        except RuntimeError:
+            raise ValueError(f"extra_bias of shape {tuple(extra_bias.shape)} does not broadcast to "
+                             f"[{batch}, {w.heads}, {n}, {n}]") from None
+        eb_sb, eb_sh = int(eb.stride(0)), int(eb.stride(1))
+    _dev(s)
     res = None
     if residual is not None:
         res = (residual.unsqueeze(0) if squeeze else residual).to(dtype=s.dtype).contiguous()
@@ -310,7 +345,8 @@ def single_attention(
         q_weight=_ptr(w.q_weight), q_bias=_ptr(w.q_bias), k_weight=_ptr(w.k_weight), v_weight=_ptr(w.v_weight),
         g_weight=_ptr(w.g_weight), o_weight=_ptr(w.o_weight),
         residual=_ptr(res), out=_ptr(out), workspace=_ptr(ws), workspace_bytes=ws_bytes,
-        pair_bias=_ptr(pair_bias),
+        pair_bias=_ptr(pair_bias), z_dtype=_code(s.dtype if zb is None else zb.dtype), out_mask=_ptr(om),
+        extra_bias=_ptr(eb), extra_bias_stride_b=eb_sb, extra_bias_stride_h=eb_sh,
     )
     _check_weights(s, w)
     _lib.check(lib.fjx_single_attention_fwd(ctypes.byref(a), _stream(s)))
@@ -346,9 +382,11 @@ def trimul(
     residual: torch.Tensor | None = None,
     *,
     no_alloc: bool = False,
+    out_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Triangle multiplicative update (``fjx_trimul_fwd``); returns the update,
-    or ``residual + update`` when ``residual`` is given.
+    or ``residual + update`` when ``residual`` is given, times
+    ``out_mask != 0`` per position when ``out_mask`` (``[..., N, N]``) is given.
 
     ``no_alloc``: run ``fjx_trimul_fwd_noalloc`` instead, whose workspace is
     the library's static per-GPU scratch (shapes up to
@@ -356,11 +394,12 @@ def trimul(
     overlap). Only the output is allocated here."""
     if direction not in ("outgoing", "incoming"):
         raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
-    _same_device(x, residual=residual)
+    _same_device(x, residual=residual, out_mask=out_mask)
     if residual is not None:
         _need_shape("residual", residual, x.shape)
     c_h = w.check(int(x.shape[-1]))
     xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
+    om = _rows_of(out_mask, x.shape[:-1], x.dtype, "out_mask")
     _dev(x)
     lib = _lib.load()
     code = _code(x.dtype)
@@ -378,7 +417,7 @@ def trimul(
         norm_out_weight=_ptr(w.norm_out_weight), norm_out_bias=_ptr(w.norm_out_bias),
         p_out_weight=_ptr(w.p_out_weight), g_out_weight=_ptr(w.g_out_weight),
         residual=_ptr(res), out=_ptr(out),
-        workspace=_ptr(ws), workspace_bytes=ws_bytes,
+        workspace=_ptr(ws), workspace_bytes=ws_bytes, out_mask=_ptr(om),
     )
     _check_weights(x, w)
     entry = lib.fjx_trimul_fwd_noalloc if no_alloc else lib.fjx_trimul_fwd
@@ -394,14 +433,17 @@ def triattn(
     inf: float = 1e9,
     eps: float = 1e-5,
     residual: torch.Tensor | None = None,
+    out_mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Triangle attention, starting or ending node (``fjx_triattn_fwd``)."""
-    _same_device(x, residual=residual)
+    """Triangle attention, starting or ending node (``fjx_triattn_fwd``);
+    ``out_mask`` (``[..., N, N]``, indexed like the output) as for ``trimul``."""
+    _same_device(x, residual=residual, out_mask=out_mask)
     if residual is not None:
         _need_shape("residual", residual, x.shape)
     hd = w.check(int(x.shape[-1]))
     heads = w.heads
     xf, mf, lead, batch, n, c = _flatten_pair(x, mask)
+    om = _rows_of(out_mask, x.shape[:-1], x.dtype, "out_mask")
     _dev(x)
     lib = _lib.load()
     code = _code(x.dtype)
@@ -417,7 +459,7 @@ def triattn(
         q_weight=_ptr(w.q_weight), k_weight=_ptr(w.k_weight), v_weight=_ptr(w.v_weight),
         g_weight=_ptr(w.g_weight), o_weight=_ptr(w.o_weight),
         residual=_ptr(res), out=_ptr(out),
-        workspace=_ptr(ws), workspace_bytes=ws_bytes,
+        workspace=_ptr(ws), workspace_bytes=ws_bytes, out_mask=_ptr(om),
     )
     _check_weights(x, w)
     _lib.check(lib.fjx_triattn_fwd(ctypes.byref(a), _stream(x)))

@@ -3,7 +3,9 @@
 Order as in every port (``B2K/pairformer.py:133-172``,
 ``PXK/pairformer.py:49-140``, ``OF3/pair_block.py:106-190``): triangle
 multiplication outgoing, incoming, triangle attention starting node, ending
-node, each added to z as a residual (fused into the epilogue kernels).
+node, pair transition, each added to z as a residual (fused into the
+epilogue kernels); then the single track's attention with pair bias and
+transition.
 """
 
 from __future__ import annotations
@@ -24,12 +26,25 @@ class TriangleSublayers:
     tri_att_start: kernels.TriAttnWeights
     tri_att_end: kernels.TriAttnWeights
 
-    def forward(self, z: torch.Tensor, mask: torch.Tensor | None) -> torch.Tensor:
-        z = kernels.trimul(z, mask, self.tri_mul_out, "outgoing", residual=z)
-        z = kernels.trimul(z, mask, self.tri_mul_in, "incoming", residual=z)
-        z = kernels.triattn(z, mask, self.tri_att_start, starting=True, residual=z)
-        z = kernels.triattn(z, mask, self.tri_att_end, starting=False, residual=z)
-        return z
+    def forward(self, z: torch.Tensor, mask: torch.Tensor | None, *, inf: float = 1e9, eps: float = 1e-5,
+                out_mask: torch.Tensor | None = None, tri_mul_first: bool = True) -> torch.Tensor:
+        """z += each sublayer in turn (the residual fused into its epilogue);
+        with ``out_mask`` every sublayer's output is multiplied by
+        ``out_mask != 0`` (Protenix's ``z * pair_gate``). ``tri_mul_first``
+        orders the multiplication pair before the attention pair (OpenFold3's
+        ``pair_block`` option)."""
+
+        def mul_pair(z):
+            z = kernels.trimul(z, mask, self.tri_mul_out, "outgoing", eps=eps, residual=z, out_mask=out_mask)
+            return kernels.trimul(z, mask, self.tri_mul_in, "incoming", eps=eps, residual=z, out_mask=out_mask)
+
+        def att_pair(z):
+            z = kernels.triattn(z, mask, self.tri_att_start, starting=True, inf=inf, eps=eps, residual=z,
+                                out_mask=out_mask)
+            return kernels.triattn(z, mask, self.tri_att_end, starting=False, inf=inf, eps=eps, residual=z,
+                                   out_mask=out_mask)
+
+        return att_pair(mul_pair(z)) if tri_mul_first else mul_pair(att_pair(z))
 
     @classmethod
     def random(cls, dtype: torch.dtype, device, seed: int = 2, c_z: int = 128, heads: int = 4) -> "TriangleSublayers":
@@ -40,39 +55,113 @@ class TriangleSublayers:
         return cls(tm(seed), tm(seed + 1), ta(seed + 2), ta(seed + 3))
 
 
+def _same(t: torch.Tensor | None, u: torch.Tensor) -> bool:
+    return t is not None and t.dtype == u.dtype
+
+
 @dataclass
 class PairformerLayerWeights:
-    """One Pairformer layer (Boltz-2 layout of sublayers), packed for the HIP
-    kernels: the four triangle sublayers, the pair transition, the single
-    attention with pair bias (with the layer's ``pre_norm_s``) and the single
-    transition."""
+    """One Pairformer block packed for the HIP kernels: the four triangle
+    sublayers, the pair transition, and (when the block has a single track)
+    the single attention with pair bias and the single transition. The single
+    track may be packed in another dtype than the pair track (Boltz-2 runs it
+    in float32 over a bfloat16 pair tensor). One packed object serves every
+    port; the port's block function picks the forward below."""
 
     triangle: TriangleSublayers
     transition_z: kernels.TransitionWeights
-    attention: kernels.SingleAttentionWeights
-    transition_s: kernels.TransitionWeights
+    attention: kernels.SingleAttentionWeights | None
+    transition_s: kernels.TransitionWeights | None
+
+    def _pair_bias_prep(self, s: torch.Tensor | None, z: torch.Tensor):
+        """The attention whose pair bias the pair transition can emit: only
+        when the single track runs in the pair track's dtype (the prepared
+        bias is stored in that dtype)."""
+        if self.attention is None or s is None or not _same(self.attention.q_weight, z) or s.dtype != z.dtype:
+            return None
+        return self.attention
+
+    def _pair_transition(self, z, s, *, row_mask=None, out_mask=None, eps=1e-5):
+        att = self._pair_bias_prep(s, z)
+        if att is None:
+            return kernels.transition(z, self.transition_z, row_mask=row_mask, residual=z, eps=eps,
+                                      out_mask=out_mask), None
+        return kernels.transition(z, self.transition_z, row_mask=row_mask, residual=z, eps=eps, out_mask=out_mask,
+                                  pair_bias_for=att, pair_bias_eps=eps)
 
     def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor | None, pair_mask: torch.Tensor | None,
                 eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
-        """``B2K/pairformer.py:133-205``: z += tri-mul out, in, tri-attn start,
-        end, transition; s += attention(LN(s), z, mask); s += transition_s.
-        The attention's pair bias LN_z(z) w_z^T comes out of the pair
-        transition's epilogue, so z is not read a further time."""
-        z = self.triangle.forward(z, pair_mask)
-        z, bias = kernels.transition(z, self.transition_z, residual=z, eps=eps, pair_bias_for=self.attention,
-                                     pair_bias_eps=eps)
-        s = kernels.single_attention(s, None, mask, self.attention, residual=s, eps=eps, pair_bias=bias)
+        """Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:133-205``):
+        z += tri-mul out, in, tri-attn start, end, transition; s +=
+        attention(LN(s), z, mask); s += transition_s. When s runs in z's dtype
+        the attention's pair bias LN_z(z) w_z^T comes out of the pair
+        transition's epilogue, so z is not read a further time; a float32 s
+        over a bfloat16 z has the attention read z itself."""
+        z = self.triangle.forward(z, pair_mask, eps=eps)
+        z, bias = self._pair_transition(z, s, eps=eps)
+        s = kernels.single_attention(s, None if bias is not None else z, mask, self.attention, residual=s, eps=eps,
+                                     pair_bias=bias)
         s = kernels.transition(s, self.transition_s, residual=s, eps=eps)
         return s, z
 
-    @classmethod
-    def from_fields(cls, w: dict, dtype: torch.dtype, device) -> "PairformerLayerWeights":
-        """From torch-layout field dicts (``synthetic.pairformer_layer_weights``)."""
-        return cls.from_boltz2(P.pairformer_layer_to_boltz2(w), dtype, device)
+    def forward_protenix(self, s: torch.Tensor | None, z: torch.Tensor,
+                         pair_mask: torch.Tensor | None) -> tuple[torch.Tensor | None, torch.Tensor]:
+        """Protenix ``pairformer_block`` (``PXK/pairformer.py:49-180``). Every
+        sublayer's output is multiplied by ``pair_gate = bool(pair_mask)``
+        inside its epilogue. Gating z (and s) on entry as well is not needed
+        for finite inputs: a gated position enters the next sublayer only
+        where the pair mask already zeroes its contribution, and the first
+        output gate zeroes it. ``single_valid`` (the boolean diagonal of the
+        pair mask) is the single attention's key mask with ``inf = 1e10`` and
+        gates its output and the single transition's; the reference's extra
+        bias ``-1e10`` on invalid query rows changes only rows that the gate
+        then zeroes."""
+        valid = None
+        if pair_mask is not None:
+            valid = torch.diagonal(pair_mask, dim1=-2, dim2=-1).ne(0)
+        z = self.triangle.forward(z, pair_mask, out_mask=pair_mask)
+        z, bias = self._pair_transition(z, s, out_mask=pair_mask)
+        if self.attention is None:
+            if s is not None and valid is not None:
+                s = s * valid.to(s.dtype)[..., None]
+            return s, z
+        if s is None:
+            raise ValueError("PairformerBlock single path requires s")
+        if self.transition_s is None:
+            raise ValueError("missing single_transition for single path")
+        s = kernels.single_attention(s, None if bias is not None else z, valid, self.attention, inf=1e10,
+                                     residual=s, pair_bias=bias, out_mask=valid)
+        s = kernels.transition(s, self.transition_s, residual=s, out_mask=valid)
+        return s, z
+
+    def forward_openfold3(self, s: torch.Tensor, z: torch.Tensor, single_mask: torch.Tensor | None,
+                          pair_mask: torch.Tensor | None, *, inf: float = 1e9, mask_transition: bool = True,
+                          eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
+        """OpenFold3 ``pairformer_block`` (``OF3/pairformer.py:42-102``): the
+        pair block (``OF3/pair_block.py:106-190``), then s += attention with
+        pair bias (key mask ``single_mask``, ``inf``) and the SwiGLU single
+        transition, whose update is multiplied by ``single_mask`` when
+        ``mask_transition``."""
+        z = self.triangle.forward(z, pair_mask, inf=inf, eps=eps)
+        z, bias = self._pair_transition(z, s, row_mask=pair_mask if mask_transition else None, eps=eps)
+        s = kernels.single_attention(s, None if bias is not None else z, single_mask, self.attention, inf=inf,
+                                     eps=eps, residual=s, pair_bias=bias)
+        s = kernels.transition(s, self.transition_s, row_mask=single_mask if mask_transition else None, residual=s,
+                               eps=eps)
+        return s, z
 
     @classmethod
-    def from_boltz2(cls, p: dict, dtype: torch.dtype, device) -> "PairformerLayerWeights":
-        """From a Boltz-2 layer dict (``M/boltz2/bridge/torch_mapping.py:603-650``)."""
+    def from_fields(cls, w: dict, dtype: torch.dtype, device, single_dtype: torch.dtype | None = None
+                    ) -> "PairformerLayerWeights":
+        """From torch-layout field dicts (``synthetic.pairformer_layer_weights``)."""
+        return cls.from_boltz2(P.pairformer_layer_to_boltz2(w), dtype, device, single_dtype=single_dtype)
+
+    @classmethod
+    def from_boltz2(cls, p: dict, dtype: torch.dtype, device, single_dtype: torch.dtype | None = None
+                    ) -> "PairformerLayerWeights":
+        """From a Boltz-2 layer dict (``M/boltz2/bridge/torch_mapping.py:603-650``);
+        the single track in ``single_dtype`` (default: ``dtype``)."""
+        sd = dtype if single_dtype is None else single_dtype
         tri = TriangleSublayers(
             P.pack_trimul_boltz2(p["tri_mul_out"], dtype, device),
             P.pack_trimul_boltz2(p["tri_mul_in"], dtype, device),
@@ -82,13 +171,62 @@ class PairformerLayerWeights:
         return cls(
             triangle=tri,
             transition_z=P.pack_transition_boltz2(p["transition_z"], dtype, device),
-            attention=P.pack_single_attention_boltz2(p["attention"], dtype, device, pre_norm=p["pre_norm_s"]),
-            transition_s=P.pack_transition_boltz2(p["transition_s"], dtype, device),
+            attention=P.pack_single_attention_boltz2(p["attention"], sd, device, pre_norm=p["pre_norm_s"]),
+            transition_s=P.pack_transition_boltz2(p["transition_s"], sd, device),
         )
 
     @classmethod
-    def random(cls, dtype: torch.dtype, device, seed: int = 2) -> "PairformerLayerWeights":
-        return cls.from_fields(syn.pairformer_layer_weights(seed=seed), dtype, device)
+    def from_protenix(cls, p, dtype: torch.dtype, device, single_dtype: torch.dtype | None = None
+                      ) -> "PairformerLayerWeights":
+        """From a Protenix ``PairformerBlockParams`` (``PXK/pairformer.py:31-41``);
+        fields may already be packed weight objects."""
+        sd = dtype if single_dtype is None else single_dtype
+
+        def pk(obj, packer, kind, dt):
+            return obj if isinstance(obj, kind) else packer(obj, dt, device)
+
+        tri = TriangleSublayers(
+            pk(p.tri_mul_out, P.pack_trimul_torch, kernels.TriMulWeights, dtype),
+            pk(p.tri_mul_in, P.pack_trimul_torch, kernels.TriMulWeights, dtype),
+            pk(p.tri_att_start, P.pack_triattn_protenix, kernels.TriAttnWeights, dtype),
+            pk(p.tri_att_end, P.pack_triattn_protenix, kernels.TriAttnWeights, dtype),
+        )
+        apb, st = p.attention_pair_bias, p.single_transition
+        return cls(
+            triangle=tri,
+            transition_z=pk(p.pair_transition, P.pack_transition_torch, kernels.TransitionWeights, dtype),
+            attention=None if apb is None else pk(apb, P.pack_single_attention_protenix,
+                                                  kernels.SingleAttentionWeights, sd),
+            transition_s=None if st is None else pk(st, P.pack_transition_torch, kernels.TransitionWeights, sd),
+        )
+
+    @classmethod
+    def from_openfold3(cls, p, dtype: torch.dtype, device, single_dtype: torch.dtype | None = None
+                       ) -> "PairformerLayerWeights":
+        """From an OpenFold3 ``PairformerBlockParams`` (``OF3/pairformer.py:27-33``)."""
+        sd = dtype if single_dtype is None else single_dtype
+
+        def pk(obj, packer, kind, dt):
+            return obj if isinstance(obj, kind) else packer(obj, dt, device)
+
+        ps = p.pair_stack
+        tri = TriangleSublayers(
+            pk(ps.tri_mul_out, P.pack_trimul_torch, kernels.TriMulWeights, dtype),
+            pk(ps.tri_mul_in, P.pack_trimul_torch, kernels.TriMulWeights, dtype),
+            pk(ps.tri_att_start, P.pack_triattn_openfold3, kernels.TriAttnWeights, dtype),
+            pk(ps.tri_att_end, P.pack_triattn_openfold3, kernels.TriAttnWeights, dtype),
+        )
+        return cls(
+            triangle=tri,
+            transition_z=pk(ps.pair_transition, P.pack_transition_openfold3, kernels.TransitionWeights, dtype),
+            attention=pk(p.attn_pair_bias, P.pack_single_attention_openfold3, kernels.SingleAttentionWeights, sd),
+            transition_s=pk(p.single_transition, P.pack_transition_openfold3, kernels.TransitionWeights, sd),
+        )
+
+    @classmethod
+    def random(cls, dtype: torch.dtype, device, seed: int = 2, single_dtype: torch.dtype | None = None
+               ) -> "PairformerLayerWeights":
+        return cls.from_fields(syn.pairformer_layer_weights(seed=seed), dtype, device, single_dtype=single_dtype)
 
 
 def flops_triangle(n: int, c: int = 128, heads: int = 4, head_dim: int = 32) -> dict[str, float]:

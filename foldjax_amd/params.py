@@ -93,6 +93,71 @@ class OpenFold3PairBlockParams(NamedTuple):
     pair_transition: object
 
 
+class ProtenixAttentionPairBiasParams(NamedTuple):
+    """Protenix ``AttentionPairBiasParams`` (``PXP/attention.py:32-41``)."""
+
+    layernorm_a: Any
+    layernorm_kv: Any
+    attention: AttentionParams
+    layernorm_z: LayerNormParams
+    linear_z: LinearParams
+    linear_a_last: Any = None
+    has_s: bool = False
+    cross_attention_mode: bool = False
+
+
+class ProtenixTransitionParams(NamedTuple):
+    """Protenix ``TransitionParams`` (``PXP/primitives.py:30-36``)."""
+
+    layer_norm: LayerNormParams
+    linear_a: LinearParams
+    linear_b: LinearParams
+    linear_out: LinearParams
+
+
+class ProtenixPairformerBlockParams(NamedTuple):
+    """Protenix ``PairformerBlockParams`` (``PXK/pairformer.py:31-41``). Each
+    field is the reference's container or a pre-packed weight object of
+    ``foldjax_amd.kernels``."""
+
+    tri_mul_out: Any
+    tri_mul_in: Any
+    tri_att_start: Any
+    tri_att_end: Any
+    pair_transition: Any
+    attention_pair_bias: Any = None
+    single_transition: Any = None
+
+
+class ProtenixPairformerStackParams(NamedTuple):
+    """Protenix ``PairformerStackParams`` (``PXK/pairformer.py:44-47``)."""
+
+    blocks: tuple
+
+
+class OpenFold3AttentionPairBiasParams(NamedTuple):
+    """OpenFold3 trunk ``AttentionPairBiasParams`` (``OF3/attention_pair_bias.py:30-37``)."""
+
+    layer_norm_a: LayerNormParams
+    layer_norm_z: LayerNormParams
+    linear_z: LinearParams
+    mha: AttentionParams
+
+
+class OpenFold3PairformerBlockParams(NamedTuple):
+    """OpenFold3 ``PairformerBlockParams`` (``OF3/pairformer.py:27-33``)."""
+
+    pair_stack: Any
+    attn_pair_bias: Any
+    single_transition: Any
+
+
+class OpenFold3PairformerStackParams(NamedTuple):
+    """OpenFold3 ``PairformerStackParams`` (``OF3/pairformer.py:36-39``)."""
+
+    blocks: tuple
+
+
 def _t(x) -> torch.Tensor:
     if isinstance(x, torch.Tensor):
         return x
@@ -382,3 +447,107 @@ def pairformer_layer_to_boltz2(w: dict) -> dict:
         "attention": att,
         "transition_s": transition_to_boltz2(w["transition_s"]),
     }
+
+
+# --------------------------------------- single attention, Protenix / OpenFold3
+
+
+def _pack_single_attention_torch(ln_a, att, ln_z, lin_z, dtype, device) -> SingleAttentionWeights:
+    """The gated attention with pair bias of the Protenix and OpenFold3 trunks:
+    ``linear_q`` may carry a bias (both ports map it so,
+    ``M/protenix/bridge/torch_mapping.py:175-198``,
+    ``M/openfold3/bridge/torch_mapping.py:153-177``); every other projection is
+    bias-free. A LayerNorm without weight or bias packs ones or zeros."""
+    if att is None:
+        raise ValueError("missing attention parameters")
+    if ln_a is None:
+        raise ValueError("missing attention pair-bias normalization params")
+    if _get(att, "linear_g") is None:
+        raise ValueError("the hip attention with pair bias needs a gated attention (linear_g)")
+    lq = _get(att, "linear_q")
+    q = _t(_get(lq, "weight"))
+    c_s = q.shape[1]
+    qb = _get(lq, "bias")
+    z_w = _weight(lin_z, "linear_z")
+    pw, pb = _ln(ln_a, c_s)
+    zw, zb = _ln(ln_z, z_w.shape[1])
+    w = SingleAttentionWeights(
+        pre_norm_weight=pw, pre_norm_bias=pb, z_norm_weight=zw, z_norm_bias=zb, z_weight=z_w,
+        q_weight=q, q_bias=None if qb is None else _t(qb),
+        k_weight=_weight(_get(att, "linear_k"), "linear_k"), v_weight=_weight(_get(att, "linear_v"), "linear_v"),
+        g_weight=_weight(_get(att, "linear_g"), "linear_g"), o_weight=_weight(_get(att, "linear_o"), "linear_o"),
+    )
+    return w.to(dtype, device)
+
+
+def pack_single_attention_protenix(params, dtype: torch.dtype, device) -> SingleAttentionWeights:
+    """Protenix ``AttentionPairBiasParams`` in its trunk form (``has_s=False``,
+    no cross attention, ``PXK/pairformer.py:150-154``): ``layernorm_a`` is the
+    attention's own pre-norm, ``linear_z`` the pair-bias projection."""
+    if _get(params, "has_s") or _get(params, "cross_attention_mode"):
+        raise ValueError("the hip attention with pair bias supports the trunk form "
+                         "(has_s=False, cross_attention_mode=False)")
+    return _pack_single_attention_torch(_get(params, "layernorm_a"), _get(params, "attention"),
+                                        _get(params, "layernorm_z"), _get(params, "linear_z"), dtype, device)
+
+
+def pack_single_attention_openfold3(params, dtype: torch.dtype, device) -> SingleAttentionWeights:
+    """OpenFold3 trunk ``AttentionPairBiasParams(layer_norm_a, layer_norm_z,
+    linear_z, mha)``."""
+    return _pack_single_attention_torch(_get(params, "layer_norm_a"), _get(params, "mha"),
+                                        _get(params, "layer_norm_z"), _get(params, "linear_z"), dtype, device)
+
+
+def single_attention_to_protenix(w: dict) -> ProtenixAttentionPairBiasParams:
+    """Torch-layout dict (``synthetic.single_attention_weights``) -> Protenix
+    container: ``pre_norm_s`` becomes ``layernorm_a``."""
+    return ProtenixAttentionPairBiasParams(
+        layernorm_a=_lnp(w["pre_norm_s"]), layernorm_kv=None,
+        attention=AttentionParams(linear_q=_lin(w["proj_q"]), linear_k=_lin(w["proj_k"]), linear_v=_lin(w["proj_v"]),
+                                  linear_o=_lin(w["proj_o"]), linear_g=_lin(w["proj_g"])),
+        layernorm_z=_lnp(w["proj_z_norm"]), linear_z=_lin(w["proj_z"]),
+    )
+
+
+def single_attention_to_openfold3(w: dict) -> OpenFold3AttentionPairBiasParams:
+    px = single_attention_to_protenix(w)
+    return OpenFold3AttentionPairBiasParams(layer_norm_a=px.layernorm_a, layer_norm_z=px.layernorm_z,
+                                            linear_z=px.linear_z, mha=px.attention)
+
+
+def transition_to_protenix(w: dict) -> ProtenixTransitionParams:
+    return ProtenixTransitionParams(layer_norm=_lnp(w["layer_norm"]), linear_a=_lin(w["linear_a"]),
+                                    linear_b=_lin(w["linear_b"]), linear_out=_lin(w["linear_out"]))
+
+
+def transition_to_openfold3(w: dict) -> dict:
+    """Field dict -> OpenFold3 ``SwiGLUTransitionParams`` shape
+    (``layer_norm``, ``swiglu.linear_a/b``, ``linear_out``)."""
+    return {"layer_norm": _lnp(w["layer_norm"]),
+            "swiglu": {"linear_a": _lin(w["linear_a"]), "linear_b": _lin(w["linear_b"])},
+            "linear_out": _lin(w["linear_out"])}
+
+
+def pairformer_block_to_protenix(w: dict) -> ProtenixPairformerBlockParams:
+    """Field dicts of one layer (``synthetic.pairformer_layer_weights``) ->
+    Protenix ``PairformerBlockParams``."""
+    return ProtenixPairformerBlockParams(
+        tri_mul_out=trimul_to_protenix(w["tri_mul_out"]), tri_mul_in=trimul_to_protenix(w["tri_mul_in"]),
+        tri_att_start=triattn_to_protenix(w["tri_att_start"]), tri_att_end=triattn_to_protenix(w["tri_att_end"]),
+        pair_transition=transition_to_protenix(w["transition_z"]),
+        attention_pair_bias=single_attention_to_protenix(w["attention"]),
+        single_transition=transition_to_protenix(w["transition_s"]),
+    )
+
+
+def pairformer_block_to_openfold3(w: dict) -> OpenFold3PairformerBlockParams:
+    """Field dicts of one layer -> OpenFold3 ``PairformerBlockParams``."""
+    return OpenFold3PairformerBlockParams(
+        pair_stack=OpenFold3PairBlockParams(
+            tri_mul_out=trimul_to_openfold3(w["tri_mul_out"]), tri_mul_in=trimul_to_openfold3(w["tri_mul_in"]),
+            tri_att_start=triattn_to_openfold3(w["tri_att_start"]), tri_att_end=triattn_to_openfold3(w["tri_att_end"]),
+            pair_transition=transition_to_openfold3(w["transition_z"]),
+        ),
+        attn_pair_bias=single_attention_to_openfold3(w["attention"]),
+        single_transition=transition_to_openfold3(w["transition_s"]),
+    )

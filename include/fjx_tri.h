@@ -15,6 +15,15 @@
  * 16-byte aligned (the kernels move rows in 16-byte pieces); masks need only
  * element alignment. A misaligned pointer is rejected with FJX_ERR_INVALID.
  *
+ * Output masks: every pair- and single-track entry point takes an optional
+ * out_mask (same element type as the activations, one element per output
+ * position or row). Where it is 0 the written value, residual included, is
+ * multiplied by 0; elsewhere it is left alone. This is Protenix's re-masking
+ * z = z * pair_gate after every sublayer and s = s * single_gate after each
+ * single-track sublayer (pair_gate = bool(pair_mask)),
+ * src/foldjax/models/protenix/models/trunk_blocks/pairformer.py:99-149,
+ * fused into the kernel that writes the output.
+ *
  * Reference interfaces replaced (paths relative to the eightmm/FoldJAX tree):
  *   fjx_trimul_fwd     cuex.triangle_multiplicative_update as called from
  *                      src/foldjax/models/boltz2/models/triangle/triangle_cueq.py:88-102
@@ -40,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FJX_ABI_VERSION 4
+#define FJX_ABI_VERSION 5
 
 /* element types of activations, masks and weights */
 enum { FJX_DTYPE_F32 = 0, FJX_DTYPE_BF16 = 1 };
@@ -99,6 +108,7 @@ typedef struct fjx_trimul_args {
   void* out;                   /* [batch, n, n, c_z] */
   void* workspace;
   size_t workspace_bytes;
+  const void* out_mask;        /* NULL, or [batch, n, n]: see "Output masks" */
 } fjx_trimul_args;
 
 size_t fjx_trimul_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype);
@@ -169,6 +179,7 @@ typedef struct fjx_triattn_args {
   void* out;                /* [batch, n, n, c_z] */
   void* workspace;
   size_t workspace_bytes;
+  const void* out_mask;     /* NULL, or [batch, n, n] indexed like out (never swapped) */
 } fjx_triattn_args;
 
 size_t fjx_triattn_workspace_size(int64_t batch, int64_t n, int64_t c_z, int64_t heads,
@@ -208,7 +219,7 @@ int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
 
 /*
  * Transition (pair or single track): for every row of c channels
- *   out = (silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T  [* row_mask]  [+ residual]
+ *   out = ((silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T  [* row_mask]  [+ residual])  [* (out_mask != 0)]
  * Replaces src/foldjax/models/boltz2/models/primitives/transition.py:39-122
  * (fc1 = w_a, fc2 = w_b, fc3 = w_o), protenix/models/primitives/primitives.py:117-146
  * and openfold3/models/primitives.py:133-150 (row_mask = the OpenFold3 mask).
@@ -255,6 +266,7 @@ typedef struct fjx_transition_args {
   const void* pb_norm_bias;
   const void* pb_weight;       /* [pb_heads, c] */
   void* pb_out;                /* fjx_pair_bias_size(rows / pb_n^2, pb_n, pb_heads, dtype) bytes, or NULL */
+  const void* out_mask;        /* NULL, or [rows]: see "Output masks"; the pair bias is taken of the masked rows */
 } fjx_transition_args;
 
 size_t fjx_transition_workspace_size(int64_t rows, int64_t c, int64_t hidden, int32_t dtype);
@@ -263,16 +275,24 @@ size_t fjx_pair_bias_size(int64_t batch, int64_t n, int64_t heads, int32_t dtype
 int fjx_transition_fwd(const fjx_transition_args* args, hipStream_t stream);
 
 /*
- * Single-track attention with pair bias of a Pairformer layer, Boltz-2 form
- * (src/foldjax/models/boltz2/models/primitives/attention.py:19-115 called from
- * trunk_blocks/pairformer.py:182-201):
+ * Single-track attention with pair bias of a Pairformer block, in the form
+ * all three ports share:
+ *   Boltz-2   src/foldjax/models/boltz2/models/primitives/attention.py:19-115,
+ *             called from trunk_blocks/pairformer.py:182-201 (inf = 1e6; fp32
+ *             s and weights over the bf16 pair tensor: dtype F32, z_dtype BF16);
+ *   Protenix  src/foldjax/models/protenix/models/primitives/attention.py:108-169
+ *             (layernorm_a = pre_norm; extra_attn_bias = extra_bias);
+ *   OpenFold3 src/foldjax/models/openfold3/models/attention_pair_bias.py:40-75
+ *             (layer_norm_a = pre_norm; inf = 1e9).
  *   s_ln = LN_pre(s)            (s itself when pre_norm_weight is NULL)
  *   q = s_ln w_q^T + b_q, k = s_ln w_k^T, v = s_ln w_v^T, g = sigmoid(s_ln w_g^T)
- *   bias[b,h,i,j] = LN_z(z[b,i,j]) w_z[h]^T
+ *   bias[b,h,i,j] = LN_z(z[b,i,j]) w_z[h]^T  (+ extra_bias[b,h,i,j])
  *   o = softmax(q k^T / sqrt(d) + bias + (1 - mask[b,j]) * (-inf)) v
- *   out = (g * o) w_o^T  (+ residual)
+ *   out = ((g * o) w_o^T  (+ residual))  (* (out_mask[b,i] != 0))
  * Weights PyTorch [out, in]. Supported: c_z == 128, heads * head_dim == c_s,
- * head_dim <= 32.
+ * head_dim <= 32. s, the weights, extra_bias, residual, out and a prepared
+ * pair_bias are `dtype`; z is `z_dtype` (either may be narrower: the bias is
+ * computed at `dtype`'s precision from z's values).
  */
 typedef struct fjx_single_attention_args {
   int64_t batch;
@@ -303,6 +323,11 @@ typedef struct fjx_single_attention_args {
   size_t workspace_bytes;
   const void* pair_bias; /* a bias prepared by fjx_transition_fwd's pb_out for this z, or NULL;
                             when given, z, z_norm_* and z_weight are not read and may be NULL */
+  int32_t z_dtype;       /* element type of z; set it even when it equals dtype (FJX_DTYPE_F32 is 0) */
+  const void* out_mask;  /* NULL, or [batch, n]: see "Output masks" */
+  const void* extra_bias;        /* NULL, or [n, n] planes added to the bias, element (b, h, i, j) at */
+  int64_t extra_bias_stride_b;   /* extra_bias[b * stride_b + h * stride_h + i * n + j]; a stride of 0 */
+  int64_t extra_bias_stride_h;   /* broadcasts that axis */
 } fjx_single_attention_args;
 
 size_t fjx_single_attention_workspace_size(int64_t batch, int64_t n, int64_t c_s, int64_t heads, int32_t dtype);

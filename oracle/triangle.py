@@ -611,3 +611,162 @@ def pair_bias_at(p, z, positions, *, eps=1e-5):
     rows = np.stack([_f(z[i])[j] for i, j in positions])
     return linear_torch(layer_norm(rows, p["proj_z_norm"]["weight"], p["proj_z_norm"]["bias"], eps),
                         {"weight": p["proj_z"]["weight"]})
+
+
+# ---------------------------------------------------------------------------
+# Protenix and OpenFold3 single attention with pair bias, and their blocks
+# ---------------------------------------------------------------------------
+
+
+def gated_attention(q_x, kv_x, att, num_heads, biases=()):
+    """Gated multi-head attention of the Protenix and OpenFold3 ports.
+
+    Protenix ``attention`` (``PXP/attention.py:60-99``: ``prepare_qkv`` :43-57
+    splits heads and divides q by ``sqrt(d)``, ``_attention_qkv_chunk``
+    :374-378 adds the bias and softmaxes, the gate is
+    ``sigmoid(linear(q_x, linear_g))`` per head) and OpenFold3 ``attention``
+    (``OF3/attention.py:71-112``, the same steps with the biases added in
+    order). ``biases`` broadcast against ``[..., H, Q, K]``.
+    """
+    q_x = _f(q_x)
+    kv_x = _f(kv_x)
+    q = _split_heads_torch(q_x, _get(att, "linear_q"), num_heads)  # [..., H, Q, D]
+    k = _split_heads_torch(kv_x, _get(att, "linear_k"), num_heads)
+    v = _split_heads_torch(kv_x, _get(att, "linear_v"), num_heads)
+    q = q / np.sqrt(q.shape[-1])
+    logits = np.ascontiguousarray(q) @ np.ascontiguousarray(np.swapaxes(k, -1, -2))
+    for b in biases:
+        logits = logits + _f(b)
+    o = np.swapaxes(softmax(logits, axis=-1) @ np.ascontiguousarray(v), -2, -3)  # [..., Q, H, D]
+    if _get(att, "linear_g") is not None:
+        o = o * sigmoid(linear_torch(q_x, _get(att, "linear_g"))).reshape(o.shape)
+    return linear_torch(o.reshape(o.shape[:-2] + (-1,)), _get(att, "linear_o"))
+
+
+def protenix_attention_pair_bias(a, z, params, *, num_heads, extra_attn_bias=None, eps=1e-5):
+    """Protenix ``attention_pair_bias`` (``PXP/attention.py:108-169``), trunk
+    form (``has_s=False``, no cross attention, ``z`` not pre-normalised):
+    ``q_x = LN_a(a)``; ``bias = LN_z(z) W_z^T`` moved to ``[..., H, N, N]``;
+    ``extra_attn_bias`` (``[..., N, N]`` or ``[..., H, N, N]``) is added after
+    the rank alignment of :140-150; then ``gated_attention(q_x, q_x, ...)``.
+    Returns the update."""
+    q_x = layer_norm(a, *_ln_params(_get(params, "layernorm_a")), eps=eps)
+    bias = np.moveaxis(linear_torch(layer_norm(z, *_ln_params(_get(params, "layernorm_z")), eps=eps),
+                                    _get(params, "linear_z")), -1, -3)
+    if extra_attn_bias is not None:
+        e = _f(extra_attn_bias)
+        while e.ndim < bias.ndim - 1:
+            e = e[None]
+        if e.ndim == bias.ndim - 1:
+            e = np.expand_dims(e, -3)
+        bias = bias + e
+    return gated_attention(q_x, q_x, _get(params, "attention"), num_heads, (bias,))
+
+
+def openfold3_attention_pair_bias(a, z, params, *, no_heads, mask=None, inf=1e9, eps=1e-5):
+    """OpenFold3 trunk ``attention_pair_bias`` (``OF3/attention_pair_bias.py:40-75``):
+    ``a = LN_a(a)``; ``mask_bias = inf (mask - 1)`` over keys; ``pair_bias =
+    LN_z(z) W_z^T`` as ``[..., H, N, N]``; ``attention(a, a, mha, biases=(mask_bias,
+    pair_bias))``. Returns the update."""
+    a = layer_norm(a, *_ln_params(_get(params, "layer_norm_a")), eps=eps)
+    if mask is None:
+        mask = np.ones(a.shape[:-1])
+    mask_bias = (inf * (_f(mask) - 1.0))[..., None, None, :]
+    pair_bias = np.moveaxis(linear_torch(layer_norm(z, *_ln_params(_get(params, "layer_norm_z")), eps=eps),
+                                         _get(params, "linear_z")), -1, -3)
+    return gated_attention(a, a, _get(params, "mha"), no_heads, (mask_bias, pair_bias))
+
+
+def protenix_pairformer_block(s, z, pair_mask, params):
+    """Protenix ``pairformer_block`` (``PXK/pairformer.py:49-180``).
+
+    With a pair mask: ``pair_gate = bool(pair_mask)`` multiplies z at entry and
+    after every sublayer (:74-77, 99-149); ``single_valid`` is the diagonal of
+    the boolean pair mask, ``single_gate`` gates s at entry and after each
+    single-track sublayer, and the single attention gets the extra bias
+    ``-1e10`` wherever query or key is invalid (:80-87). The ending-node
+    attention is a starting module between two transposes (:123-140). Heads
+    come from the weight shapes (:112, :157). ``params`` is a dict (or
+    NamedTuple) with the fields of ``PairformerBlockParams`` (:31-41), the
+    triangle sublayers in the Protenix field names. Returns ``(s, z)``.
+    """
+    z = _f(z)
+    s = None if s is None else _f(s)
+    pair_gate = single_gate = extra = None
+    if pair_mask is not None:
+        valid = _f(pair_mask) != 0
+        pair_gate = valid.astype(F64)[..., None]
+        z = z * pair_gate
+        single_valid = np.diagonal(valid, axis1=-2, axis2=-1)
+        single_gate = single_valid.astype(F64)[..., None]
+        extra = np.where(single_valid[..., :, None] & single_valid[..., None, :], 0.0, -1.0e10)
+        if s is not None:
+            s = s * single_gate
+
+    def gate(z):
+        return z if pair_gate is None else z * pair_gate
+
+    z = gate(z + protenix_triangle_multiplication(z, pair_mask, _get(params, "tri_mul_out"), "outgoing"))
+    z = gate(z + protenix_triangle_multiplication(z, pair_mask, _get(params, "tri_mul_in"), "incoming"))
+    heads = _f(_get(_get(_get(params, "tri_att_start"), "linear"), "weight")).shape[0]
+    z = gate(z + protenix_triangle_attention(z, pair_mask, _get(params, "tri_att_start"), num_heads=heads))
+    zt = np.swapaxes(z, -2, -3)
+    mt = None if pair_mask is None else np.swapaxes(_f(pair_mask), -1, -2)
+    zt = zt + protenix_triangle_attention(zt, mt, _get(params, "tri_att_end"), num_heads=heads)
+    z = gate(np.swapaxes(zt, -2, -3))
+    z = gate(z + transition(z, _get(params, "pair_transition")))
+    apb = _get(params, "attention_pair_bias")
+    if apb is not None:
+        if s is None:
+            raise ValueError("PairformerBlock single path requires s")
+        heads_s = _f(_get(_get(apb, "linear_z"), "weight")).shape[0]
+        s = s + protenix_attention_pair_bias(s, z, apb, num_heads=heads_s, extra_attn_bias=extra)
+        if single_gate is not None:
+            s = s * single_gate
+        s = s + transition(s, _get(params, "single_transition"))
+        if single_gate is not None:
+            s = s * single_gate
+    return s, z
+
+
+def openfold3_pair_block(z, params, *, pair_mask, no_heads_pair, inf=1e9, mask_transition=True,
+                         tri_mul_first=True, eps=1e-5):
+    """OpenFold3 ``pair_block`` (``OF3/pair_block.py:106-190``): tri-mul out and
+    in, tri-attn start and end (the ending node a starting module between two
+    transposes, :65-103), ``tri_mul_first`` ordering the two pairs, then the
+    SwiGLU transition multiplied by ``pair_mask`` when ``mask_transition``.
+    Each sublayer is a residual add."""
+    z = _f(z)
+
+    def mul_pair(z):
+        z = z + openfold3_triangle_multiplication(z, _get(params, "tri_mul_out"), outgoing=True, mask=pair_mask,
+                                                  eps=eps)
+        return z + openfold3_triangle_multiplication(z, _get(params, "tri_mul_in"), outgoing=False, mask=pair_mask,
+                                                     eps=eps)
+
+    def att_pair(z):
+        z = z + openfold3_triangle_attention(z, _get(params, "tri_att_start"), no_heads=no_heads_pair,
+                                             mask=pair_mask, inf=inf, eps=eps)
+        zt = np.swapaxes(z, -2, -3)
+        mt = None if pair_mask is None else np.swapaxes(_f(pair_mask), -1, -2)
+        zt = zt + openfold3_triangle_attention(zt, _get(params, "tri_att_end"), no_heads=no_heads_pair, mask=mt,
+                                               inf=inf, eps=eps)
+        return np.swapaxes(zt, -2, -3)
+
+    z = att_pair(mul_pair(z)) if tri_mul_first else mul_pair(att_pair(z))
+    return z + transition(z, _get(params, "pair_transition"), mask=pair_mask if mask_transition else None, eps=eps)
+
+
+def openfold3_pairformer_block(s, z, params, *, single_mask, pair_mask, no_heads_pair, no_heads_pair_bias, inf=1e9,
+                               mask_transition=True, eps=1e-5):
+    """OpenFold3 ``pairformer_block`` (``OF3/pairformer.py:42-102``): z through
+    ``pair_block``; ``s += attention_pair_bias(s, z, mask=single_mask)``;
+    ``s += swiglu_transition(s, mask=single_mask if mask_transition)``.
+    ``params`` has ``pair_stack``, ``attn_pair_bias`` and ``single_transition``
+    (``OF3/pairformer.py:27-33``). Returns ``(s, z)``."""
+    z = openfold3_pair_block(z, _get(params, "pair_stack"), pair_mask=pair_mask, no_heads_pair=no_heads_pair,
+                             inf=inf, mask_transition=mask_transition, eps=eps)
+    s = _f(s) + openfold3_attention_pair_bias(s, z, _get(params, "attn_pair_bias"), no_heads=no_heads_pair_bias,
+                                              mask=single_mask, inf=inf, eps=eps)
+    s = s + transition(s, _get(params, "single_transition"), mask=single_mask if mask_transition else None, eps=eps)
+    return s, z

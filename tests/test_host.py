@@ -172,3 +172,65 @@ def test_kernels_refuse_mismatched_shapes():
     with pytest.raises(ValueError, match="residual must have shape"):
         kernels.single_attention(torch.zeros(1, 8, 384), torch.zeros(1, 8, 8, 128), None, sa,
                                  residual=torch.zeros(1, 7, 384))
+
+
+def test_port_single_attention_and_block_arguments_are_validated():
+    """Selector values, the diffusion-only forms and missing pieces are
+    refused on the host, with the reference's messages where it has them."""
+    z = _z(8)
+    s = torch.zeros(1, 8, 384)
+    w = syn.single_attention_weights(seed=3)
+    px = P.single_attention_to_protenix(w)
+    with pytest.raises(ValueError, match="unsupported attention backend"):
+        protenix.attention_pair_bias(s, None, z, px, num_heads=16, attention_backend="flash")
+    with pytest.raises(ValueError, match="z_is_normalized"):
+        protenix.attention_pair_bias(s, None, z, px, num_heads=16, z_is_normalized=True)
+    with pytest.raises(ValueError, match="trunk form"):
+        P.pack_single_attention_protenix(px._replace(has_s=True), torch.float32, "cpu")
+    with pytest.raises(ValueError, match="gated attention"):
+        P.pack_single_attention_openfold3(P.single_attention_to_openfold3(w)._replace(
+            mha=px.attention._replace(linear_g=None)), torch.float32, "cpu")
+    with pytest.raises(ValueError, match="num_heads=8"):
+        protenix.attention_pair_bias(s, None, z, px, num_heads=8)
+    with pytest.raises(ValueError, match="PairformerStack requires at least one block"):
+        protenix.pairformer_stack(s, z, None, protenix.PairformerStackParams(blocks=()))
+    with pytest.raises(ValueError, match="unsupported triangle attention backend"):
+        protenix.pairformer_block(s, z, None, P.pairformer_block_to_protenix(syn.pairformer_layer_weights()),
+                                  triangle_attention_backend="pallas")
+
+
+def test_single_attention_extra_bias_and_out_mask_shapes():
+    """An extra bias must be 4-D over [N, N] and broadcast to [B, H, N, N];
+    an output mask must broadcast to [B, N]. Both are refused before any
+    launch (here on host tensors, which the device check then refuses)."""
+    w = P.pack_single_attention_boltz2(*P.single_attention_to_boltz2(syn.single_attention_weights(seed=3))[:1],
+                                       torch.float32, "cpu")
+    s = torch.zeros(1, 8, 384)
+    z = _z(8)
+    with pytest.raises(ValueError, match="extra_bias must be a 4-D tensor"):
+        kernels.single_attention(s, z, None, w, extra_bias=torch.zeros(8, 8))
+    with pytest.raises(ValueError, match="does not broadcast"):
+        kernels.single_attention(s, z, None, w, extra_bias=torch.zeros(1, 3, 8, 8))
+    with pytest.raises(ValueError, match="out_mask of shape"):
+        kernels.single_attention(s, z, None, w, out_mask=torch.ones(1, 7))
+
+
+def test_stacked_layers_share_one_buffer_per_weight_kind():
+    from foldjax_amd.pairformer import PairformerLayerWeights
+    from foldjax_amd.stacking import StackedLayers, stackable, stacked_or_stack
+
+    ls = [PairformerLayerWeights.random(torch.float32, "cpu", seed=i) for i in (1, 9)]
+    st = stacked_or_stack(ls)
+    assert stacked_or_stack(st) is st and len(st) == 2 and stackable(ls)
+    buf = st.stacked["triangle"]["tri_mul_out"]["p_in_weight"]
+    assert tuple(buf.shape) == (2, 256, 128)
+    for i, layer in enumerate(st):
+        v = layer.triangle.tri_mul_out.p_in_weight
+        assert torch.equal(v, ls[i].triangle.tri_mul_out.p_in_weight)
+        assert v.data_ptr() == buf[i].data_ptr() and v.is_contiguous()
+    other = PairformerLayerWeights.from_fields(syn.pairformer_layer_weights(heads_single=8), torch.float32, "cpu")
+    assert not stackable([ls[0], other])
+    with pytest.raises(ValueError):
+        StackedLayers([ls[0], other])
+    with pytest.raises(ValueError, match="empty"):
+        stacked_or_stack([])

@@ -21,6 +21,10 @@ import torch
 from foldjax_amd import synthetic as syn
 from oracle import triangle as O
 from tests import _brute as B
+from tests.port_fields import of3_apb_fields as _of3_apb_fields
+from tests.port_fields import of3_block_fields as _of3_block_fields
+from tests.port_fields import px_apb_fields as _px_apb_fields
+from tests.port_fields import px_block_fields as _px_block_fields
 
 
 def _of3_attn(p):
@@ -383,3 +387,135 @@ def test_planted_swapped_position_is_caught():
     # incoming on z^T reads the same a/b lines as outgoing on z, but its gate
     # is z^T[1, 4] = z[4, 1]: the planted swap must differ from z's answer
     assert np.max(np.abs(got[0] - full[1, 4])) > 1e-3
+
+
+# ------------------- Protenix / OpenFold3 single attention and Pairformer blocks
+
+
+def test_gated_attention_matches_torch_sdpa():
+    """The Protenix/OpenFold3 gated attention equals torch SDPA with the bias
+    as an additive mask, gated and projected (``PXP/attention.py:60-99``)."""
+    rng = np.random.default_rng(40)
+    b, n, c, h = 2, 6, 12, 3
+    x = rng.standard_normal((b, n, c))
+    p = syn.single_attention_weights(c, 4, h, seed=40)
+    att = _px_apb_fields(p)["attention"]
+    bias = rng.standard_normal((b, h, n, n))
+    got = O.gated_attention(x, x, att, h, (bias,))
+    T = lambda a: torch.from_numpy(np.asarray(a, dtype=np.float64))  # noqa: E731
+    xt = T(x)
+    lin = lambda name: xt @ T(p[name]["weight"]).T  # noqa: E731
+    q = (lin("proj_q") + T(p["proj_q"]["bias"])).reshape(b, n, h, -1).transpose(1, 2)
+    k = lin("proj_k").reshape(b, n, h, -1).transpose(1, 2)
+    v = lin("proj_v").reshape(b, n, h, -1).transpose(1, 2)
+    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=T(bias)).transpose(1, 2).reshape(b, n, c)
+    want = (torch.sigmoid(lin("proj_g")) * o) @ T(p["proj_o"]["weight"]).T
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_protenix_and_openfold3_attention_pair_bias_equal_boltz2():
+    """With ``LN_a`` = Boltz-2's ``pre_norm_s`` the three ports' attentions with
+    pair bias are one function: Protenix with an extra key bias ``inf (mask - 1)``
+    (ranks [N, N] and [B, N, N] aligned as ``PXP/attention.py:140-150``),
+    OpenFold3 with the key mask, Boltz-2 (pinned to torch SDPA above) on
+    ``LN(s)``."""
+    rng = np.random.default_rng(41)
+    b, n, c_s, c_z, h = 2, 7, 24, 8, 4
+    s = rng.standard_normal((b, n, c_s))
+    z = rng.standard_normal((b, n, n, c_z))
+    mask = (rng.random((b, n)) > 0.3).astype(np.float64)
+    mask[:, 0] = 1.0
+    p = syn.single_attention_weights(c_s, c_z, h, seed=41)
+    s_ln = O.layer_norm(s, p["pre_norm_s"]["weight"], p["pre_norm_s"]["bias"])
+    want = O.boltz2_attention_pair_bias(p, s_ln, z, mask, inf=1e9)
+    of3 = O.openfold3_attention_pair_bias(s, z, _of3_apb_fields(p), no_heads=h, mask=mask, inf=1e9)
+    np.testing.assert_allclose(of3, want, rtol=1e-10, atol=1e-10)
+    extra = np.broadcast_to(((mask - 1.0) * 1e9)[:, None, :], (b, n, n))
+    px = O.protenix_attention_pair_bias(s, z, _px_apb_fields(p), num_heads=h, extra_attn_bias=extra)
+    np.testing.assert_allclose(px, want, rtol=1e-10, atol=1e-10)
+    # a rank-2 extra bias broadcasts over batch and heads
+    one = O.protenix_attention_pair_bias(s[:1], z[:1], _px_apb_fields(p), num_heads=h, extra_attn_bias=extra[0])
+    np.testing.assert_allclose(one, want[:1], rtol=1e-10, atol=1e-10)
+
+
+def test_protenix_block_unmasked_equals_boltz2_layer():
+    """Without padding the Protenix block is the Boltz-2 layer under the field
+    mapping (``PXK/pairformer.py:49-180`` vs ``B2K/pairformer.py:100-206``):
+    same sublayer order, heads from the weight shapes, ``LN_a`` = ``pre_norm_s``."""
+    rng = np.random.default_rng(42)
+    n, c_s, c_z = 5, 16, 8
+    w = syn.pairformer_layer_weights(c_s=c_s, c_z=c_z, heads_pair=2, heads_single=4, seed=42)
+    s = rng.standard_normal((1, n, c_s))
+    z = rng.standard_normal((1, n, n, c_z))
+    want_s, want_z = O.boltz2_pairformer_layer(w, s, z, np.ones((1, n)), np.ones((1, n, n)))
+    for pm in (None, np.ones((1, n, n))):
+        got_s, got_z = O.protenix_pairformer_block(s, z, pm, _px_block_fields(w))
+        np.testing.assert_allclose(got_z, want_z, rtol=1e-10, atol=1e-10)
+        np.testing.assert_allclose(got_s, want_s, rtol=1e-10, atol=1e-10)
+
+
+def test_protenix_block_isolates_adversarial_padded_tokens():
+    """``T/models/protenix/test_pairformer.py:91-132``: padded tokens set to
+    +-1e6 leave the real block unchanged, and the padded region of both tracks
+    is exactly zero (the pair and single gates)."""
+    rng = np.random.default_rng(43)
+    n, pad, c_s, c_z = 3, 2, 16, 8
+    w = syn.pairformer_layer_weights(c_s=c_s, c_z=c_z, heads_pair=2, heads_single=4, seed=43)
+    s = rng.standard_normal((1, n, c_s))
+    z = rng.standard_normal((1, n, n, c_z))
+    want_s, want_z = O.protenix_pairformer_block(s, z, np.ones((1, n, n)), _px_block_fields(w))
+    sp = np.pad(s, ((0, 0), (0, pad), (0, 0)))
+    sp[:, n:] = 1e6
+    zp = np.pad(z, ((0, 0), (0, pad), (0, pad), (0, 0)))
+    zp[:, n:] = -1e6
+    zp[:, :, n:] = 1e6
+    got_s, got_z = O.protenix_pairformer_block(sp, zp, syn.pair_mask(n + pad, n)[None], _px_block_fields(w))
+    np.testing.assert_allclose(got_s[:, :n], want_s, rtol=1e-8, atol=1e-8)
+    np.testing.assert_allclose(got_z[:, :n, :n], want_z, rtol=1e-8, atol=1e-8)
+    assert not np.any(got_s[:, n:]) and not np.any(got_z[:, n:]) and not np.any(got_z[:, :, n:])
+
+
+def test_protenix_block_gate_is_boolean_and_masked_pairs_are_zero():
+    """A pair mask with a hole between two valid tokens and a fractional entry:
+    the hole is zero in z, the fractional entry is gated as True
+    (``pair_valid = bool(pair_mask)``, ``PXK/pairformer.py:74-76``), and the
+    entry values of z at the hole do not matter (z is gated on entry)."""
+    rng = np.random.default_rng(44)
+    n, c_s, c_z = 5, 16, 8
+    w = syn.pairformer_layer_weights(c_s=c_s, c_z=c_z, heads_pair=2, heads_single=4, seed=44)
+    s = rng.standard_normal((1, n, c_s))
+    z = rng.standard_normal((1, n, n, c_z))
+    pm = np.ones((1, n, n))
+    pm[0, 1, 3] = 0.0
+    pm[0, 2, 4] = 0.5
+    got_s, got_z = O.protenix_pairformer_block(s, z, pm, _px_block_fields(w))
+    assert not np.any(got_z[0, 1, 3]) and np.all(np.abs(got_z[0, 2, 4]) > 0)
+    z2 = z.copy()
+    z2[0, 1, 3] = 50.0
+    s2, zz2 = O.protenix_pairformer_block(s, z2, pm, _px_block_fields(w))
+    np.testing.assert_array_equal(zz2, got_z)
+    np.testing.assert_array_equal(s2, got_s)
+
+
+def test_openfold3_block_equals_boltz2_layer_without_transition_masks():
+    """With ``mask_transition=False`` the OpenFold3 block is the Boltz-2 layer
+    (``OF3/pairformer.py:42-102`` vs ``B2K/pairformer.py:100-206``): the key
+    masks differ only in ``inf`` (1e9 vs 1e6), which underflows the same."""
+    rng = np.random.default_rng(45)
+    n, n_real, c_s, c_z = 6, 4, 16, 8
+    w = syn.pairformer_layer_weights(c_s=c_s, c_z=c_z, heads_pair=2, heads_single=4, seed=45)
+    s = rng.standard_normal((1, n, c_s))
+    z = rng.standard_normal((1, n, n, c_z))
+    tm = syn.token_mask(n, n_real)[None]
+    pm = syn.pair_mask(n, n_real)[None]
+    want_s, want_z = O.boltz2_pairformer_layer(w, s, z, tm, pm)
+    got_s, got_z = O.openfold3_pairformer_block(s, z, _of3_block_fields(w), single_mask=tm, pair_mask=pm,
+                                                no_heads_pair=2, no_heads_pair_bias=4, mask_transition=False)
+    np.testing.assert_allclose(got_z, want_z, rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(got_s, want_s, rtol=1e-10, atol=1e-10)
+    # with the transition masks the padded rows of both tracks are zeroed updates
+    ms, mz = O.openfold3_pairformer_block(s, z, _of3_block_fields(w), single_mask=tm, pair_mask=pm,
+                                          no_heads_pair=2, no_heads_pair_bias=4, mask_transition=True)
+    v = slice(0, n_real)
+    np.testing.assert_allclose(mz[:, v, v], want_z[:, v, v], rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(ms[:, v], want_s[:, v], rtol=1e-10, atol=1e-10)
