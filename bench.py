@@ -1,22 +1,25 @@
 """Benchmark of one Pairformer block on one MI355X.
 
-One step = one Boltz-2-form Pairformer layer at N=1024, c_z=128, c_s=384,
-bf16: tri-mul outgoing and incoming, tri-attn starting and ending node
-(4 heads x 32), the pair transition (4x SwiGLU), the single attention with
-pair bias (16 heads) and the single transition, every residual fused. Inputs
-are synthetic (z, s ~ N(0,1), PCG64 seeds 0/1) with a 5% padded tail (973 real
-tokens) and random-init weights (seed 2).
+One step = one Boltz-2-form Pairformer layer at N=1024, c_z=128, c_s=384:
+tri-mul outgoing and incoming, tri-attn starting and ending node (4 heads x
+32), the pair transition (4x SwiGLU), the single attention with pair bias (16
+heads) and the single transition, every residual fused. The pair track runs
+in bf16; the single track in fp32 by default, as the reference runs it
+(``B2K/pairformer.py:182-199``). Inputs are synthetic (z, s ~ N(0,1), PCG64
+seeds 0/1) with a 5% padded tail (973 real tokens) and random-init weights
+(seed 2).
 
 Prints one JSON line. ``value`` times the K steps with no instrumentation;
 the same K steps then run again while the library records HIP events on its
 launch stream around every kernel (``fjx_prof_*``), which gives the
 per-kernel durations, ``ms_per_step_profiled`` and the roofline object (for
-the kernel with the largest total time). The CPU baseline times the float64
-numpy oracle (``oracle/``) on a bounded sample and scales it to the metric's
-unit.
+the kernel with the largest total time). ``other_configs_gpu`` times the
+other baseline configurations the same way (no events); ``cpu_baseline``
+times the float32 numpy restatement (``oracle/``) on a bounded sample of the
+headline workload and on configs 1 and 2.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--n N] [--no-cpu]
-    python bench.py --config trunk|long      (the N=2048 trunk / the N=3072 block)
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--n N] [--no-cpu] [--no-configs]
+    python bench.py --op trimul|triattn|transition|copy   (one sublayer kind, a profiling aid)
 """
 
 from __future__ import annotations
@@ -39,17 +42,18 @@ PEAK_HBM_GBS = 8000.0
 def _args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--steps", type=int, default=30)
+    p.add_argument("--warmup", type=int, default=20,
+                   help="untimed steps first; the GPU clock needs some 100 ms of load to settle")
     p.add_argument("--n", type=int, default=1024)
     p.add_argument("--pad-frac", type=float, default=0.05)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    p.add_argument("--cpu-n", type=int, default=256, help="size of the CPU oracle sample")
+    p.add_argument("--no-configs", action="store_true", help="skip the GPU timings of configs 1, 2, 4 and 5")
+    p.add_argument("--single-dtype", default="fp32", choices=["fp32", "bf16"],
+                   help="the single track's dtype: fp32 as the reference runs it over the bf16 pair track "
+                        "(B2K/pairformer.py:182-199), or bf16")
     p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "copy"],
                    help="profiling aid: run only one sublayer kind per step instead of the whole block")
-    p.add_argument("--config", default="block", choices=["block", "trunk", "long"],
-                   help="block: one layer at N=1024 (the headline line); trunk: the 48-layer trunk at N=2048 "
-                        "with an all-ones mask; long: one unchunked layer at N=3072 with 3012 real tokens")
     return p.parse_args()
 
 
@@ -71,110 +75,208 @@ def measured_traffic(kernel: str, n: int):
     return int(k["hbm_bytes"])
 
 
-def cpu_baseline(n_target: int, n_sample: int, budget_s: float = 25.0) -> dict:
-    """Time the float64 oracle on one Pairformer layer at ``n_sample`` and
-    scale to ``n_target`` by the ratio of algorithmic flops."""
+def _median_time(fn, budget_s: float, max_runs: int = 3) -> tuple[float, int]:
     import numpy as np
-
-    from foldjax_amd import synthetic as syn
-    from foldjax_amd.pairformer import flops_block
-    from oracle import triangle as O
-
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max([int(i.get("num_threads", 1)) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover - informational only
-        threads = len(os.sched_getaffinity(0))
-    n = n_sample
-    n_real = n - int(round(0.05 * n))
-    r = lambda a: syn.bf16_round(a).astype(np.float64)  # noqa: E731
-    z = r(syn.pair_input(n, 128, seed=0, batch=1))
-    s = r(syn.single_input(n, 384, seed=1, batch=1))
-    tm = syn.token_mask(n, n_real)[None].astype(np.float64)
-    pm = syn.pair_mask(n, n_real)[None].astype(np.float64)
-    w = syn.pairformer_layer_weights(seed=2)
 
     times = []
     t_start = time.perf_counter()
     while True:
         t0 = time.perf_counter()
-        O.boltz2_pairformer_layer(w, s, z, tm, pm)
+        fn()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s / 2 or len(times) >= 5:
-            break
-    t = float(np.median(times))
-    scale = sum(flops_block(n_target).values()) / sum(flops_block(n).values())
+        if len(times) >= max_runs or time.perf_counter() - t_start > budget_s:
+            return float(np.median(times)), len(times)
+
+
+def _rows_model(fn, r1: int, r2: int, n: int) -> float:
+    """Time ``fn(rows)`` at r1 and r2 rows and extrapolate the linear model
+    t = shared + rows * per_row (exact: attention rows are independent) to n."""
+    t1, _ = _median_time(lambda: fn(r1), 0.0, 1)
+    t2, _ = _median_time(lambda: fn(r2), 0.0, 1)
+    per_row = max(t2 - t1, 0.0) / (r2 - r1)
+    return t1 + (n - r1) * per_row
+
+
+def _trimul_sample_s(O, z, pm, p, n: int, pos_div: int = 16, ch: int = 16) -> float:
+    """Seconds of one float32 tri-mul (``oracle.protenix_triangle_multiplication``)
+    at size n from two exact samples: its per-position steps (LN_in, the four
+    gated input projections, LN_out, the output projection and gate) on
+    1/pos_div of the positions, and the contraction on ``ch`` of its 128
+    channels; each part scales linearly to the whole."""
+    import numpy as np
+
+    x, m = z[:, : n // pos_div], pm[:, : n // pos_div]
+
+    def per_position():
+        zn = O.layer_norm(x, *O._ln_params(p["layer_norm_in"]))
+        mm = m[..., None]
+        a = mm * O.sigmoid(O.linear_torch(zn, p["linear_a_g"])) * O.linear_torch(zn, p["linear_a_p"])
+        b = mm * O.sigmoid(O.linear_torch(zn, p["linear_b_g"])) * O.linear_torch(zn, p["linear_b_p"])
+        o = O.layer_norm(a + b, *O._ln_params(p["layer_norm_out"]))  # stands in for the contraction output
+        return O.linear_torch(o, p["linear_z"]) * O.sigmoid(O.linear_torch(zn, p["linear_g"]))
+
+    rng = np.random.default_rng(0)
+    a = rng.standard_normal((1, n, n, ch), dtype=np.float32)
+    b = rng.standard_normal((1, n, n, ch), dtype=np.float32)
+    t_pos, _ = _median_time(per_position, 0.0, 1)
+    t_con, _ = _median_time(lambda: O.triangle_contract(a, b, "outgoing"), 0.0, 1)
+    return t_pos * pos_div + t_con * (128 / ch)
+
+
+def cpu_baseline(n: int, n_real: int) -> dict:
+    """The float32 numpy restatement (``oracle/``, the reference's XLA path in
+    fp32) timed on this host's cores at the headline size, on a bounded
+    sample whose work scales exactly to the whole block:
+
+    * tri-mul outgoing at N: its per-position steps on 1/16 of the positions
+      and its contraction on 16 of the 128 channels, each scaled linearly;
+      incoming is the same work transposed and is counted as a second
+      outgoing;
+    * tri-attn starting node at N, on r1 and r2 of the N rows, extrapolated
+      linearly in rows (rows are independent; the LayerNorm and bias of the
+      whole grid are in both samples); the ending node counted as a second
+      starting node;
+    * the pair transition on 1/32 of the positions, times 32;
+    * the single attention with pair bias and the single transition, whole.
+
+    Also times config 1 of the baseline table whole (tri-mul out+in at N=256
+    in fp32) and config 2 (tri-attn start+end at N=384, 346 real tokens) by
+    the same row extrapolation."""
+    import numpy as np
+
+    from foldjax_amd import synthetic as syn
+    from oracle import triangle as O
+
+    cores = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = max([int(i.get("num_threads", 1)) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover - informational only
+        blas = cores
+    w = syn.pairformer_layer_weights(seed=2)
+    z = syn.pair_input(n, 128, seed=0, batch=1)
+    s = syn.single_input(n, 384, seed=1, batch=1)
+    tm = syn.token_mask(n, n_real)[None]
+    pm = syn.pair_mask(n, n_real)[None]
+    r1, r2 = 8, 56
+    parts = {}
+    with O.compute_dtype(np.float32):
+        parts["trimul_out"] = _trimul_sample_s(O, z, pm, w["tri_mul_out"], n)
+        parts["triattn_start"] = _rows_model(
+            lambda r: O.protenix_triangle_attention(z, pm, w["tri_att_start"], num_heads=4, rows=np.arange(r)),
+            r1, r2, n)
+        zs = z[:, : n // 32]
+        parts["transition_z"] = 32 * _median_time(lambda: O.transition(zs, w["transition_z"]), 0.0, 1)[0]
+        a = w["attention"]
+
+        def single():
+            s_ln = O.layer_norm(s, a["pre_norm_s"]["weight"], a["pre_norm_s"]["bias"])
+            s2 = s + O.boltz2_attention_pair_bias(a, s_ln, z, tm)
+            return s2 + O.transition(s2, w["transition_s"])
+
+        parts["single_track"], _ = _median_time(single, 0.0, 1)
+        # configs 1 and 2, whole
+        z1 = syn.pair_input(256, 128, seed=0, batch=1).astype(np.float32)
+        t_c1, _ = _median_time(lambda: [O.protenix_triangle_multiplication(z1, None, w[k], d) for k, d in
+                                        (("tri_mul_out", "outgoing"), ("tri_mul_in", "incoming"))], 0.0, 1)
+        z2 = syn.pair_input(384, 128, seed=0, batch=1)
+        pm2 = syn.pair_mask(384, 346)[None]
+        t_c2 = sum(_rows_model(lambda r, k=k, st=st: O.protenix_triangle_attention(
+            z2, pm2, w[k], num_heads=4, starting=st, rows=np.arange(r)), 16, 48, 384)
+            for k, st in (("tri_att_start", True), ("tri_att_end", False)))
+    total = 2 * parts["trimul_out"] + 2 * parts["triattn_start"] + parts["transition_z"] + parts["single_track"]
     return {
-        "value": t * scale * 1e3,
+        "value": round(total * 1e3, 1),
         "unit": "ms",
-        "cores": threads,
+        "cores": cores,
         "kind": "port",
         "sample": (
-            f"float64 numpy oracle, one Pairformer layer (tri-mul out+in, tri-attn start+end, pair transition, "
-            f"single attention with pair bias, single transition) at N={n} ({n_real} real tokens), median of "
-            f"{len(times)} run(s) = {t * 1e3:.1f} ms, scaled to N={n_target} by the algorithmic-flop ratio {scale:.1f}"
+            f"float32 numpy restatement of the reference's XLA path (oracle/triangle.py) at N={n} ({n_real} real "
+            f"tokens), BLAS on {blas} threads, elementwise numpy on one: tri-mul outgoing from its per-position "
+            f"steps on 1/16 of the positions and its contraction on 16 of 128 channels, each scaled linearly "
+            f"({parts['trimul_out']:.1f} s, counted for both directions); tri-attn starting node on {r1} and {r2} "
+            f"rows extrapolated linearly to {n} ({parts['triattn_start']:.1f} s, counted for both nodes); pair "
+            f"transition on 1/32 of the positions x32 ({parts['transition_z']:.1f} s); single track whole "
+            f"({parts['single_track']:.2f} s)"
         ),
+        "configs": {
+            "config1_trimul_out_in_n256_fp32_ms": round(t_c1 * 1e3, 1),
+            "config2_triattn_start_end_n384_ms": round(t_c2 * 1e3, 1),
+        },
     }
 
 
-def run_config(a) -> int:
-    """The other two BASELINE configurations, reported as their own JSON
-    lines: the 48-layer trunk at N=2048 (all-ones mask, each layer with its
-    own random weights) and one unchunked layer at N=3072 (3012 real tokens)."""
+def _timed(fn, steps: int, warmup: int, dev) -> float:
     import torch
 
-    from foldjax_amd import _lib
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize(dev)
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def other_configs(single_dtype) -> dict:
+    """GPU milliseconds of the other baseline configurations, timed like the
+    headline (no per-kernel events): config 1 (tri-mul out+in, N=256, fp32,
+    all-ones mask), config 2 (tri-attn start+end, N=384, bf16, 346 real
+    tokens), config 4 (the 48-layer trunk at N=2048, all-ones mask, each
+    layer with its own weights) and config 5 (one unchunked layer at N=3072,
+    3012 real tokens)."""
+    import torch
+
+    from foldjax_amd import kernels
     from foldjax_amd import synthetic as syn
     from foldjax_amd.pairformer import PairformerLayerWeights, flops_block
 
     dev = torch.device("cuda:0")
-    dtype = torch.bfloat16
-    if a.config == "trunk":
-        n, n_real, layers = 2048, 2048, 48
-    else:
-        n, n_real, layers = 3072, 3012, 1
-    z0 = torch.from_numpy(syn.pair_input(n, 128, seed=0, batch=1)).to(dev, dtype)
-    s0 = torch.from_numpy(syn.single_input(n, 384, seed=1, batch=1)).to(dev, dtype)
-    tmask = torch.from_numpy(syn.token_mask(n, n_real)[None]).to(dev, dtype)
-    pmask = torch.from_numpy(syn.pair_mask(n, n_real)[None]).to(dev, dtype)
-    stack = [PairformerLayerWeights.random(dtype, dev, seed=2 + l) for l in range(layers)]
+    bf = torch.bfloat16
+    t = lambda a, dt: torch.from_numpy(a).to(dev, dt)  # noqa: E731
+    out = {}
+    layer32 = PairformerLayerWeights.random(torch.float32, dev, seed=2)
+    z1 = t(syn.pair_input(256, 128, seed=0, batch=1), torch.float32)
+    tri = layer32.triangle
+    out["config1_trimul_out_in_n256_fp32_ms"] = round(_timed(lambda: kernels.trimul(
+        kernels.trimul(z1, None, tri.tri_mul_out, "outgoing", residual=z1), None, tri.tri_mul_in, "incoming",
+        residual=z1), 20, 3, dev), 4)
+    del layer32, z1
+    layer = PairformerLayerWeights.random(bf, dev, seed=2, single_dtype=single_dtype)
+    tri = layer.triangle
+    z2 = t(syn.pair_input(384, 128, seed=0, batch=1), bf)
+    m2 = t(syn.pair_mask(384, 346)[None], bf)
+    out["config2_triattn_start_end_n384_bf16_ms"] = round(_timed(lambda: kernels.triattn(
+        kernels.triattn(z2, m2, tri.tri_att_start, starting=True, residual=z2), m2, tri.tri_att_end, starting=False,
+        residual=z2), 20, 3, dev), 4)
+    del z2, m2
+    for key, n, n_real, layers, steps in (("config5_block_n3072_ms", 3072, 3012, 1, 3),
+                                          ("config4_trunk48_n2048_ms", 2048, 2048, 48, 2)):
+        z0 = t(syn.pair_input(n, 128, seed=0, batch=1), bf)
+        s0 = t(syn.single_input(n, 384, seed=1, batch=1), single_dtype)
+        tmask = t(syn.token_mask(n, n_real)[None], single_dtype)
+        pmask = t(syn.pair_mask(n, n_real)[None], bf)
+        stack = [PairformerLayerWeights.random(bf, dev, seed=2 + i, single_dtype=single_dtype)
+                 for i in range(layers)]
 
-    def step():
-        s, z = s0, z0
-        for layer in stack:
-            s, z = layer.forward(s, z, tmask, pmask)
-        return s, z
+        def step():
+            s, z = s0, z0
+            for lay in stack:
+                s, z = lay.forward(s, z, tmask, pmask)
+            return s, z
 
-    steps = max(1, min(a.steps, 3 if layers > 1 else a.steps))
-    for _ in range(max(1, min(a.warmup, 1))):
-        step()
-    torch.cuda.synchronize(dev)
-    _lib.prof_reset()
-    _lib.prof_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(steps):
+        ms = _timed(step, steps, 1, dev)
         s, z = step()
-    torch.cuda.synchronize(dev)
-    elapsed = time.perf_counter() - t0
-    _lib.prof_enable(False)
-    stats = _lib.prof_read()
-    if not (torch.isfinite(z.float()).all() and torch.isfinite(s.float()).all()):
-        print("non-finite output", file=sys.stderr)
-        return 1
-    ms = elapsed * 1e3 / steps
-    per = {k: {"avg_ms": round(v[0] / v[1], 4), "launches": v[1]} for k, v in stats.items() if v[1]}
-    fl = sum(flops_block(n).values()) * layers
-    what = "48-layer Pairformer trunk" if layers > 1 else "one Pairformer block, unchunked in HBM"
-    print(json.dumps({
-        "metric": f"ms per {what} @N={n} c_z=128 bf16",
-        "value": round(ms, 3), "unit": "ms", "n_gpus": 1, "steps": steps, "higher_is_better": False,
-        "ms_per_block": round(ms / layers, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1), "dtype": "bf16",
-        "data": "synthetic: z, s ~ N(0,1), random-init weights per layer",
-        "config": {"workload": what, "n": n, "n_real": n_real, "layers": layers, "c_z": 128, "c_s": 384},
-        "kernels": per,
-    }))
-    return 0
+        torch.cuda.synchronize(dev)
+        if not (torch.isfinite(z.float()).all() and torch.isfinite(s.float()).all()):
+            raise RuntimeError(f"non-finite output in {key}")
+        out[key] = round(ms, 3)
+        out[key.replace("_ms", "_tflops")] = round(sum(flops_block(n).values()) * layers / (ms * 1e-3) / 1e12, 1)
+        del z0, s0, stack
+        torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -186,9 +288,6 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
-    if a.config != "block":
-        return run_config(a)
-
     import torch
 
     from foldjax_amd import _lib
@@ -197,13 +296,14 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
+    sdt = torch.float32 if a.single_dtype == "fp32" else torch.bfloat16
     n = a.n
     n_real = n - int(round(a.pad_frac * n))
     z0 = torch.from_numpy(syn.pair_input(n, 128, seed=0, batch=1)).to(dev, dtype)
-    s0 = torch.from_numpy(syn.single_input(n, 384, seed=1, batch=1)).to(dev, dtype)
-    tmask = torch.from_numpy(syn.token_mask(n, n_real)[None]).to(dev, dtype)
+    s0 = torch.from_numpy(syn.single_input(n, 384, seed=1, batch=1)).to(dev, sdt)
+    tmask = torch.from_numpy(syn.token_mask(n, n_real)[None]).to(dev, sdt)
     pmask = torch.from_numpy(syn.pair_mask(n, n_real)[None]).to(dev, dtype)
-    layer = PairformerLayerWeights.random(dtype, dev, seed=2)
+    layer = PairformerLayerWeights.random(dtype, dev, seed=2, single_dtype=sdt)
 
     from foldjax_amd import kernels
 
@@ -213,9 +313,10 @@ def main() -> int:
         "trimul": lambda: (s0, kernels.trimul(z0, pmask, tri.tri_mul_out, "outgoing", residual=z0)),
         "triattn": lambda: (s0, kernels.triattn(z0, pmask, tri.tri_att_start, starting=True, residual=z0)),
         "transition": lambda: (s0, kernels.transition(z0, layer.transition_z, residual=z0)),
-        # a plain device copy of the pair tensor (N*N*128*2 bytes each way): the
-        # calibration point for the FETCH_SIZE / WRITE_SIZE counters
-        "copy": lambda: (s0, z0.clone()),
+        # one elementwise pass over the pair tensor (N*N*128*2 bytes read and
+        # written by torch's neg kernel): the calibration point for the
+        # FETCH_SIZE / WRITE_SIZE counters
+        "copy": lambda: (s0, torch.neg(z0)),
     }
     step = steps_fn[a.op]
     for _ in range(a.warmup):
@@ -286,9 +387,10 @@ def main() -> int:
         roof = {"bound": "hbm", "achieved": None, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": None,
                 "traffic": traffic, "kernel": dominant}
 
+    configs = None if a.no_configs else other_configs(sdt)
     cpu = None
     if not a.no_cpu:
-        cpu = cpu_baseline(n, a.cpu_n)
+        cpu = cpu_baseline(n, n_real)
 
     out = {
         "metric": METRIC,
@@ -308,11 +410,12 @@ def main() -> int:
             "workload": "one Pairformer block (Boltz-2 layer): tri-mul out+in, tri-attn start+end, pair transition "
                         "4x SwiGLU, single attention with pair bias, single transition; residuals fused",
             "n": n, "n_real": n_real, "c_z": 128, "c_hidden": 128, "c_s": 384, "tri_heads": 4, "tri_head_dim": 32,
-            "single_heads": 16,
+            "single_heads": 16, "pair_dtype": "bf16", "single_dtype": a.single_dtype,
         },
         "block_tflops": round(block_tflops, 1),
         "roofline": roof,
         "cpu_baseline": cpu,
+        "other_configs_gpu": configs,
         "mfma_frac": {"primary": round(primary, 4), "secondary": round(secondary, 4)},
         "kernels": kern,
     }

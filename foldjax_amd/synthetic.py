@@ -20,11 +20,18 @@ import numpy as np
 def bf16_round(x: np.ndarray) -> np.ndarray:
     """Round float32 values to the nearest bfloat16 (ties to even), as float32."""
     x = np.ascontiguousarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    rounded = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
-    out = rounded.astype(np.uint32).view(np.float32)
-    # NaN stays NaN (not produced by these generators, kept for safety)
-    return np.where(np.isnan(x), x, out)
+    u = x.view(np.uint32)
+    # no finite value overflows 32 bits here (the largest, 0xFF7FFFFF, gains
+    # at most 0x8000); NaN patterns may, and are restored below
+    r = (u >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = x[nan]
+    return out
 
 
 def _glorot(rng, out_f: int, in_f: int) -> np.ndarray:

@@ -24,9 +24,24 @@ transposed starting, row-chunk invariance, padding isolation).
 
 from __future__ import annotations
 
+import contextlib
+
 import numpy as np
 
 F64 = np.float64
+_DT = [F64]  # the element type every function converts its inputs to
+
+
+@contextlib.contextmanager
+def compute_dtype(dtype):
+    """Run the restatements in ``dtype`` instead of float64 (the CPU baseline
+    times them in float32, the reference's fp32 arithmetic). Parity checks
+    always use the float64 default."""
+    _DT.append(np.dtype(dtype).type)
+    try:
+        yield
+    finally:
+        _DT.pop()
 
 
 def _get(obj, name):
@@ -37,7 +52,7 @@ def _get(obj, name):
 
 
 def _f(x):
-    return None if x is None else np.asarray(x, dtype=F64)
+    return None if x is None else np.asarray(x, dtype=_DT[-1])
 
 
 # ---------------------------------------------------------------------------
@@ -224,7 +239,7 @@ def attention_rows(q, k, v, mask_bias, tri_bias, row_block=16):
     q, k, v = _f(q), _f(k), _f(v)
     mask_bias, tri_bias = _f(mask_bias), _f(tri_bias)
     n_rows = q.shape[-4]
-    out = np.empty(q.shape[:-1] + (v.shape[-1],))
+    out = np.empty(q.shape[:-1] + (v.shape[-1],), dtype=_DT[-1])
     for s in range(0, n_rows, row_block):
         e = min(n_rows, s + row_block)
         qs, ks, vs = q[..., s:e, :, :, :], k[..., s:e, :, :, :], v[..., s:e, :, :, :]
@@ -285,12 +300,18 @@ def boltz2_triangle_attention(params, x, mask=None, starting=True, inf=1e9, eps=
     return out
 
 
-def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, inf=1e9):
+def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, inf=1e9, rows=None):
     """Protenix ``triangle_attention`` dense path.
 
     ``PXT/triangle.py:509-535`` and ``_triangle_attention_dense`` :732-847:
     same math as Boltz-2 with torch-layout weights, ``scale = D**-0.5``
     multiplied into q (:792), and an optional ``linear_g``.
+
+    ``rows``: compute only these rows of the attention grid (rows i of x for
+    the starting node, columns for the ending node) and return them as
+    ``[..., len(rows), N, C]`` in that grid (not swapped back); the
+    reference's row blocking shows rows are independent
+    (``PXT/triangle.py:850-860``). The bias still comes from the whole grid.
     """
     x = _f(x)
     if mask is None:
@@ -303,6 +324,10 @@ def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, in
     mask_bias = (inf * (mask - 1.0))[..., :, None, None, :]
     tri_bias = linear_torch(x, _get(params, "linear"))
     tri_bias = np.moveaxis(tri_bias, -1, -3)[..., None, :, :, :]
+    if rows is not None:
+        rows = np.asarray(rows)
+        x = x[..., rows, :, :]
+        mask_bias = mask_bias[..., rows, :, :, :]
     att = _get(params, "attention")
     d = _f(_get(_get(att, "linear_k"), "weight")).shape[0] // num_heads
     q = _split_heads_torch(x, _get(att, "linear_q"), num_heads) * (float(d) ** -0.5)
@@ -313,7 +338,7 @@ def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, in
         o = o * sigmoid(linear_torch(x, _get(att, "linear_g"))).reshape(o.shape)
     o = o.reshape(o.shape[:-2] + (-1,))
     out = linear_torch(o, _get(att, "linear_o"))
-    if not starting:
+    if not starting and rows is None:
         out = np.swapaxes(out, -2, -3)
     return out
 

@@ -519,3 +519,23 @@ def test_openfold3_block_equals_boltz2_layer_without_transition_masks():
     v = slice(0, n_real)
     np.testing.assert_allclose(mz[:, v, v], want_z[:, v, v], rtol=1e-10, atol=1e-10)
     np.testing.assert_allclose(ms[:, v], want_s[:, v], rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_triattn_row_subset_equals_full_rows(starting):
+    """``rows=`` gives exactly those rows of the attention grid (the CPU
+    baseline times a row sample), and float32 mode stays close to float64."""
+    rng = np.random.default_rng(50)
+    n, c = 11, 8
+    z = rng.standard_normal((n, n, c))
+    mask = (rng.random((n, n)) > 0.2).astype(np.float64)
+    w = syn.triattn_weights(c, 2, 4, seed=50)
+    full = O.protenix_triangle_attention(z, mask, w, num_heads=2, starting=starting)
+    grid = full if starting else np.swapaxes(full, 0, 1)
+    rows = [0, 4, 10]
+    got = O.protenix_triangle_attention(z, mask, w, num_heads=2, starting=starting, rows=rows)
+    np.testing.assert_allclose(got, grid[rows], rtol=1e-12, atol=1e-12)
+    with O.compute_dtype(np.float32):
+        f32 = O.protenix_triangle_attention(z, mask, w, num_heads=2, starting=starting, rows=rows)
+    assert f32.dtype == np.float32
+    np.testing.assert_allclose(f32, grid[rows], rtol=1e-4, atol=1e-4)
