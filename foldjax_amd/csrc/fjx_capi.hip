@@ -734,21 +734,27 @@ int single_run(const fjx_single_attention_args* a, hipStream_t st) {
     if (a->pre_norm_weight)
       launch_layernorm_rows<T>(s_in, static_cast<const T*>(a->pre_norm_weight),
                                static_cast<const T*>(a->pre_norm_bias), s_ln, B * n, (int)cs, a->eps, st);
-    const void* ws_[4] = {a->q_weight, a->k_weight, a->v_weight, a->g_weight};
-    for (int j = 0; j < 4; ++j) {
+    const T* ws_[4] = {static_cast<const T*>(a->q_weight), static_cast<const T*>(a->k_weight),
+                       static_cast<const T*>(a->v_weight), static_cast<const T*>(a->g_weight)};
+    // weights stored back to back ([4 c_s, c_s], as the package packs them)
+    // run as one GEMM of four times the width: four times the tiles in flight
+    const bool stacked = ws_[1] == ws_[0] + cs * cs && ws_[2] == ws_[1] + cs * cs && ws_[3] == ws_[2] + cs * cs;
+    for (int j = 0; j < (stacked ? 1 : 4); ++j) {
       GemmParams<T, T> g = {};
       g.a = a->pre_norm_weight ? s_ln : s_in;
-      g.b = static_cast<const T*>(ws_[j]);
+      g.b = ws_[j];
       g.c = qkvg + j * cs;
       g.m = B * n;
-      g.n = cs;
+      g.n = stacked ? 4 * cs : cs;
       g.k = cs;
       g.lda = cs;
       g.ldb = cs;
       g.ldc = 4 * cs;
       g.batches = 1;
       g.bias = j == 0 ? static_cast<const T*>(a->q_bias) : nullptr;
-      g.act = j == 3 ? 1 : 0;
+      g.bias_n = cs;
+      g.act = stacked || j == 3 ? 1 : 0;
+      g.act_col0 = stacked ? 3 * cs : 0;  // the gate's columns
       launch_gemm<T, T>(g, st);
     }
     launch_split_heads<T>(qkvg, 4 * cs, B, n, np, (int)H, dh, (1.0f / sqrtf((float)dh)) * kLog2e,

@@ -148,14 +148,15 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
     for (int j = 0; j < WT; ++j) {
       const int64_t col = n0 + wn + 16 * j + li;
       if (col >= N) continue;
-      const float bias = P.bias ? to_f32(P.bias[col]) : 0.f;
+      const float bias = P.bias && (P.bias_n == 0 || col < P.bias_n) ? to_f32(P.bias[col]) : 0.f;
+      const int act = col >= P.act_col0 ? P.act : 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int64_t row = m0 + wm + 16 * i + 4 * lg + q;
         if (row >= M) continue;
         float v = acc[i][j][q] + bias;
-        if (P.act == 1) v = fast_sigmoid(v);
-        else if (P.act == 2) v *= fast_sigmoid(v);  // silu
+        if (act == 1) v = fast_sigmoid(v);
+        else if (act == 2) v *= fast_sigmoid(v);  // silu
         const int64_t off = row * P.ldc + col;
         if (G) v *= to_f32(G[off]);
         if (R) v += to_f32(R[off]);

@@ -415,30 +415,22 @@ void flash_tri_fast_kernel_bf16(FlashParams<bf16> P) {
 __global__ __launch_bounds__(64 * kRows) void flash_tri_kernel_f32(FlashParams<float> P) {
   flash_tri_body<float, kRows, 4>(P);
 }
-// the same body for the single-track attention (rows == 1), under its own
-// name so that per-kernel profiles keep the two workloads apart
-__global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
-void flash_single_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows, 4>(P);
-}
-__global__ __launch_bounds__(64 * kRows) void flash_single_kernel_f32(FlashParams<float> P) {
-  flash_tri_body<float, kRows, 4>(P);
-}
 
 template <typename T>
 void launch_flash(const FlashParams<T>& p_in, int64_t batch, hipStream_t st) {
   const int64_t rg = (p_in.rows + kRows - 1) / kRows;
   const dim3 grid((unsigned)(batch * p_in.heads * rg * (p_in.np / kQT)));
-  const bool single = p_in.rows == 1;
+  // one row (the single-track attention, a bias per head): the keys are split
+  // over the waves of a workgroup instead (fjx_single_flash.hip)
+  if (p_in.rows == 1) {
+    launch_flash_single<T>(p_in, batch, st);
+    return;
+  }
   // the offset kernels skip unflagged workgroups whenever `fallback` is set,
   // so it stays set only where an offset-free pass fills the flags first
   FlashParams<T> plain = p_in;
   plain.fallback = nullptr;
   if constexpr (std::is_same<T, bf16>::value) {
-    if (single) {
-      hipLaunchKernelGGL(flash_single_kernel_bf16, grid, dim3(64 * kRows), 0, st, plain);
-      return;
-    }
     const FlashParams<T>& p = p_in;
     const bool q128 = p.np % 128 == 0;
     const dim3 g = q128 ? dim3((unsigned)(batch * p.heads * rg * (p.np / 128))) : grid;
@@ -454,7 +446,7 @@ void launch_flash(const FlashParams<T>& p_in, int64_t batch, hipStream_t st) {
     }
     hipLaunchKernelGGL(q128 ? flash_tri8_kernel_bf16 : flash_tri_kernel_bf16, g, dim3(64 * kRows), 0, st, p);
   } else
-    hipLaunchKernelGGL(single ? flash_single_kernel_f32 : flash_tri_kernel_f32, grid, dim3(64 * kRows), 0, st, plain);
+    hipLaunchKernelGGL(flash_tri_kernel_f32, grid, dim3(64 * kRows), 0, st, plain);
 }
 
 template void launch_flash<bf16>(const FlashParams<bf16>&, int64_t, hipStream_t);

@@ -89,7 +89,9 @@ struct GemmParams {
   int64_t sa, sb, sc;  // batch strides in elements (0 = shared)
   int64_t batches;
   const T* bias;       // [n] or null
+  int64_t bias_n;      // the bias covers columns < bias_n (0: all n)
   int act;             // 0 none, 1 sigmoid, 2 silu
+  int64_t act_col0;    // the activation applies to columns >= act_col0
   const TO* gate;      // indexed like c, or null
   const TO* residual;  // indexed like c, or null (may alias c)
   const TO* row_gate;  // [m] per output row, or null: rows where it is 0 are written as 0 (after the residual)
@@ -186,6 +188,10 @@ void launch_gate_unpad(const T* o, const T* g, int64_t ldg, T* out, int64_t rows
                        hipStream_t st);
 template <typename T>
 void launch_flash(const FlashParams<T>& p, int64_t batch, hipStream_t st);
+// rows == 1, a bias per head: keys split over the waves of a workgroup
+// (fjx_single_flash.hip); launch_flash routes such calls here
+template <typename T>
+void launch_flash_single(const FlashParams<T>& p, int64_t batch, hipStream_t st);
 // the pipelined offset-free pass (fjx_flash_pipe.hip); false when the shape
 // or the parameters do not suit it (then nothing is launched)
 bool launch_flash_pipe(const FlashParams<bf16>& p, int64_t batch, hipStream_t st);

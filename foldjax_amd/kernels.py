@@ -178,7 +178,15 @@ class SingleAttentionWeights:
         return int(self.z_weight.shape[0])
 
     def to(self, dtype: torch.dtype, device) -> "SingleAttentionWeights":
-        return SingleAttentionWeights(**{f.name: _prep(getattr(self, f.name), dtype, device) for f in fields(self)})
+        """Each weight in ``dtype`` on ``device``; q, k, v and g are stored back
+        to back in one ``[4 c_s, c_s]`` buffer (the library then runs their four
+        projections as one GEMM)."""
+        f = {fl.name: _prep(getattr(self, fl.name), dtype, device) for fl in fields(self)}
+        parts = [f[k] for k in ("q_weight", "k_weight", "v_weight", "g_weight")]
+        if len({tuple(t.shape) for t in parts}) == 1:
+            qkvg = torch.cat(parts, 0)
+            f["q_weight"], f["k_weight"], f["v_weight"], f["g_weight"] = qkvg.chunk(4, 0)
+        return SingleAttentionWeights(**f)
 
     def check(self, c_s: int, c_z: int | None) -> None:
         """Shapes against the single width ``c_s`` and (when z is read) the
