@@ -25,7 +25,7 @@ FJX_ERR_UNSUPPORTED = 2
 FJX_ERR_WORKSPACE = 3
 FJX_ERR_HIP = 4
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 NOALLOC_SCRATCH_BYTES = 256 << 20
 
 _vp = ctypes.c_void_p
@@ -81,7 +81,7 @@ class TransitionArgs(ctypes.Structure):
         ("hidden", _i64), ("workspace", _vp), ("workspace_bytes", _sz),
         ("pb_n", _i64), ("pb_heads", _i64), ("pb_eps", _f32),
         ("pb_norm_weight", _vp), ("pb_norm_bias", _vp), ("pb_weight", _vp), ("pb_out", _vp),
-        ("out_mask", _vp),
+        ("out_mask", _vp), ("pb_f32", _i32),
     ]
 
 

@@ -420,19 +420,30 @@ int transition_run(const fjx_transition_args* a, bool pb_fused, hipStream_t st) 
   p.out = static_cast<T*>(a->out);
   p.rows = a->rows;
   p.eps = a->eps;
+  const bool pb_f32 = pb_fused && a->pb_f32 && std::is_same<T, bf16>::value;
   if (pb_fused) {
-    p.pb_ln_w = static_cast<const T*>(a->pb_norm_weight);
-    p.pb_ln_b = static_cast<const T*>(a->pb_norm_bias);
-    p.pb_w = static_cast<const T*>(a->pb_weight);
-    p.pb_out = static_cast<T*>(a->pb_out);
+    if (pb_f32) {
+      p.pbf_ln_w = static_cast<const float*>(a->pb_norm_weight);
+      p.pbf_ln_b = static_cast<const float*>(a->pb_norm_bias);
+      p.pbf_w = static_cast<const float*>(a->pb_weight);
+      p.pbf_out = static_cast<float*>(a->pb_out);
+    } else {
+      p.pb_ln_w = static_cast<const T*>(a->pb_norm_weight);
+      p.pb_ln_b = static_cast<const T*>(a->pb_norm_bias);
+      p.pb_w = static_cast<const T*>(a->pb_weight);
+      p.pb_out = static_cast<T*>(a->pb_out);
+    }
     p.pb_n = a->pb_n;
     p.pb_np = round64(a->pb_n);
     p.pb_heads = (int)a->pb_heads;
     p.pb_eps = a->pb_eps;
   }
   return timed(K_TRANSITION, st, "transition", [&] {
-    if (pb_fused)
-      launch_pair_bias_border<T>(p.pb_out, a->rows / (a->pb_n * a->pb_n) * a->pb_heads, a->pb_n, p.pb_np, st);
+    const int64_t planes = pb_fused ? a->rows / (a->pb_n * a->pb_n) * a->pb_heads : 0;
+    if (pb_f32)
+      launch_pair_bias_border<float>(p.pbf_out, planes, a->pb_n, p.pb_np, st);
+    else if (pb_fused)
+      launch_pair_bias_border<T>(p.pb_out, planes, a->pb_n, p.pb_np, st);
     launch_transition<T>(p, (int)a->c, st);
   });
 }
@@ -442,6 +453,13 @@ int transition_run(const fjx_transition_args* a, bool pb_fused, hipStream_t st) 
 template <typename T>
 int transition_pair_bias_pass(const fjx_transition_args* a, hipStream_t st) {
   const int64_t batch = a->rows / (a->pb_n * a->pb_n);
+  if (a->pb_f32 && std::is_same<T, bf16>::value)
+    return timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
+      launch_pair_bias<bf16, float>(static_cast<const bf16*>(a->out), static_cast<const float*>(a->pb_norm_weight),
+                                    static_cast<const float*>(a->pb_norm_bias), static_cast<const float*>(a->pb_weight),
+                                    static_cast<float*>(a->pb_out), batch, a->pb_n, round64(a->pb_n),
+                                    (int)a->pb_heads, a->pb_eps, st);
+    });
   return timed(K_SINGLE_PAIR_BIAS, st, "single_pair_bias", [&] {
     launch_pair_bias<T, T>(static_cast<const T*>(a->out), static_cast<const T*>(a->pb_norm_weight),
                         static_cast<const T*>(a->pb_norm_bias), static_cast<const T*>(a->pb_weight),
@@ -974,6 +992,9 @@ int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
       return fail(FJX_ERR_UNSUPPORTED, "fjx_transition_fwd: the pair-bias batch is too large");
     if (!a->pb_norm_weight || !a->pb_norm_bias || !a->pb_weight)
       return fail(FJX_ERR_INVALID, "fjx_transition_fwd: a pair-bias weight pointer is NULL");
+    if (a->pb_f32 && a->dtype != FJX_DTYPE_BF16)
+      return fail(FJX_ERR_INVALID, "fjx_transition_fwd: pb_f32 is for a bf16 transition (an fp32 one has fp32 pair-bias "
+                                   "weights already)");
     if (!aligned16({a->pb_norm_weight, a->pb_norm_bias, a->pb_weight, a->pb_out}))
       return fail(FJX_ERR_INVALID, "fjx_transition_fwd: tensors must be 16-byte aligned");
   }

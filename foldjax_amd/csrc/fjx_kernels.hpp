@@ -123,6 +123,12 @@ struct TransitionParams {
   int64_t pb_np;
   int pb_heads;
   float pb_eps;
+  // the same epilogue with the norm, weight and bias in fp32 over a bf16
+  // transition (the Boltz-2 single track's precision); pbf_out null: off
+  const float* pbf_ln_w;
+  const float* pbf_ln_b;
+  const float* pbf_w;  // [pb_heads][C]
+  float* pbf_out;
 };
 
 template <typename T>

@@ -60,9 +60,9 @@ __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restric
 }
 
 // LayerNorm of 128 channels held by 4 consecutive threads (the chunks of
-// load_row_part), written to the same channels of dst_row as TO
-template <typename T, typename TO>
-__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row) {
+// load_row_part); put(c, o) receives the 8 outputs of channels c .. c+7
+template <typename T, typename Put>
+__device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine& l, float eps, Put put) {
   float v[32];
 #pragma unroll
   for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
@@ -98,8 +98,14 @@ __device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, 
       o[e] = fmaf(fmaf(v[8 * q + e], rstd, shift), w0[e], b0[e]);
       o[4 + e] = fmaf(fmaf(v[8 * q + 4 + e], rstd, shift), w1[e], b1[e]);
     }
-    store8(dst_row + c, pack8<TO>(o));
+    put(c, o);
   }
+}
+
+// ... written to the same channels of dst_row as TO
+template <typename T, typename TO>
+__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row) {
+  ln_quad_put(r, l, eps, [&](int c, const float* o) { store8(dst_row + c, pack8<TO>(o)); });
 }
 
 // One wave's 32 output channels col0..col0+31 of a [128][128] weight as MFMA

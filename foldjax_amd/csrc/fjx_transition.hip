@@ -70,6 +70,95 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P,
   }
 }
 
+// The same projection in fp32 for a bf16 transition (the attention runs in
+// fp32 over the bf16 pair tensor): the LayerNormed rows and the fp32 weight
+// are split into bf16 high and low parts, hi = bf16(v), lo = bf16(v - hi),
+// and the product is taken as hi.hi + hi.lo + lo.hi on the bf16 MFMA (the
+// dropped lo.lo term is below 2^-16 of the product). The high parts go to
+// xs, the low parts to hs (free after the last chunk).
+__device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf16>& P, bf16 (*xs)[tile::kLd],
+                                                       bf16 (*hs)[tile::kLd], const tile::LnAffine& ln, int64_t m0,
+                                                       int nvalid) {
+  using namespace tile;
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int p = t >> 2;
+  // the weight rows of head l % 16 (zero past pb_heads), split hi + lo
+  WCol<bf16> whi, wlo;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    float w[8], hi[8], lo[8];
+    if (li < P.pb_heads) {
+      const float* src = P.pbf_w + (int64_t)li * kC + 32 * ks + 8 * lg;
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(src);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        w[e] = w0[e];
+        w[4 + e] = w1[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) w[e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      hi[e] = round_to<bf16>(w[e]);
+      lo[e] = w[e] - hi[e];
+    }
+    whi[ks] = pack8<bf16>(hi);
+    wlo[ks] = pack8<bf16>(lo);
+  }
+  __syncthreads();
+  {
+    RowPart<bf16> yr;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) yr.f[q] = load8(&xs[p][row_chunk(q)]);
+    ln_quad_put(yr, ln, P.pb_eps, [&](int c, const float* o) {  // each thread rewrites only the chunks it read
+      float hi[8], lo[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hi[e] = round_to<bf16>(o[e]);
+        lo[e] = o[e] - hi[e];
+      }
+      store8(&xs[p][c], pack8<bf16>(hi));
+      store8(&hs[p][c], pack8<bf16>(lo));
+    });
+  }
+  __syncthreads();
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const bf16x8 xh = load8(&xs[16 * wave + li][32 * ks + 8 * lg]);
+    const bf16x8 xl = load8(&hs[16 * wave + li][32 * ks + 8 * lg]);
+    mma(acc, xh, whi[ks]);
+    mma(acc, xh, wlo[ks]);
+    mma(acc, xl, whi[ks]);
+  }
+  const int pos0 = 16 * wave + 4 * lg;
+  if (li >= P.pb_heads || pos0 >= nvalid) return;
+  const int64_t n = P.pb_n, nn = n * n, np = P.pb_np;
+  float v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = acc[q] * kLog2e;
+  if ((n & 3) == 0) {
+    const int64_t m = m0 + pos0;
+    const int64_t b = m / nn, rem = m - b * nn, r = rem / n, c = rem - r * n;
+    store4f(P.pbf_out + ((b * P.pb_heads + li) * np + r) * np + c, v);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (pos0 + q >= nvalid) break;
+      const int64_t m = m0 + pos0 + q;
+      const int64_t b = m / nn, rem = m - b * nn, r = rem / n, c = rem - r * n;
+      P.pbf_out[((b * P.pb_heads + li) * np + r) * np + c] = v[q];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Pair-track transition (C = 128, hidden 512): 128-row tiles, 512 threads.
 // Wave w owns hidden columns 16w .. 16w+15 of every 128-wide hidden chunk and
@@ -79,8 +168,10 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P,
 // products use the transposed accumulator form (a lane holds 4 consecutive
 // columns of one row), so silu(a)*b and the output go out 8 bytes per lane.
 // ---------------------------------------------------------------------------
-template <typename T>
-__global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> P) {
+// kPbF32: the fp32 pair-bias epilogue of a bf16 transition (a kernel of its
+// own, so the other paths compile exactly as without it)
+template <typename T, bool kPbF32>
+__device__ __forceinline__ void transition128_body(const TransitionParams<T>& P) {
   using namespace tile;
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];  // LN(x)
   __shared__ __attribute__((aligned(16))) T hs[kTP][kLd];  // silu(a) * b, one hidden chunk
@@ -100,6 +191,7 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
     load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
     stage_ln<T>(P.ln_w, P.ln_b, ln);
     if (P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
+    if constexpr (kPbF32) stage_ln<float>(P.pbf_ln_w, P.pbf_ln_b, pb_ln);
     __syncthreads();
     ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
   }
@@ -134,14 +226,13 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
   // the pair-bias weight (rows = heads, zero past pb_heads) is fetched ahead
   // of the output stores so that its latency is not exposed after them
   WCol<T> pb_wf;
-  if (P.pb_out) {
+  if (!kPbF32 && P.pb_out) {
     const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int h = lane & 15;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       pb_wf[ks] = h < P.pb_heads ? load8(P.pb_w + (int64_t)h * kC + 32 * ks + 8 * (lane >> 4)) : pack8<T>(zero);
   }
-
   // every row tile's row mask and residual are loaded before the first
   // store: a store counts against the same memory counter a load's use
   // waits on, so loads between stores would each wait for the stores
@@ -191,10 +282,25 @@ __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> 
 #pragma unroll
       for (int q = 0; q < 4; ++q) y[q] *= gate[rt];
       store4f(P.out + off, y);
-      if (P.pb_out) store4f(&xs[row][col + 4 * (lane >> 4)], y);  // xs is free after the last chunk
+      if (kPbF32 || P.pb_out) store4f(&xs[row][col + 4 * (lane >> 4)], y);  // xs is free after the last chunk
     }
   }
-  if (P.pb_out) pair_bias_epilogue<T>(P, xs, pb_ln, pb_wf, m0, nvalid);
+  if constexpr (kPbF32) {
+    pair_bias_epilogue_f32(P, xs, hs, pb_ln, m0, nvalid);
+  } else {
+    if (P.pb_out) pair_bias_epilogue<T>(P, xs, pb_ln, pb_wf, m0, nvalid);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> P) {
+  transition128_body<T, false>(P);
+}
+// two 512-thread workgroups (70 KB of LDS each) share a CU only at 4 waves
+// per SIMD, so this variant is held to 128 VGPRs as the plain one fits
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void transition128_pbf32_kernel(TransitionParams<bf16> P) {
+  transition128_body<bf16, true>(P);
 }
 
 // C = 128 only; other widths take the general path of the C ABI layer (row
@@ -204,6 +310,12 @@ template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st) {
   (void)c;
   const dim3 grid((unsigned)((p.rows + tile::kTP - 1) / tile::kTP));
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (p.pbf_out) {
+      hipLaunchKernelGGL(transition128_pbf32_kernel, grid, dim3(512), 0, st, p);
+      return;
+    }
+  }
   hipLaunchKernelGGL(transition128_kernel<T>, grid, dim3(512), 0, st, p);
 }
 

@@ -222,7 +222,9 @@ def transition(
     library's ``[B, H, Np, Np]`` layout, for ``single_attention(...,
     pair_bias=...)``; with 128 channels, a 4x hidden width and at most 16
     heads it is computed in the transition's epilogue, so the pair tensor is
-    not read again."""
+    not read again. The bias takes the attention's dtype: a float32
+    attention over a bfloat16 pair track gets a float32 bias computed to
+    float32 accuracy."""
     c = int(x.shape[-1])
     w.check(c)
     _same_device(x, row_mask=row_mask, residual=residual, out_mask=out_mask)
@@ -240,12 +242,17 @@ def transition(
     out = torch.empty_like(xf)
     pb = None
     pb_n = pb_heads = 0
+    pb_f32 = False
     if pair_bias_for is not None:
         if x.dim() < 3 or x.shape[-3] != x.shape[-2]:
             raise ValueError(f"a pair-bias output needs a pair tensor [..., N, N, C], got {tuple(x.shape)}")
+        pb_dtype = pair_bias_for.z_weight.dtype
+        pb_f32 = pb_dtype == torch.float32 and x.dtype == torch.bfloat16
+        if pb_dtype != x.dtype and not pb_f32:
+            raise ValueError(f"a {pb_dtype} pair bias over a {x.dtype} transition is not supported")
         pb_n, pb_heads = int(x.shape[-2]), pair_bias_for.heads
         np_ = (pb_n + 63) // 64 * 64
-        pb = torch.empty((rows // (pb_n * pb_n), pb_heads, np_, np_), dtype=x.dtype, device=x.device)
+        pb = torch.empty((rows // (pb_n * pb_n), pb_heads, np_, np_), dtype=pb_dtype, device=x.device)
     rm = _rows_of(row_mask, x.shape[:-1], x.dtype, "row_mask")
     om = _rows_of(out_mask, x.shape[:-1], x.dtype, "out_mask")
     res = None if residual is None else residual.to(dtype=x.dtype).contiguous()
@@ -265,7 +272,8 @@ def transition(
         a.pb_norm_bias = _ptr(pair_bias_for.z_norm_bias)
         a.pb_weight = _ptr(pair_bias_for.z_weight)
         a.pb_out = _ptr(pb)
-        _check_weights(x, pair_bias_for)
+        a.pb_f32 = 1 if pb_f32 else 0
+        _check_weights(pb, pair_bias_for)
     _check_weights(x, w)
     _lib.check(lib.fjx_transition_fwd(ctypes.byref(a), _stream(x)))
     return out if pb is None else (out, pb)

@@ -74,12 +74,14 @@ class PairformerLayerWeights:
     transition_s: kernels.TransitionWeights | None
 
     def _pair_bias_prep(self, s: torch.Tensor | None, z: torch.Tensor):
-        """The attention whose pair bias the pair transition can emit: only
-        when the single track runs in the pair track's dtype (the prepared
-        bias is stored in that dtype)."""
-        if self.attention is None or s is None or not _same(self.attention.q_weight, z) or s.dtype != z.dtype:
+        """The attention whose pair bias the pair transition emits: a single
+        track in the pair track's dtype, or a float32 one over a bfloat16
+        pair track (the bias then comes out in float32)."""
+        if self.attention is None or s is None or not _same(self.attention.q_weight, s):
             return None
-        return self.attention
+        if s.dtype == z.dtype or (s.dtype == torch.float32 and z.dtype == torch.bfloat16):
+            return self.attention
+        return None
 
     def _pair_transition(self, z, s, *, row_mask=None, out_mask=None, eps=1e-5):
         att = self._pair_bias_prep(s, z)
@@ -93,10 +95,10 @@ class PairformerLayerWeights:
                 eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
         """Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:133-205``):
         z += tri-mul out, in, tri-attn start, end, transition; s +=
-        attention(LN(s), z, mask); s += transition_s. When s runs in z's dtype
-        the attention's pair bias LN_z(z) w_z^T comes out of the pair
-        transition's epilogue, so z is not read a further time; a float32 s
-        over a bfloat16 z has the attention read z itself."""
+        attention(LN(s), z, mask); s += transition_s. The attention's pair
+        bias LN_z(z) w_z^T comes out of the pair transition's epilogue (in
+        float32 when s is float32 over a bfloat16 z), so z is not read a
+        further time."""
         z = self.triangle.forward(z, pair_mask, eps=eps)
         z, bias = self._pair_transition(z, s, eps=eps)
         s = kernels.single_attention(s, None if bias is not None else z, mask, self.attention, residual=s, eps=eps,

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FJX_ABI_VERSION 5
+#define FJX_ABI_VERSION 6
 
 /* element types of activations, masks and weights */
 enum { FJX_DTYPE_F32 = 0, FJX_DTYPE_BF16 = 1 };
@@ -267,6 +267,10 @@ typedef struct fjx_transition_args {
   const void* pb_weight;       /* [pb_heads, c] */
   void* pb_out;                /* fjx_pair_bias_size(rows / pb_n^2, pb_n, pb_heads, dtype) bytes, or NULL */
   const void* out_mask;        /* NULL, or [rows]: see "Output masks"; the pair bias is taken of the masked rows */
+  int32_t pb_f32;              /* 1: pb_norm_*, pb_weight and pb_out are fp32 over a bf16 transition (an fp32
+                                  single track over the bf16 pair track); the bias is computed to fp32 accuracy
+                                  (bf16 high + low parts, three MFMA products); pb_out holds
+                                  fjx_pair_bias_size(..., FJX_DTYPE_F32) bytes. 0: they are `dtype` */
 } fjx_transition_args;
 
 size_t fjx_transition_workspace_size(int64_t rows, int64_t c, int64_t hidden, int32_t dtype);

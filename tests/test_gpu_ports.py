@@ -364,3 +364,40 @@ def test_boltz2_fp32_single_track_attention_against_fp32_bar():
     want = want + O.transition(want, w["transition_s"])
     err = max_abs(to_np(got), want)
     assert err <= FP32_MAX_ABS, err
+
+
+@pytest.mark.parametrize("n,heads,expansion", [(64, 16, 4), (37, 16, 4), (24, 24, 4), (24, 16, 2)])
+def test_transition_fp32_pair_bias_over_bf16(n, heads, expansion):
+    """A bf16 pair transition preparing the bias of an fp32 attention (the
+    Boltz-2 precision split): the bias is LN_z(out) w_z^T of the transition's
+    own bf16 output to the fp32 bar, zero on the padded border, and the
+    attention fed it agrees with the one that reads z itself (fused epilogue
+    at 16 heads and a 4x width; the separate pass otherwise)."""
+    say(f"transition fp32 pair bias over bf16 n={n} heads={heads} x{expansion}")
+    bf = torch.bfloat16
+    z = syn.pair_input(n, 128, seed=160, batch=1)
+    s = syn.single_input(n, 384, seed=161, batch=1)
+    mask = syn.token_mask(n, n - 2)[None]
+    tr = syn.transition_weights(128, expansion, seed=162)
+    tw = P.pack_transition_torch(P.transition_to_protenix(tr), bf, "cuda")
+    w = syn.single_attention_weights(heads=heads, seed=163)
+    att, pre = P.single_attention_to_boltz2(w)
+    att32 = P.pack_single_attention_boltz2(att, torch.float32, "cuda", pre_norm=pre)
+    zt = device_tensor(z, bf)
+    plain = kernels.transition(zt, tw, residual=zt)
+    out, pb = kernels.transition(zt, tw, residual=zt, pair_bias_for=att32)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain) and pb.dtype == torch.float32
+    np_ = (n + 63) // 64 * 64
+    pbn = to_np(pb)
+    assert not pbn[:, :, n:, :].any() and not pbn[:, :, :, n:].any()
+    ln = O.layer_norm(to_np(out), w["proj_z_norm"]["weight"], w["proj_z_norm"]["bias"])
+    want = np.transpose(O.linear_torch(ln, {"weight": w["proj_z"]["weight"]}), (0, 3, 1, 2)) * np.log2(np.e)
+    err = max_abs(pbn[:, :, :n, :n], want)
+    assert err <= FP32_MAX_ABS, f"fp32 pair bias max-abs {err:.2e}"
+    st, mt = device_tensor(s, torch.float32), device_tensor(mask, torch.float32)
+    ref = kernels.single_attention(st, out, mt, att32, residual=st)
+    got = kernels.single_attention(st, None, mt, att32, residual=st, pair_bias=pb)
+    torch.cuda.synchronize()
+    err = max_abs(to_np(got), to_np(ref))
+    assert err <= FP32_MAX_ABS, f"attention with the prepared fp32 bias: max-abs {err:.2e}"
