@@ -234,3 +234,31 @@ def test_stacked_layers_share_one_buffer_per_weight_kind():
         StackedLayers([ls[0], other])
     with pytest.raises(ValueError, match="empty"):
         stacked_or_stack([])
+
+
+def test_neutral_triangle_kernel_knob():
+    """``triangle_kernel`` (``src/foldjax/execution.py:43``) gains "hip";
+    "auto" maps to it explicitly on every port, the reference's values keep
+    their native spellings, and errors follow ``execution.translate``."""
+    from foldjax_amd import execution as E
+
+    for model, native in (("boltz2", "triangle_backend"), ("protenix", "trunk_triangle_attention_backend"),
+                          ("openfold3", "triangle_kernel")):
+        assert E.translate({"triangle_kernel": "auto"}, model) == {native: "hip"}
+        assert E.triangle_kernel(model) == "hip" and E.triangle_kernel(model, "hip") == "hip"
+    assert E.triangle_kernel("protenix", "cueq") == "cueq_jit"
+    assert E.triangle_kernel("protenix", "xla") == "xla_jit"
+    assert E.triangle_kernel("boltz2", "xla") == "xla"
+    with pytest.raises(ValueError, match="must be one of"):
+        E.translate({"triangle_kernel": "pallas"}, "boltz2")
+    with pytest.raises(ValueError, match="were both set"):
+        E.translate({"triangle_kernel": "auto", "triangle_backend": "xla"}, "boltz2")
+    with pytest.raises(ValueError, match="unknown model"):
+        E.translate({"triangle_kernel": "auto"}, "af2")
+    assert E.normalize({"triangle_backend": "hip"}, native=set()) == {"triangle_kernel": "hip"}
+    assert E.normalize({"triangle_backend": "hip"}, native={"triangle_backend"}) == {"triangle_backend": "hip"}
+    # the translated value is accepted by the port's own selector
+    assert boltz2.resolve_matmul_precision("highest")
+    with pytest.raises(RuntimeError, match="JAX backend"):
+        protenix.triangle_attention(_z(8), None, P.triattn_to_protenix(syn.triattn_weights()), num_heads=4,
+                                    attention_backend=E.triangle_kernel("protenix", "xla"))

@@ -539,3 +539,28 @@ def test_triattn_row_subset_equals_full_rows(starting):
         f32 = O.protenix_triangle_attention(z, mask, w, num_heads=2, starting=starting, rows=rows)
     assert f32.dtype == np.float32
     np.testing.assert_allclose(f32, grid[rows], rtol=1e-4, atol=1e-4)
+
+
+# ------------------------------------------------------------ golden fixtures
+
+
+def test_oracle_matches_golden_fixtures():
+    """Every committed fixture (inputs and the brute-force loops' outputs,
+    tests/golden/make_golden.py) against the oracle, both directions and
+    nodes, float32 and bf16-rounded inputs."""
+    from tests.golden import fixtures
+
+    n_cases = 0
+    for c in fixtures.cases("trimul"):
+        for d in ("outgoing", "incoming"):
+            got = O.protenix_triangle_multiplication(c["z"], c["mask"], c["w"], d)
+            np.testing.assert_allclose(got, c["out"][d], rtol=1e-9, atol=1e-9, err_msg=f"{c['tag']} {c['name']} {d}")
+            n_cases += 1
+    for c in fixtures.cases("triattn"):
+        for node in ("starting", "ending"):
+            got = O.protenix_triangle_attention(c["z"], c["mask"], c["w"], num_heads=c["heads"],
+                                                starting=node == "starting")
+            np.testing.assert_allclose(got, c["out"][node], rtol=1e-9, atol=1e-9,
+                                       err_msg=f"{c['tag']} {c['name']} {node}")
+            n_cases += 1
+    assert n_cases == 40
