@@ -44,6 +44,69 @@ def compute_dtype(dtype):
         _DT.pop()
 
 
+# ---------------------------------------------------------------------------
+# bfloat16 programs (analysis mode)
+# ---------------------------------------------------------------------------
+
+_PROGRAM = [None]  # the port whose bfloat16 program is emulated, or None
+
+#: Where each port's jnp program, run on bfloat16 inputs and weights, stores a
+#: bfloat16 result: a jnp op on bfloat16 operands returns bfloat16. Points not
+#: listed stay exact.
+#:   Boltz-2 takes LayerNorm statistics in float32 and rounds the normalized
+#:   value before the affine (``B2P/_common.py:15-26``); its attention core
+#:   upcasts q, k, v and both biases and keeps scores, softmax and the
+#:   probability-value product in float32 (``B2T/triangle_attention.py:446-455``).
+#:   Protenix runs every LayerNorm op in bfloat16 (``PXP/primitives.py:57-72``),
+#:   multiplies bfloat16 q and k into bfloat16 logits, adds the float32 mask
+#:   bias and the triangle bias, takes softmax in float32 and rounds the
+#:   probabilities to bfloat16 before the value product (``PXT/triangle.py:850-860``).
+#: Both store every projection, the scaled q, the sigmoid gates, the gated
+#: products and the triangle contraction (Protenix accumulates it in float32
+#: and casts, ``PXT/triangle.py:174``) in bfloat16.
+_POINTS = {
+    "boltz2": frozenset({"ln_normed", "ln_affine", "linear", "q_scale", "sigmoid", "gated", "contract", "attn_out"}),
+    "protenix": frozenset(
+        {"ln_ops", "ln_affine", "linear", "q_scale", "sigmoid", "gated", "contract", "logits", "probs", "attn_out"}
+    ),
+}
+
+
+@contextlib.contextmanager
+def bf16_program(port):
+    """Round where ``port``'s bfloat16 program stores bfloat16 (``_POINTS``).
+
+    Analysis mode, used to measure how far apart the ports' own bfloat16
+    results are and where the HIP kernels sit between them; no parity bar
+    rests on it (XLA's fusion may keep some of these values in float32, which
+    only running the reference could settle). Inputs and weights should be
+    bfloat16 values already. ``port=None`` is the exact default."""
+    if port is not None and port not in _POINTS:
+        raise ValueError(f"unknown port {port!r}; expected one of {tuple(_POINTS)}")
+    _PROGRAM.append(port)
+    try:
+        yield
+    finally:
+        _PROGRAM.pop()
+
+
+def bf16(x):
+    """Round to the nearest bfloat16 value (ties to even), as float64."""
+    b = np.ascontiguousarray(np.asarray(x, dtype=np.float32)).view(np.uint32)
+    r = (b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) & np.uint32(0xFFFF0000)
+    r = r.astype(np.uint32).view(np.float32).astype(F64)
+    x32 = np.asarray(x, dtype=np.float32)
+    return np.where(np.isfinite(x32), r, x32.astype(F64))  # inf stays inf, NaN stays NaN
+
+
+def _st(x, point):
+    """``x`` as the emulated program stores it at ``point``."""
+    port = _PROGRAM[-1]
+    if port is None or point not in _POINTS[port]:
+        return x
+    return bf16(x)
+
+
 def _get(obj, name):
     """Field access for dict- or NamedTuple-shaped parameter containers."""
     if isinstance(obj, dict):
@@ -69,13 +132,21 @@ def layer_norm(x, weight, bias, eps=1e-5):
     weight/bias follow the Protenix/OpenFold3 containers.
     """
     x = _f(x)
-    mean = x.mean(axis=-1, keepdims=True)
-    var = np.square(x - mean).mean(axis=-1, keepdims=True)
-    y = (x - mean) / np.sqrt(var + eps)
+    if _PROGRAM[-1] is not None and "ln_ops" in _POINTS[_PROGRAM[-1]]:
+        # every op of the LayerNorm rounded to bfloat16
+        mean = _st(x.mean(axis=-1, keepdims=True), "ln_ops")
+        d = _st(x - mean, "ln_ops")
+        var = _st(_st(np.square(d), "ln_ops").mean(axis=-1, keepdims=True), "ln_ops")
+        r = _st(1.0 / _st(np.sqrt(_st(var + eps, "ln_ops")), "ln_ops"), "ln_ops")
+        y = _st(d * r, "ln_ops")
+    else:
+        mean = x.mean(axis=-1, keepdims=True)
+        var = np.square(x - mean).mean(axis=-1, keepdims=True)
+        y = _st((x - mean) / np.sqrt(var + eps), "ln_normed")
     if weight is not None:
-        y = y * _f(weight)
+        y = _st(y * _f(weight), "ln_affine")
     if bias is not None:
-        y = y + _f(bias)
+        y = _st(y + _f(bias), "ln_affine")
     return y
 
 
@@ -87,7 +158,7 @@ def sigmoid(x):
     """
     x = _f(x)
     e = np.exp(-np.abs(x))
-    return np.where(x >= 0, 1.0 / (1.0 + e), e / (1.0 + e))
+    return _st(np.where(x >= 0, 1.0 / (1.0 + e), e / (1.0 + e)), "sigmoid")
 
 
 def silu(x):
@@ -101,7 +172,7 @@ def _mm(x, w_in_out):
     x = _f(x)
     w = np.ascontiguousarray(_f(w_in_out))
     y = np.ascontiguousarray(x).reshape(-1, x.shape[-1]) @ w
-    return y.reshape(x.shape[:-1] + (w.shape[-1],))
+    return _st(y.reshape(x.shape[:-1] + (w.shape[-1],)), "linear")
 
 
 def linear_torch(x, lin):
@@ -109,7 +180,7 @@ def linear_torch(x, lin):
     y = _mm(x, _f(_get(lin, "weight")).T)
     b = _get(lin, "bias")
     if b is not None:
-        y = y + _f(b)
+        y = _st(y + _f(b), "linear")
     return y
 
 
@@ -167,14 +238,14 @@ def boltz2_triangle_multiplication(params, x, mask, direction, eps=1e-5):
     """
     x = layer_norm(x, params["norm_in"]["scale"], params["norm_in"]["bias"], eps)
     mask = _f(mask)
-    proj = sigmoid(_mm(x, params["g_in"]["kernel"])) * _mm(x, params["p_in"]["kernel"])
-    proj = proj * mask[..., None]
+    proj = _st(sigmoid(_mm(x, params["g_in"]["kernel"])) * _mm(x, params["p_in"]["kernel"]), "gated")
+    proj = _st(proj * mask[..., None], "gated")
     a, b = np.split(proj, 2, axis=-1)
-    out = triangle_contract(a, b, direction)
+    out = _st(triangle_contract(a, b, direction), "contract")
     out = layer_norm(out, params["norm_out"]["scale"], params["norm_out"]["bias"], eps)
     out = _mm(out, params["p_out"]["kernel"])
     gate = sigmoid(_mm(x, params["g_out"]["kernel"]))
-    return out * gate
+    return _st(out * gate, "gated")
 
 
 def protenix_triangle_multiplication(z, mask, params, direction):
@@ -189,14 +260,14 @@ def protenix_triangle_multiplication(z, mask, params, direction):
         mask = np.ones(z.shape[:-1])
     m = _f(mask)[..., None]
     zn = layer_norm(z, *_ln_params(_get(params, "layer_norm_in")))
-    b = m * sigmoid(linear_torch(zn, _get(params, "linear_b_g")))
-    b = b * linear_torch(zn, _get(params, "linear_b_p"))
-    a = m * sigmoid(linear_torch(zn, _get(params, "linear_a_g")))
-    a = a * linear_torch(zn, _get(params, "linear_a_p"))
-    out = triangle_contract(a, b, direction)
+    b = _st(m * sigmoid(linear_torch(zn, _get(params, "linear_b_g"))), "gated")
+    b = _st(b * linear_torch(zn, _get(params, "linear_b_p")), "gated")
+    a = _st(m * sigmoid(linear_torch(zn, _get(params, "linear_a_g"))), "gated")
+    a = _st(a * linear_torch(zn, _get(params, "linear_a_p")), "gated")
+    out = _st(triangle_contract(a, b, direction), "contract")
     out = layer_norm(out, *_ln_params(_get(params, "layer_norm_out")))
     out = linear_torch(out, _get(params, "linear_z"))
-    return out * sigmoid(linear_torch(zn, _get(params, "linear_g")))
+    return _st(out * sigmoid(linear_torch(zn, _get(params, "linear_g"))), "gated")
 
 
 def openfold3_triangle_multiplication(z, params, *, outgoing, mask=None, eps=1e-5):
@@ -244,9 +315,10 @@ def attention_rows(q, k, v, mask_bias, tri_bias, row_block=16):
         e = min(n_rows, s + row_block)
         qs, ks, vs = q[..., s:e, :, :, :], k[..., s:e, :, :, :], v[..., s:e, :, :, :]
         mb = mask_bias[..., s:e, :, :, :] if mask_bias.shape[-4] > 1 else mask_bias
-        scores = np.ascontiguousarray(qs) @ np.ascontiguousarray(np.swapaxes(ks, -1, -2))
+        scores = _st(np.ascontiguousarray(qs) @ np.ascontiguousarray(np.swapaxes(ks, -1, -2)), "logits")
         scores = scores + mb + tri_bias
-        out[..., s:e, :, :, :] = softmax(scores, axis=-1) @ np.ascontiguousarray(vs)
+        probs = _st(softmax(scores, axis=-1), "probs")
+        out[..., s:e, :, :, :] = _st(probs @ np.ascontiguousarray(vs), "attn_out")
     return out
 
 
@@ -287,13 +359,13 @@ def boltz2_triangle_attention(params, x, mask=None, starting=True, inf=1e9, eps=
         y = y.reshape(y.shape[:-1] + (heads, d))
         return np.swapaxes(y, -2, -3)
 
-    q = proj("linear_q") / np.sqrt(d)
+    q = _st(proj("linear_q") / np.sqrt(d), "q_scale")
     k = proj("linear_k")
     v = proj("linear_v")
     o = attention_rows(q, k, v, mask_bias, tri_bias)
     o = np.swapaxes(o, -2, -3)  # [..., I, J, H, D]
     gate = sigmoid(_mm(x, mha["linear_g"]["kernel"])).reshape(o.shape)
-    o = (o * gate).reshape(o.shape[:-2] + (heads * d,))
+    o = _st(o * gate, "gated").reshape(o.shape[:-2] + (heads * d,))
     out = _mm(o, mha["linear_o"]["kernel"])
     if not starting:
         out = np.swapaxes(out, -2, -3)
@@ -330,12 +402,12 @@ def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, in
         mask_bias = mask_bias[..., rows, :, :, :]
     att = _get(params, "attention")
     d = _f(_get(_get(att, "linear_k"), "weight")).shape[0] // num_heads
-    q = _split_heads_torch(x, _get(att, "linear_q"), num_heads) * (float(d) ** -0.5)
+    q = _st(_split_heads_torch(x, _get(att, "linear_q"), num_heads) * (float(d) ** -0.5), "q_scale")
     k = _split_heads_torch(x, _get(att, "linear_k"), num_heads)
     v = _split_heads_torch(x, _get(att, "linear_v"), num_heads)
     o = np.swapaxes(attention_rows(q, k, v, mask_bias, tri_bias), -2, -3)
     if _get(att, "linear_g") is not None:
-        o = o * sigmoid(linear_torch(x, _get(att, "linear_g"))).reshape(o.shape)
+        o = _st(o * sigmoid(linear_torch(x, _get(att, "linear_g"))).reshape(o.shape), "gated")
     o = o.reshape(o.shape[:-2] + (-1,))
     out = linear_torch(o, _get(att, "linear_o"))
     if not starting and rows is None:

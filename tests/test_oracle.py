@@ -564,3 +564,87 @@ def test_oracle_matches_golden_fixtures():
                                        err_msg=f"{c['tag']} {c['name']} {node}")
             n_cases += 1
     assert n_cases == 40
+
+
+# ---------------------------------------------------------------------------
+# bfloat16 programs (analysis mode of the oracle)
+# ---------------------------------------------------------------------------
+
+
+def test_bf16_rounding_equals_torch():
+    rng = np.random.default_rng(7)
+    x = np.concatenate([
+        rng.standard_normal(4096) * 10.0 ** rng.integers(-30, 30, 4096),
+        # exact ties between two bfloat16 neighbours, both parities
+        (np.arange(1, 257, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.4e38, -3.4e38, 1e-40]),
+    ]).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).to(torch.float64).numpy()
+    got = O.bf16(x)
+    assert np.array_equal(got, want)
+    assert np.isnan(O.bf16(np.array([np.nan])))[0]
+
+
+def _ta_case(seed, n, scale):
+    rng = np.random.default_rng(seed)
+    z = O.bf16(rng.standard_normal((n, n, 16)))
+    w = syn.cast_tree(syn.triattn_weights(16, 2, 8, seed=seed + 1), O.bf16)
+    for name in ("linear_q", "linear_k"):  # logits of size ~ scale
+        w["attention"][name]["weight"] = O.bf16(np.asarray(w["attention"][name]["weight"]) * np.sqrt(scale))
+    return z, w
+
+
+def test_bf16_programs_round_only_inside_their_context():
+    z, w = _ta_case(0, 6, 1.0)
+    m = np.ones((6, 6))
+    exact = O.protenix_triangle_attention(z, m, w, num_heads=2)
+    with O.bf16_program("protenix"):
+        px = O.protenix_triangle_attention(z, m, w, num_heads=2)
+    with O.bf16_program(None):
+        none = O.protenix_triangle_attention(z, m, w, num_heads=2)
+    assert np.array_equal(none, exact)
+    assert np.array_equal(O.protenix_triangle_attention(z, m, w, num_heads=2), exact)
+    # bfloat16 storage moves the result, by a bfloat16-sized amount
+    rel = np.linalg.norm(px - exact) / np.linalg.norm(exact)
+    assert 1e-4 < rel < 2e-2, rel
+    with pytest.raises(ValueError):
+        with O.bf16_program("alphafold"):
+            pass
+
+
+def test_protenix_program_rounds_logits_boltz2_program_does_not():
+    """On bfloat16 q, k, v: with logits of a few hundred, bfloat16 logits
+    (spacing 1-2) move the softmax weights by factors of e, while Boltz-2's
+    float32 scores leave only the output rounding."""
+    rng = np.random.default_rng(5)
+    errs = {}
+    for scale in (1.0, 300.0):
+        q = O.bf16(rng.standard_normal((4, 2, 16, 8)) * np.sqrt(scale / 8))
+        k = O.bf16(rng.standard_normal((4, 2, 16, 8)) * np.sqrt(scale / 8))
+        v = O.bf16(rng.standard_normal((4, 2, 16, 8)))
+        mb = np.zeros((4, 1, 1, 16))
+        tb = O.bf16(rng.standard_normal((1, 2, 16, 16)))
+        exact = O.attention_rows(q, k, v, mb, tb)
+        for port in ("boltz2", "protenix"):
+            with O.bf16_program(port):
+                got = O.attention_rows(q, k, v, mb, tb)
+            errs[port, scale] = np.linalg.norm(got - exact) / np.linalg.norm(exact)
+    assert errs["boltz2", 300.0] < 4e-3  # the output's own rounding only
+    assert errs["protenix", 300.0] > 5 * errs["boltz2", 300.0], errs
+    assert errs["protenix", 1.0] < 2e-2
+
+
+def test_boltz2_program_layernorm_rounds_normalized_value_before_affine():
+    rng = np.random.default_rng(3)
+    x = O.bf16(rng.standard_normal((64, 32)) * 3.0 + 1.0)
+    w = O.bf16(rng.standard_normal(32))
+    b = O.bf16(rng.standard_normal(32))
+    with O.bf16_program("boltz2"):
+        got = O.layer_norm(x, w, b)
+    mean = x.mean(-1, keepdims=True)
+    normed = O.bf16((x - mean) / np.sqrt(np.square(x - mean).mean(-1, keepdims=True) + 1e-5))
+    assert np.array_equal(got, O.bf16(O.bf16(normed * w) + b))
+    with O.bf16_program("protenix"):
+        px = O.layer_norm(x, w, b)
+    assert not np.array_equal(px, got)  # every op rounded: a different program
+    assert np.abs(px - got).max() < 0.1
