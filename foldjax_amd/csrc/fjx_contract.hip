@@ -14,8 +14,11 @@
 // a register prefetch of the next k-tile. Blocks are numbered so that all
 // tiles of one batch land on one XCD (workgroups are dealt round-robin over
 // the 8 XCDs), keeping that batch's operands in the XCD's L2.
+#include <algorithm>
+
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
+#include "fjx_tile.hpp"
 
 namespace fjx {
 
@@ -306,21 +309,29 @@ __device__ __forceinline__ int dma_swz(int r) { return (r / (16 / CH)) % CH; }
 template <int CH>
 __device__ __forceinline__ int dma_slot(int r, int c) { return CH * r + (c ^ dma_swz<CH>(r)); }
 
+// Persistent: one workgroup per CU walks its XCD's contiguous share of the
+// tiles (workgroup w runs on XCD w % 8), so all tiles of a channel stay on
+// one XCD and reuse its L2. During the last k-step of a tile the first stage
+// of the next tile is already in flight (its LDS buffer is free), and the
+// tile's output stores go out after it: the next tile's first wait then
+// covers that DMA only (vmcnt counts loads and stores in issue order, so it
+// waits for vmcnt(kStores)), and the stores drain under the next k-loop
+// instead of holding the workgroup at its exit.
 template <int DS, int DK>
 __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
                                                            bf16* __restrict__ O, int64_t n, int64_t batches) {
+  static_assert(DS == 2, "the persistent hand-over assumes two stages");
   constexpr int CH = DK / 8;       // 16-byte chunks per row
   constexpr int RPI = 64 / CH;     // rows per DMA instruction (1 KB)
   constexpr int NI = CH / 2;       // DMA instructions per wave per operand per stage
+  constexpr int kStores = 32;      // output stores per lane per tile (8 x 4 of 4 elements)
   __shared__ __attribute__((aligned(16))) bf16 S[DS][2][kCT * DK];  // [stage][A, B][256 rows x DK]
 
   const int64_t tpd = n / kCT;
   const int64_t total = batches * tpd * tpd;
-  const int64_t lid = xcd_remap(blockIdx.x, total);
-  const int64_t bat = lid / (tpd * tpd);
-  const int64_t tile = lid % (tpd * tpd);
-  const int64_t m0 = (tile / tpd) * kCT;
-  const int64_t n0 = (tile % tpd) * kCT;
+  const int64_t per_xcd = gridDim.x / kNumXcd;  // workgroups per XCD (the grid is a multiple of 8)
+  const int64_t xcd = blockIdx.x % kNumXcd;
+  const int64_t hi = (xcd + 1) * total / kNumXcd;  // this XCD's tiles: [xcd * total / 8, hi)
 
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -334,8 +345,6 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
   // offset that is the same for both operands (row r of the tile, swizzled
   // chunk c); 64-bit per-lane pointers would cost 32 VGPRs at a point where
   // the accumulators leave none to spare
-  const char* base[2] = {reinterpret_cast<const char*>(A + (bat * n + m0) * n),
-                         reinterpret_cast<const char*>(B + (bat * n + n0) * n)};
   uint32_t voff[NI];
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
@@ -343,79 +352,113 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
     const int c = (lane % CH) ^ dma_swz<CH>(r);
     voff[j] = (uint32_t)(r * n * 2 + 16 * c);
   }
+  struct Tile {
+    int64_t bat, m0, n0;
+    const char* base[2];
+  };
+  auto tile_of = [&](int64_t lid) {
+    Tile tl;
+    tl.bat = lid / (tpd * tpd);
+    const int64_t r = lid % (tpd * tpd);
+    tl.m0 = (r / tpd) * kCT;
+    tl.n0 = (r % tpd) * kCT;
+    tl.base[0] = reinterpret_cast<const char*>(A + (tl.bat * n + tl.m0) * n);
+    tl.base[1] = reinterpret_cast<const char*>(B + (tl.bat * n + tl.n0) * n);
+    return tl;
+  };
   // k-tile kt goes to stage kt % DS; the stage is always a compile-time
   // constant (a run-time stage index makes the compiler wait for every DMA in
   // flight before each LDS read)
-  auto issue = [&](int64_t kt, int st) {
+  auto issue = [&](const Tile& tl, int64_t kt, int st) {
     const int64_t k0 = kt * DK;
 #pragma unroll
     for (int op = 0; op < 2; ++op)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(base[op] + 2 * k0 + voff[j]),
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(tl.base[op] + 2 * k0 + voff[j]),
                                          reinterpret_cast<void*>(&S[st][op][(32 * wave + RPI * j) * DK]), 16, 0, 0);
   };
 
-  f32x4 acc[4][8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   const int64_t ktiles = n / DK;  // a multiple of DS (checked by the launcher)
+  int64_t lid = xcd * total / kNumXcd + blockIdx.x / kNumXcd;
+  if (lid >= hi) return;
+  Tile cur = tile_of(lid);
+  issue(cur, 0, 0);
+  bool first = true;
+  for (;;) {
+    const int64_t next_lid = lid + per_xcd;
+    const bool has_next = next_lid < hi;
+    const Tile nxt = tile_of(has_next ? next_lid : lid);
+
+    f32x4 acc[4][8];
 #pragma unroll
-  for (int s0 = 0; s0 < DS - 1; ++s0) issue(s0, s0);
-  for (int64_t kb = 0; kb < ktiles; kb += DS) {
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int st = 0; st < DS; ++st) {
-      const int64_t kt = kb + st;
-      // opaque per iteration: keeps the compiler from hoisting base + voff
-      // into eight loop-invariant 64-bit pointers (it then spills them)
+      for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t kb = 0; kb < ktiles; kb += DS) {
 #pragma unroll
-      for (int j = 0; j < NI; ++j) asm volatile("" : "+v"(voff[j]));
-      const int64_t later = min<int64_t>(DS - 2, ktiles - 1 - kt);
-      if (DS >= 4 && later >= 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * 2 * NI));
-      else if (DS >= 3 && later >= 1) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * NI));
-      else __builtin_amdgcn_s_waitcnt(0xF70);
-      __builtin_amdgcn_s_barrier();
-      if (kt + DS - 1 < ktiles) issue(kt + DS - 1, (st + DS - 1) % DS);
-      const bf16* As_ = &S[st][0][0];
-      const bf16* Bs_ = &S[st][1][0];
+      for (int st = 0; st < DS; ++st) {
+        const int64_t kt = kb + st;
+        // opaque per iteration: keeps the compiler from hoisting base + voff
+        // into eight loop-invariant 64-bit pointers (it then spills them)
 #pragma unroll
-      for (int ks = 0; ks < DK / 32; ++ks) {
-        bf16x8 af[8], bfr[4];
+        for (int j = 0; j < NI; ++j) asm volatile("" : "+v"(voff[j]));
+        // this wave's DMA of stage st is complete; on a tile's first k-step
+        // the previous tile's stores, issued after that DMA, may still run
+        if (st == 0 && kt == 0 && !first) __builtin_amdgcn_s_waitcnt(0x0F70 | ((kStores >> 4) << 14) | (kStores & 15));
+        else __builtin_amdgcn_s_waitcnt(0xF70);
+        __builtin_amdgcn_s_barrier();
+        if (kt + 1 < ktiles) issue(cur, kt + 1, st ^ 1);
+        else if (has_next) issue(nxt, 0, st ^ 1);  // stage 0 of the next tile (ktiles is even: buffer 0)
+        const bf16* As_ = &S[st][0][0];
+        const bf16* Bs_ = &S[st][1][0];
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-          af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * dma_slot<CH>(wm + 16 * i + li, 4 * ks + lg));
+        for (int ks = 0; ks < DK / 32; ++ks) {
+          bf16x8 af[8], bfr[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * dma_slot<CH>(wn + 16 * j + li, 4 * ks + lg));
+          for (int i = 0; i < 8; ++i)
+            af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * dma_slot<CH>(wm + 16 * i + li, 4 * ks + lg));
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < 4; ++j)
+            bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * dma_slot<CH>(wn + 16 * j + li, 4 * ks + lg));
 #pragma unroll
-          for (int i = 0; i < 8; ++i) mma(acc[j][i], bfr[j], af[i]);
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mma(acc[j][i], bfr[j], af[i]);
+        }
       }
     }
-  }
 
-  bf16* Ob = O + bat * n * n;
+    bf16* Ob = O + cur.bat * n * n;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int64_t row = m0 + wm + 16 * i + li;
+    for (int i = 0; i < 8; ++i) {
+      const int64_t row = cur.m0 + wm + 16 * i + li;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + wn + 16 * j + 4 * lg;
-      float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
-      store4f(Ob + row * n + col, v);
+      for (int j = 0; j < 4; ++j) {
+        const int64_t col = cur.n0 + wn + 16 * j + 4 * lg;
+        float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
+        store4f(Ob + row * n + col, v);
+      }
     }
+    if (!has_next) break;
+    lid = next_lid;
+    cur = nxt;
+    first = false;
   }
 }
 
 void launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st) {
   const int64_t tpd = (n + kCT - 1) / kCT;
-  if (n % kCT == 0)
-    hipLaunchKernelGGL((contract_dma_kernel<2, 64>), dim3((unsigned)(batches * tpd * tpd)), dim3(512), 0, st, a, b,
-                       o, n, batches);
+  if (n % kCT == 0) {
+    // persistent: the device's resident capacity, a multiple of the 8 XCDs,
+    // and no more workgroups than tiles need (rounded up to 8)
+    const void* k = reinterpret_cast<const void*>(&contract_dma_kernel<2, 64>);
+    const int64_t total = batches * tpd * tpd;
+    const int64_t cap = std::max<int64_t>(kNumXcd, tile::resident_blocks(k, 512) / kNumXcd * kNumXcd);
+    const int64_t grid = std::min<int64_t>(cap, (total + kNumXcd - 1) / kNumXcd * kNumXcd);
+    hipLaunchKernelGGL((contract_dma_kernel<2, 64>), dim3((unsigned)grid), dim3(512), 0, st, a, b, o, n, batches);
+  }
   else
     hipLaunchKernelGGL(contract_kernel, dim3((unsigned)(batches * tpd * tpd)), dim3(512), 0, st, a, b, o, n,
                        batches);
