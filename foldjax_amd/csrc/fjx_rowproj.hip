@@ -345,6 +345,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
   // whose transposing LDS writes collide more)
   RowPart<T> xr;
   typename Frag<T>::type ot[4];
+  T om[kTE / 16];  // the output mask of this lane's output positions, fetched with the tile
   auto o_chunk = [&](int it, int& ch, int& p0) {
     const int grp = 4 * it + wave;  // 0..15
     ch = 16 * (grp & 7) + (lane & 15);
@@ -367,6 +368,10 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
         for (int e = 0; e < 8; ++e) ot[it][e] = (p0 + e < nvalid) ? src[(int64_t)ch * nn + p0 + e] : from_f32<T>(0.f);
       }
     }
+    if (P.out_mask) {
+#pragma unroll
+      for (int rt = 0; rt < kTE / 16; ++rt) om[rt] = P.out_mask[pos0 + min(16 * rt + (lane & 15), nvalid - 1)];
+    }
   };
 
   int64_t tile = blockIdx.x;
@@ -378,6 +383,14 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
 
     if (res_x) store_row_part<T>(xr, &xraw[p][0]);
+    // the output gate of this tile (bit rt: row tile rt is kept), taken
+    // before the next fetch replaces om
+    uint32_t keep = (1u << (kTE / 16)) - 1;
+    if (P.out_mask) {
+      keep = 0;
+#pragma unroll
+      for (int rt = 0; rt < kTE / 16; ++rt) keep |= to_f32(om[rt]) != 0.f ? 1u << rt : 0u;
+    }
     ln_quad<T>(xr, ln_in, P.eps, &xg[p][0]);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
@@ -419,7 +432,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
           for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
         if (P.out_mask) {
-          const float g = to_f32(P.out_mask[pos0 + pp]) != 0.f ? 1.f : 0.f;
+          const float g = (keep >> rt) & 1u ? 1.f : 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) y[e] *= g;
         }
@@ -474,6 +487,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
   // col0 + 8g .. +7)
   RowPart<T> xr;
   typename Frag<T>::type ov[kTE / 16];
+  T om[kTE / 16];  // the output mask of this lane's output positions, fetched with the tile
   auto fetch = [&](int64_t tile) {
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
@@ -489,6 +503,10 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
         for (int e = 0; e < 8; ++e) ov[rt][e] = from_f32<T>(0.f);
       }
     }
+    if (P.out_mask) {
+#pragma unroll
+      for (int rt = 0; rt < kTE / 16; ++rt) om[rt] = P.out_mask[orig_of(tl, min(16 * rt + (lane & 15), nvalid - 1))];
+    }
   };
 
   int64_t tile = blockIdx.x;
@@ -499,6 +517,14 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
 
     if (res_x) store_row_part<T>(xr, &xraw[p][0]);
+    // the output gate of this tile (bit rt: row tile rt is kept), taken
+    // before the next fetch replaces om
+    uint32_t keep = (1u << (kTE / 16)) - 1;
+    if (P.out_mask) {
+      keep = 0;
+#pragma unroll
+      for (int rt = 0; rt < kTE / 16; ++rt) keep |= to_f32(om[rt]) != 0.f ? 1u << rt : 0u;
+    }
     if (gated) {
       ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
       __syncthreads();
@@ -540,7 +566,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
           for (int e = 0; e < 8; ++e) y[e] += rv[e];
         }
         if (P.out_mask) {
-          const float g = to_f32(P.out_mask[orig_of(tl, pp)]) != 0.f ? 1.f : 0.f;
+          const float g = (keep >> rt) & 1u ? 1.f : 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) y[e] *= g;
         }

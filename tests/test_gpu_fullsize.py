@@ -201,6 +201,28 @@ def test_trimul_multi_tile_sampled(n, n_real, direction):
     check_trimul(z, pm, wt, prep_tree(w, BF16), direction, pos, f"n={n} {direction}")
 
 
+def test_trimul_persistent_batch_n768():
+    """The persistent LDS-DMA contraction walks each XCD's share of the
+    (batch, channel, tile) space; at N=768 (3x3 tiles of 256 per channel) and
+    a batch of 3 the shares cut across channels and batch items and the
+    workgroups take unequal tile counts. Each item of the batched call equals
+    the item run alone, bit for bit, and item 1 matches the oracle at sampled
+    positions."""
+    n, n_real, batch = 768, 750, 3
+    say(f"trimul persistent contraction n={n} batch={batch}")
+    w = syn.trimul_weights(seed=31)
+    wt = P.pack_trimul_torch(P.trimul_to_protenix(w), BF16, "cuda")
+    pm = syn.pair_mask(n, n_real)
+    zb = device_normal((batch, n, n, 128), seed=32)
+    mb = torch.from_numpy(np.stack([pm] * batch)).to("cuda", BF16)
+    for direction in ("outgoing", "incoming"):
+        out = kernels.trimul(zb, mb, wt, direction)
+        for i in range(batch):
+            torch.testing.assert_close(out[i], kernels.trimul(zb[i], mb[i], wt, direction), rtol=0, atol=0)
+        pos = [(i, j) for i in (0, 255, 256, 511, 512, n - 1) for j in (0, 256, 511, 512, n_real, n - 1)]
+        check_trimul(zb[1], pm, wt, prep_tree(w, BF16), direction, pos, f"n={n} batch item 1 {direction}")
+
+
 def test_config4_trunk_48_layers_n2048():
     """the 48-layer trunk at N=2048 (all-ones mask, each
     layer with its own weights). Layer-level parity is
