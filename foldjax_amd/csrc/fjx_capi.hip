@@ -253,9 +253,10 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] { launch_trimul_prologue<T>(pp, a->batch, st); });
   if (rc) return rc;
 
+  bool o_blocked = false;  // the LDS-DMA contraction writes o tile-blocked for the epilogue
   rc = timed(K_TRIMUL_CONTRACT, st, "trimul_contract", [&] {
     if constexpr (std::is_same<T, bf16>::value) {
-      launch_contract(abuf, bbuf, obuf, a->n, a->batch * 128, st);
+      o_blocked = launch_contract(abuf, bbuf, obuf, a->n, a->batch * 128, st, true);
     } else {
       GemmParams<T, T> cp = {};
       cp.a = abuf;
@@ -270,8 +271,9 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   });
   if (rc) return rc;
 
-  TriMulEpilogueParams<T> ep;
+  TriMulEpilogueParams<T> ep = {};
   ep.o = obuf;
+  ep.o_blocked = o_blocked;
   ep.x = static_cast<const T*>(a->x);
   ep.ln_in_w = pp.ln_w;
   ep.ln_in_b = pp.ln_b;

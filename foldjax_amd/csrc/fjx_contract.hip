@@ -23,6 +23,7 @@
 namespace fjx {
 
 constexpr int kNumXcd = 8;
+constexpr int64_t kOBlk = 256;  // positions per block of the tile-blocked output
 
 template <typename T> struct GemmCfg;
 template <> struct GemmCfg<bf16> { static constexpr int BK = 64; };
@@ -319,7 +320,8 @@ __device__ __forceinline__ int dma_slot(int r, int c) { return CH * r + (c ^ dma
 // instead of holding the workgroup at its exit.
 template <int DS, int DK>
 __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restrict__ A, const bf16* __restrict__ B,
-                                                           bf16* __restrict__ O, int64_t n, int64_t batches) {
+                                                           bf16* __restrict__ O, int64_t n, int64_t batches,
+                                                           bool blocked) {
   static_assert(DS == 2, "the persistent hand-over assumes two stages");
   constexpr int CH = DK / 8;       // 16-byte chunks per row
   constexpr int RPI = 64 / CH;     // rows per DMA instruction (1 KB)
@@ -430,15 +432,33 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
       }
     }
 
-    bf16* Ob = O + cur.bat * n * n;
+    if (blocked) {
+      // [item][position / 64][channel][position % 64]; cur.bat = item * 128 + channel
+      // the tile's 256 columns are one 256-position block of each row (n and
+      // n0 are multiples of 256): block row * n/256 + n0/256
+      bf16* Ob = O + ((cur.bat >> 7) * (n * n) * tile::kC) + (cur.bat & 127) * kOBlk +
+                 (cur.n0 / kOBlk) * (tile::kC * kOBlk) + wn + 4 * lg;
+      const int64_t bpr = (n / kOBlk) * (tile::kC * kOBlk);  // elements per row of blocks
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t row = cur.m0 + wm + 16 * i + li;
+      for (int i = 0; i < 8; ++i) {
+        bf16* dst = Ob + (cur.m0 + wm + 16 * i + li) * bpr;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t col = cur.n0 + wn + 16 * j + 4 * lg;
-        float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
-        store4f(Ob + row * n + col, v);
+        for (int j = 0; j < 4; ++j) {
+          float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
+          store4f(dst + 16 * j, v);
+        }
+      }
+    } else {
+      bf16* Ob = O + cur.bat * n * n;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t row = cur.m0 + wm + 16 * i + li;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t col = cur.n0 + wn + 16 * j + 4 * lg;
+          float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
+          store4f(Ob + row * n + col, v);
+        }
       }
     }
     if (!has_next) break;
@@ -448,20 +468,23 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
   }
 }
 
-void launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st) {
+bool launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st,
+                     bool blocked) {
   const int64_t tpd = (n + kCT - 1) / kCT;
   if (n % kCT == 0) {
+    blocked = blocked && batches % tile::kC == 0;
     // persistent: the device's resident capacity, a multiple of the 8 XCDs,
     // and no more workgroups than tiles need (rounded up to 8)
     const void* k = reinterpret_cast<const void*>(&contract_dma_kernel<2, 64>);
     const int64_t total = batches * tpd * tpd;
     const int64_t cap = std::max<int64_t>(kNumXcd, tile::resident_blocks(k, 512) / kNumXcd * kNumXcd);
     const int64_t grid = std::min<int64_t>(cap, (total + kNumXcd - 1) / kNumXcd * kNumXcd);
-    hipLaunchKernelGGL((contract_dma_kernel<2, 64>), dim3((unsigned)grid), dim3(512), 0, st, a, b, o, n, batches);
+    hipLaunchKernelGGL((contract_dma_kernel<2, 64>), dim3((unsigned)grid), dim3(512), 0, st, a, b, o, n, batches,
+                       blocked);
+    return blocked;
   }
-  else
-    hipLaunchKernelGGL(contract_kernel, dim3((unsigned)(batches * tpd * tpd)), dim3(512), 0, st, a, b, o, n,
-                       batches);
+  hipLaunchKernelGGL(contract_kernel, dim3((unsigned)(batches * tpd * tpd)), dim3(512), 0, st, a, b, o, n, batches);
+  return false;
 }
 
 template <typename T, typename TO>

@@ -48,7 +48,7 @@ struct TriAttnPrologueParams {
 
 template <typename T>
 struct TriMulEpilogueParams {
-  const T* o;         // contraction output, channel-major [B][128][N*N]
+  const T* o;         // contraction output, channel-major [B][128][N*N], or tile-blocked (o_blocked)
   const T* x;         // the op's input [B][N][N][128] (for the output gate)
   const T* ln_in_w;   // LN_in, recomputed for the gate
   const T* ln_in_b;
@@ -61,6 +61,10 @@ struct TriMulEpilogueParams {
   T* out;
   int64_t n;
   float eps;
+  // o tile-blocked: [B][N*N/256][128][256], the 128 channels of 256
+  // consecutive positions in one 64 KB block (the LDS-DMA contraction's
+  // blocked output)
+  bool o_blocked;
 };
 
 template <typename T>
@@ -165,7 +169,11 @@ void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, h
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st);
 // triangle contraction, bf16: o[c] = a[c] b[c]^T for c < batches, each n x n
-void launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st);
+// blocked: write o tile-blocked, [batches / 128][N*N/256][128][256] (needs
+// batches a multiple of 128 and n a multiple of 256), else [batches][N*N];
+// returns whether it wrote the blocked layout
+bool launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t batches, hipStream_t st,
+                     bool blocked = false);
 template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st);
 

@@ -356,16 +356,21 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
     load_row_part<T>(p < nvalid ? P.x + (pos0 + p) * kC : nullptr, xr);
-    const T* src = P.o + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
+    // channel-major: channel ch of the tile at src + ch * nn; tile-blocked:
+    // the whole tile is one contiguous [128][64] block
+    const int64_t cstride = P.o_blocked ? 256 : nn;
+    const int64_t ipos = (int64_t)tl.r * n + tl.s0;  // within the batch item
+    const T* src = P.o_blocked ? P.o + ((int64_t)tl.b * nn + (ipos & ~(int64_t)255)) * kC + (ipos & 255)
+                               : P.o + (int64_t)tl.b * kC * nn + ipos;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       int ch, p0;
       o_chunk(it, ch, p0);
       if (vec8 && p0 + 8 <= nvalid) {
-        ot[it] = load8(src + (int64_t)ch * nn + p0);
+        ot[it] = load8(src + (int64_t)ch * cstride + p0);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ot[it][e] = (p0 + e < nvalid) ? src[(int64_t)ch * nn + p0 + e] : from_f32<T>(0.f);
+        for (int e = 0; e < 8; ++e) ot[it][e] = (p0 + e < nvalid) ? src[(int64_t)ch * cstride + p0 + e] : from_f32<T>(0.f);
       }
     }
     if (P.out_mask) {
