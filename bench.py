@@ -19,7 +19,7 @@ times the float32 numpy restatement (``oracle/``) on a bounded sample of the
 headline workload and on configs 1 and 2.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--n N] [--no-cpu] [--no-configs]
-    python bench.py --op trimul|triattn|transition|copy   (one sublayer kind, a profiling aid)
+    python bench.py --op trimul|triattn|transition|transition_pb|copy   (one sublayer kind, a profiling aid)
 """
 
 from __future__ import annotations
@@ -52,7 +52,7 @@ def _args():
     p.add_argument("--single-dtype", default="fp32", choices=["fp32", "bf16"],
                    help="the single track's dtype: fp32 as the reference runs it over the bf16 pair track "
                         "(B2K/pairformer.py:182-199), or bf16")
-    p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "copy"],
+    p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "transition_pb", "copy"],
                    help="profiling aid: run only one sublayer kind per step instead of the whole block")
     return p.parse_args()
 
@@ -313,6 +313,9 @@ def main() -> int:
         "trimul": lambda: (s0, kernels.trimul(z0, pmask, tri.tri_mul_out, "outgoing", residual=z0)),
         "triattn": lambda: (s0, kernels.triattn(z0, pmask, tri.tri_att_start, starting=True, residual=z0)),
         "transition": lambda: (s0, kernels.transition(z0, layer.transition_z, residual=z0)),
+        # the block's form: the transition also writes the single attention's pair bias
+        "transition_pb": lambda: (s0, kernels.transition(z0, layer.transition_z, residual=z0,
+                                                         pair_bias_for=layer.attention)[0]),
         # one elementwise pass over the pair tensor (N*N*128*2 bytes read and
         # written by torch's neg kernel): the calibration point for the
         # FETCH_SIZE / WRITE_SIZE counters

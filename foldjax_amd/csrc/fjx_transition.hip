@@ -77,8 +77,8 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P,
 // dropped lo.lo term is below 2^-16 of the product). The high parts go to
 // xs, the low parts to hs (free after the last chunk).
 __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf16>& P, bf16 (*xs)[tile::kLd],
-                                                       bf16 (*hs)[tile::kLd], const tile::LnAffine& ln, int64_t m0,
-                                                       int nvalid) {
+                                                       bf16 (*hs)[tile::kLd], const tile::LnAffine& ln,
+                                                       const bf16 (*wz)[16][tile::kC], int64_t m0, int nvalid) {
   using namespace tile;
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -86,31 +86,13 @@ __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf
   const int li = lane & 15;
   const int lg = lane >> 4;
   const int p = t >> 2;
-  // the weight rows of head l % 16 (zero past pb_heads), split hi + lo
+  // the weight rows of head l % 16, split hi + lo at the kernel's start
+  // (stage_wz_split; zero past pb_heads)
   WCol<bf16> whi, wlo;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    float w[8], hi[8], lo[8];
-    if (li < P.pb_heads) {
-      const float* src = P.pbf_w + (int64_t)li * kC + 32 * ks + 8 * lg;
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(src);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(src + 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        w[e] = w0[e];
-        w[4 + e] = w1[e];
-      }
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) w[e] = 0.f;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      hi[e] = round_to<bf16>(w[e]);
-      lo[e] = w[e] - hi[e];
-    }
-    whi[ks] = pack8<bf16>(hi);
-    wlo[ks] = pack8<bf16>(lo);
+    whi[ks] = load8(&wz[0][li][32 * ks + 8 * lg]);
+    wlo[ks] = load8(&wz[1][li][32 * ks + 8 * lg]);
   }
   __syncthreads();
   {
@@ -159,6 +141,31 @@ __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf
   }
 }
 
+// The fp32 pair-bias weight [heads][128], split once per workgroup into
+// bf16 high and low parts (hi = bf16(w), lo = bf16(w - hi)) in LDS, rows past
+// pb_heads zero: the epilogue then reads its fragments from LDS instead of
+// waiting, at the end of the tile, for global loads and the split
+__device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, bf16 (*wz)[16][tile::kC]) {
+  using namespace tile;
+  const int t = threadIdx.x;  // 512 threads x 4 weights = 16 x 128
+  const int h = t >> 5;
+  const int k0 = 4 * (t & 31);
+  float hi[4], lo[4];
+  if (h < P.pb_heads) {
+    const f32x4 w = *reinterpret_cast<const f32x4*>(P.pbf_w + (int64_t)h * kC + k0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hi[e] = round_to<bf16>(w[e]);
+      lo[e] = w[e] - hi[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) hi[e] = lo[e] = 0.f;
+  }
+  store4f(&wz[0][h][k0], hi);
+  store4f(&wz[1][h][k0], lo);
+}
+
 // ---------------------------------------------------------------------------
 // Pair-track transition (C = 128, hidden 512): 128-row tiles, 512 threads.
 // Wave w owns hidden columns 16w .. 16w+15 of every 128-wide hidden chunk and
@@ -177,6 +184,8 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   __shared__ __attribute__((aligned(16))) T hs[kTP][kLd];  // silu(a) * b, one hidden chunk
   __shared__ __attribute__((aligned(16))) LnAffine ln;
   __shared__ __attribute__((aligned(16))) LnAffine pb_ln;  // the pair-bias epilogue's norm
+  // the fp32 pair-bias weight split into bf16 hi / lo (the fp32-bias form only)
+  __shared__ __attribute__((aligned(16))) bf16 wz[kPbF32 ? 2 : 1][16][kPbF32 ? kC : 8];
 
   const int64_t m0 = (int64_t)blockIdx.x * kTP;
   const int nvalid = (int)min<int64_t>(kTP, P.rows - m0);
@@ -191,7 +200,10 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
     load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
     stage_ln<T>(P.ln_w, P.ln_b, ln);
     if (P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
-    if constexpr (kPbF32) stage_ln<float>(P.pbf_ln_w, P.pbf_ln_b, pb_ln);
+    if constexpr (kPbF32) {
+      stage_ln<float>(P.pbf_ln_w, P.pbf_ln_b, pb_ln);
+      stage_wz_split(P, wz);
+    }
     __syncthreads();
     ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
   }
@@ -286,7 +298,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
     }
   }
   if constexpr (kPbF32) {
-    pair_bias_epilogue_f32(P, xs, hs, pb_ln, m0, nvalid);
+    pair_bias_epilogue_f32(P, xs, hs, pb_ln, wz, m0, nvalid);
   } else {
     if (P.pb_out) pair_bias_epilogue<T>(P, xs, pb_ln, pb_wf, m0, nvalid);
   }
