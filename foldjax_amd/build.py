@@ -39,14 +39,14 @@ def _hipcc() -> str:
     return cand
 
 
-# per-file extras: the flash kernel keeps its MFMA accumulators in VGPRs (its
-# softmax reads and rescales them every block) and never produces NaNs on
-# purpose, so max() needs no NaN canonicalisation
+# per-file extras: the flash kernels keep their MFMA accumulators in VGPRs
+# (the softmax reads the scores, and the offset kernel rescales the outputs,
+# every block) and never produce NaNs on purpose, so max() needs no NaN
+# canonicalisation; the row-projection kernels read their accumulators in
+# the epilogue arithmetic as well
 FILE_FLAGS = {
     "fjx_flash.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "fjx_rowproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-    # scores in VGPRs (compiler MFMAs); the output accumulators are pinned to
-    # AGPRs by inline asm in the kernel itself
     "fjx_flash_pipe.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
