@@ -54,6 +54,11 @@ def _args():
                         "(B2K/pairformer.py:182-199), or bf16")
     p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "transition_pb", "copy"],
                    help="profiling aid: run only one sublayer kind per step instead of the whole block")
+    p.add_argument("--c-z", type=int, default=128,
+                   help="with --op trimul|triattn|transition: the pair width (other than 128 runs the general-width "
+                        "paths, e.g. 64 for the template stack, 384 for OpenDDE's structural pair track)")
+    p.add_argument("--c-h", type=int, default=128, help="with --op trimul: the hidden width")
+    p.add_argument("--heads", type=int, default=4, help="with --op triattn: heads of 32 channels")
     return p.parse_args()
 
 
@@ -308,6 +313,14 @@ def main() -> int:
     from foldjax_amd import kernels
 
     tri = layer.triangle
+    if a.op in ("trimul", "triattn", "transition") and (a.c_z, a.c_h, a.heads) != (128, 128, 4):
+        # the general-width paths at another pair width
+        z0 = torch.from_numpy(syn.pair_input(n, a.c_z, seed=0, batch=1)).to(dev, dtype)
+        from foldjax_amd import params as PP
+        tri.tri_mul_out = PP.pack_trimul_torch(PP.trimul_to_protenix(syn.trimul_weights(a.c_z, a.c_h, seed=3)), dtype, dev)
+        tri.tri_att_start = PP.pack_triattn_protenix(
+            PP.triattn_to_protenix(syn.triattn_weights(a.c_z, a.heads, 32, seed=4)), dtype, dev)
+        layer.transition_z = PP.pack_transition_torch(syn.transition_weights(a.c_z, seed=5), dtype, dev)
     steps_fn = {
         "block": lambda: layer.forward(s0, z0, tmask, pmask),
         "trimul": lambda: (s0, kernels.trimul(z0, pmask, tri.tri_mul_out, "outgoing", residual=z0)),
@@ -354,7 +367,8 @@ def main() -> int:
     ms_step = elapsed * 1e3 / a.steps
     if a.op != "block":
         per = {k: {"avg_ms": round(v[0] / v[1], 4), "launches": v[1]} for k, v in stats.items() if v[1]}
-        print(json.dumps({"op": a.op, "n": n, "ms_per_step": round(ms_step, 4), "kernels": per}))
+        print(json.dumps({"op": a.op, "n": n, "c_z": a.c_z, "c_h": a.c_h, "heads": a.heads,
+                          "ms_per_step": round(ms_step, 4), "kernels": per}))
         return 0
     fl = flops_triangle(n)
     per_launch = {
