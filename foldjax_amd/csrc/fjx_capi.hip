@@ -238,7 +238,9 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   T* bbuf = at<T>(a->workspace, ws.b);
   T* obuf = at<T>(a->workspace, ws.o);
 
-  TriMulPrologueParams<T> pp;
+  // c_z below 128 (the template stack's 64): the narrow forms of the kernels
+  const int cw = a->c_z < 128 ? (int)a->c_z : 0;
+  TriMulPrologueParams<T> pp = {};
   pp.x = static_cast<const T*>(a->x);
   pp.mask = static_cast<const T*>(a->mask);
   pp.ln_w = static_cast<const T*>(a->norm_in_weight);
@@ -250,6 +252,7 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   pp.n = a->n;
   pp.eps = a->eps;
   pp.transpose = a->direction == FJX_INCOMING;
+  pp.cw = cw;
   int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] { launch_trimul_prologue<T>(pp, a->batch, st); });
   if (rc) return rc;
 
@@ -286,6 +289,7 @@ int trimul_run(const fjx_trimul_args* a, hipStream_t st) {
   ep.out = static_cast<T*>(a->out);
   ep.n = a->n;
   ep.eps = a->eps;
+  ep.cw = cw;
   return timed(K_TRIMUL_EPILOGUE, st, "trimul_epilogue", [&] { launch_trimul_epilogue<T>(ep, a->batch, st); });
 }
 
@@ -297,7 +301,8 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   const TriAttnWs ws = triattn_ws(a->batch, n, n, a->heads, a->dtype, true);
   void* W = a->workspace;
 
-  TriAttnPrologueParams<T> pp;
+  const int cw = a->c_z < 128 ? (int)a->c_z : 0;
+  TriAttnPrologueParams<T> pp = {};
   pp.x = static_cast<const T*>(a->x);
   pp.mask = static_cast<const T*>(a->mask);
   pp.ln_w = static_cast<const T*>(a->norm_weight);
@@ -318,6 +323,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   pp.inf = a->inf;
   pp.q_scale = (1.0f / sqrtf((float)a->head_dim)) * kLog2e;
   pp.transpose = a->starting ? 0 : 1;
+  pp.cw = cw;
   int rc = timed(K_TRIATTN_PROLOGUE, st, "triattn_prologue", [&] { launch_triattn_prologue<T>(pp, a->batch, st); });
   if (rc) return rc;
 
@@ -342,7 +348,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });
   if (rc) return rc;
 
-  TriAttnEpilogueParams<T> ep;
+  TriAttnEpilogueParams<T> ep = {};
   ep.o = fp.out;
   ep.x = pp.x;
   ep.ln_w = pp.ln_w;
@@ -355,6 +361,7 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   ep.n = n;
   ep.eps = a->eps;
   ep.transpose = pp.transpose;
+  ep.cw = cw;
   return timed(K_TRIATTN_EPILOGUE, st, "triattn_epilogue", [&] { launch_triattn_epilogue<T>(ep, a->batch, st); });
 }
 
@@ -422,6 +429,7 @@ int transition_run(const fjx_transition_args* a, bool pb_fused, hipStream_t st) 
   p.out = static_cast<T*>(a->out);
   p.rows = a->rows;
   p.eps = a->eps;
+  p.cw = a->c < 128 ? (int)a->c : 0;
   const bool pb_f32 = pb_fused && a->pb_f32 && std::is_same<T, bf16>::value;
   if (pb_fused) {
     if (pb_f32) {
@@ -471,14 +479,18 @@ int transition_pair_bias_pass(const fjx_transition_args* a, hipStream_t st) {
 }
 
 // ------------------------------------------------- general-width paths
-// Widths the fused kernels are not built for (the Protenix template stack's
-// c_z = 64, wider tracks): row LayerNorms, GEMMs and layout passes around
-// the same contraction and flash kernels (fjx_generic.hip).
-bool fused_trimul(int64_t c_z, int64_t c_h) { return c_z == 128 && c_h == 128; }
+// Widths the fused kernels are not built for (wider tracks such as 384,
+// hidden widths other than 128): row LayerNorms, GEMMs and layout passes
+// around the same contraction and flash kernels (fjx_generic.hip).
+// The fused kernels also take a narrow pair width c_z of 32, 64 or 96 (the
+// Protenix template stack's 64 among them), with the channels past c_z held
+// at zero.
+bool fused_width(int64_t c) { return c == 128 || (c >= 32 && c < 128 && c % 32 == 0); }
+bool fused_trimul(int64_t c_z, int64_t c_h) { return fused_width(c_z) && c_h == 128; }
 bool fused_triattn(int64_t c_z, int64_t heads, int64_t head_dim) {
-  return c_z == 128 && head_dim == 32 && heads * head_dim == 128;
+  return fused_width(c_z) && head_dim == 32 && heads * head_dim == 128;
 }
-bool fused_transition(int64_t c, int64_t hidden) { return c == 128 && hidden == 4 * c; }
+bool fused_transition(int64_t c, int64_t hidden) { return fused_width(c) && hidden == 4 * c; }
 int64_t transition_hidden(const fjx_transition_args* a) { return a->hidden > 0 ? a->hidden : 4 * a->c; }
 
 template <typename T>
@@ -1004,7 +1016,7 @@ int fjx_transition_fwd(const fjx_transition_args* a, hipStream_t st) {
   int rc;
   bool pb_fused = false;
   if (fused_transition(a->c, hid)) {
-    pb_fused = a->pb_out && a->pb_heads <= 16;
+    pb_fused = a->pb_out && a->pb_heads <= 16 && a->c == 128;
     rc = bf ? transition_run<bf16>(a, pb_fused, st) : transition_run<float>(a, pb_fused, st);
   } else {
     const size_t need = fjx_transition_workspace_size(a->rows, a->c, hid, a->dtype);

@@ -20,6 +20,7 @@ struct TriMulPrologueParams {
   int64_t n;
   float eps;
   int transpose;    // 1 for the incoming direction
+  int cw;           // channels of x (and rows of w_p/w_g) when below 128 (a multiple of 32); 0: 128
 };
 
 template <typename T>
@@ -44,6 +45,7 @@ struct TriAttnPrologueParams {
   float inf;
   float q_scale;    // head_dim^-0.5 * log2(e)
   int transpose;    // 1 for the ending node
+  int cw;           // channels of x (the k of every weight) when below 128 (a multiple of 32); 0: 128
 };
 
 template <typename T>
@@ -65,6 +67,7 @@ struct TriMulEpilogueParams {
   // consecutive positions in one 64 KB block (the LDS-DMA contraction's
   // blocked output)
   bool o_blocked;
+  int cw;             // channels of x / out (k of w_gout, rows of both weights) when below 128; 0: 128
 };
 
 template <typename T>
@@ -81,6 +84,7 @@ struct TriAttnEpilogueParams {
   int64_t n;
   float eps;
   int transpose;      // 1 for the ending node
+  int cw;             // channels of x / out (k of w_g, rows of w_o) when below 128; 0: 128
 };
 
 template <typename T, typename TO>
@@ -133,6 +137,9 @@ struct TransitionParams {
   const float* pbf_ln_b;
   const float* pbf_w;  // [pb_heads][C]
   float* pbf_out;
+  // channels of x / out when below 128 (a multiple of 32, hidden 4 cw): the
+  // narrow form of the kernel; 0 or 128: the full form
+  int cw;
 };
 
 template <typename T>

@@ -54,8 +54,10 @@ namespace {
 //   a_cm/b_cm: [B][128][N*N] channel-major in the virtual grid (contraction
 //   operands with the contracted axis contiguous), each
 //   mask * sigmoid(x_ln g_in^T) * (x_ln p_in^T).
+// kNarrow: x has P.cw < 128 channels (a multiple of 32); the tile's channels
+// past cw are held at zero (zero LayerNorm affine, zero weight columns).
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool kNarrow>
 __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulPrologueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
   __shared__ __attribute__((aligned(16))) float mrow[kTP];
@@ -72,11 +74,18 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
   const int p = t >> 2;  // LayerNorm position of this thread
   const bool vec4 = (n % 4) == 0;
   const bool vec8 = (n % 8) == 0;
+  const int cw = kNarrow ? P.cw : kC;
 
   WSlab<T> wp, wg;
-  load_wslab<T>(P.w_p + (int64_t)half * kC * kC, col0, wp);
-  load_wslab<T>(P.w_g + (int64_t)half * kC * kC, col0, wg);
-  stage_ln<T>(P.ln_w, P.ln_b, ln);
+  if constexpr (kNarrow) {
+    load_wslab_w<T>(P.w_p + (int64_t)half * kC * cw, cw, col0, wp, kC, cw);
+    load_wslab_w<T>(P.w_g + (int64_t)half * kC * cw, cw, col0, wg, kC, cw);
+    stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
+  } else {
+    load_wslab<T>(P.w_p + (int64_t)half * kC * kC, col0, wp);
+    load_wslab<T>(P.w_g + (int64_t)half * kC * kC, col0, wg);
+    stage_ln<T>(P.ln_w, P.ln_b, ln);
+  }
 
   // the fetched position's mask value stays raw until it is used: a
   // conversion in the fetch would wait there for every load in flight,
@@ -91,7 +100,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     auto pos_of = [&](int ss) {
       return (int64_t)tl.b * nn + (P.transpose ? (int64_t)ss * n + tl.r : (int64_t)tl.r * n + ss);
     };
-    load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
+    if constexpr (kNarrow) load_row_part_w<T>(valid ? P.x + pos_of(s) * cw : nullptr, xr, cw);
+    else load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
     mvalid = valid;
     if (P.mask) mraw = P.mask[pos_of(valid ? s : tl.s0)];
   };
@@ -102,7 +112,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
   for (; tile < ntiles; tile += gridDim.x) {
     const TileRS tl = tile_at(tile, ntx, n);
     const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
-    ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+    ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
     if ((t & 3) == 0) mrow[p] = mvalid ? (P.mask ? to_f32(mraw) : 1.0f) : 0.f;
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
@@ -143,8 +153,9 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
 //   bias [B][H][Np][Np]  x_ln w_bias^T times log2 e (in T)
 //   mb [B][N][Np] fp32   inf*(mask-1)*log2 e, -inf for keys >= N
 // Np = N rounded up to 64; key slots in [N, Np) are written as zeros.
+// kNarrow: x has P.cw < 128 channels, as for the tri-mul prologue.
 // ---------------------------------------------------------------------------
-template <typename T>
+template <typename T, bool kNarrow>
 __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnPrologueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
   __shared__ __attribute__((aligned(16))) LnAffine ln;
@@ -161,6 +172,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   const int role = wave >> 2;  // 0: q and k; 1: v and bias
   const int col0 = 32 * (wave & 3);
   const int p = t >> 2;
+  const int cw = kNarrow ? P.cw : kC;
 
   // role 0: w1 = q slab, w2 = k slab of head (wave & 3)
   // role 1: w1 = v slab; w2[ks][0] = bias weights as one 16-column tile
@@ -168,19 +180,27 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   WSlab<T> w1, w2;
   if (role == 0) {
     // paired: lane group g holds head dims 8g .. +7, a quarter of a q/k row
-    load_wslab_paired<T>(P.w_q, col0, w1);
-    load_wslab_paired<T>(P.w_k, col0, w2);
+    if constexpr (kNarrow) {
+      load_wslab_paired_w<T>(P.w_q, cw, col0, w1, kC, cw);
+      load_wslab_paired_w<T>(P.w_k, cw, col0, w2, kC, cw);
+    } else {
+      load_wslab_paired<T>(P.w_q, col0, w1);
+      load_wslab_paired<T>(P.w_k, col0, w2);
+    }
   } else {
-    load_wslab<T>(P.w_v, col0, w1);
+    if constexpr (kNarrow) load_wslab_w<T>(P.w_v, cw, col0, w1, kC, cw);
+    else load_wslab<T>(P.w_v, col0, w1);
     const int li = lane & 15;
     const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      w2[ks][0] = li < H ? load8(P.w_bias + li * kC + 32 * ks + 8 * (lane >> 4)) : pack8<T>(z);
+      const int k = 32 * ks + 8 * (lane >> 4);
+      w2[ks][0] = li < H && k < cw ? load8(P.w_bias + li * cw + k) : pack8<T>(z);
       w2[ks][1] = pack8<T>(z);
     }
   }
-  stage_ln<T>(P.ln_w, P.ln_b, ln);
+  if constexpr (kNarrow) stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
+  else stage_ln<T>(P.ln_w, P.ln_b, ln);
 
   // the mask value stays raw until it is used (as in the tri-mul prologue)
   RowPart<T> xr;
@@ -193,7 +213,8 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
     auto pos_of = [&](int ss) {
       return (int64_t)tl.b * nn + (P.transpose ? (int64_t)ss * n + tl.r : (int64_t)tl.r * n + ss);
     };
-    load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
+    if constexpr (kNarrow) load_row_part_w<T>(valid ? P.x + pos_of(s) * cw : nullptr, xr, cw);
+    else load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
     mvalid = valid;
     if (P.mask) mraw = P.mask[pos_of(valid ? s : tl.s0)];
   };
@@ -205,7 +226,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
     const TileRS tl = tile_at(tile, ntx, n);
     const int nstore = (int)min<int64_t>(kTP, np - tl.s0);  // incl. zero padding; a multiple of 64
     const int nreal = (int)max<int64_t>(0, min<int64_t>(kTP, n - tl.s0));
-    ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+    ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
     if ((t & 3) == 0 && p < nstore) {
       const float mv = P.mask ? to_f32(mraw) : 1.0f;
       P.mb[((int64_t)tl.b * n + tl.r) * np + tl.s0 + p] = mvalid ? P.inf * (mv - 1.0f) * kLog2e : -INFINITY;
@@ -314,8 +335,11 @@ constexpr int kTE = 64;
 // LDS). A compile-time choice: one pointer that may address LDS or global
 // memory compiles to a generic load, which waits for every global access in
 // flight -- the previous row tile's store and the next tile's prefetch.
+// kNarrow: x, the residual and out have P.cw < 128 channels (a multiple of
+// 32); o keeps 128. The waves whose output channels start at or past cw
+// only help fill the LDS tiles.
 // ---------------------------------------------------------------------------
-template <typename T, bool kResX>
+template <typename T, bool kResX, bool kNarrow>
 __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpilogueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xg[kTE][kLd];    // LN_in(x)
   __shared__ __attribute__((aligned(16))) T xp[kTE][kLd];    // LN_out(o)
@@ -332,11 +356,19 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
   const int p = t >> 2;  // LayerNorm position of this thread
   constexpr bool res_x = kResX;
   const bool vec8 = (n % 8) == 0;
+  const int cw = kNarrow ? P.cw : kC;
+  const bool active = !kNarrow || col0 < cw;
 
   WSlab<T> wg, wp;
-  load_wslab_paired<T>(P.w_gout, col0, wg);
-  load_wslab_paired<T>(P.w_pout, col0, wp);
-  stage_ln<T>(P.ln_in_w, P.ln_in_b, ln_in);
+  if constexpr (kNarrow) {
+    load_wslab_paired_w<T>(P.w_gout, cw, col0, wg, cw, cw);
+    load_wslab_paired_w<T>(P.w_pout, kC, col0, wp, cw, kC);
+    stage_ln_w<T>(P.ln_in_w, P.ln_in_b, ln_in, cw);
+  } else {
+    load_wslab_paired<T>(P.w_gout, col0, wg);
+    load_wslab_paired<T>(P.w_pout, col0, wp);
+    stage_ln<T>(P.ln_in_w, P.ln_in_b, ln_in);
+  }
   stage_ln<T>(P.ln_out_w, P.ln_out_b, ln_out);
 
   // per-tile inputs: the x row of position t/4 and 4 chunks of the
@@ -355,7 +387,8 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
-    load_row_part<T>(p < nvalid ? P.x + (pos0 + p) * kC : nullptr, xr);
+    if constexpr (kNarrow) load_row_part_w<T>(p < nvalid ? P.x + (pos0 + p) * cw : nullptr, xr, cw);
+    else load_row_part<T>(p < nvalid ? P.x + (pos0 + p) * kC : nullptr, xr);
     // channel-major: channel ch of the tile at src + ch * nn; tile-blocked:
     // the whole tile is one contiguous [128][64] block
     const int64_t cstride = P.o_blocked ? 256 : nn;
@@ -396,7 +429,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 #pragma unroll
       for (int rt = 0; rt < kTE / 16; ++rt) keep |= to_f32(om[rt]) != 0.f ? 1u << rt : 0u;
     }
-    ln_quad<T>(xr, ln_in, P.eps, &xg[p][0]);
+    ln_quad<T>(xr, ln_in, P.eps, &xg[p][0], cw);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       int ch, p0;
@@ -415,7 +448,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
 #pragma unroll 2
-    for (int rt = 0; rt < kTE / 16; ++rt) {
+    for (int rt = 0; rt < (active ? kTE / 16 : 0); ++rt) {
       f32x4 ag[2], ap[2];
       tile_mma<T, true>(xg, rt, wg, ag);
       tile_mma<T, true>(xp, rt, wp, ap);
@@ -423,7 +456,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
       const int pp = 16 * rt + (lane & 15);
       if (pp < nvalid) {
         const int c = col0 + 8 * (lane >> 4);
-        const int64_t off = (pos0 + pp) * kC + c;
+        const int64_t off = (pos0 + pp) * cw + c;
         float y[8];
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
@@ -453,10 +486,10 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 //   out[orig] = T(o[r,s] * sigmoid(LN(x[orig]) w_g^T)) w_o^T (+ residual[orig])
 // with o position-major [B][N*N][128] and orig = (r, s) or (s, r). 256
 // threads: wave w owns output channels 32w .. 32w+31 of both products for the
-// 64 positions, holding the w_g and w_o slabs. kResX as for the tri-mul
-// epilogue.
+// 64 positions, holding the w_g and w_o slabs. kResX and kNarrow as for the
+// tri-mul epilogue (o and the gate keep 128 channels).
 // ---------------------------------------------------------------------------
-template <typename T, bool kResX>
+template <typename T, bool kResX, bool kNarrow>
 __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpilogueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTE][kLd];    // LN(x)
   __shared__ __attribute__((aligned(16))) T xo[kTE][kLd];    // gated o
@@ -474,13 +507,21 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
   const bool gated = P.w_g != nullptr;
   constexpr bool res_x = kResX;
   const bool need_x = gated || res_x;
+  const int cw = kNarrow ? P.cw : kC;
+  const bool active = !kNarrow || col0 < cw;
 
   // paired slabs: lane group g works on the 8 consecutive channels
   // col0 + 8g .. +7, so o, the residual and the output move 16 bytes a lane
   WSlab<T> wg, wo;
-  if (gated) load_wslab_paired<T>(P.w_g, col0, wg);
-  load_wslab_paired<T>(P.w_o, col0, wo);
-  if (gated) stage_ln<T>(P.ln_w, P.ln_b, ln);
+  if constexpr (kNarrow) {
+    if (gated) load_wslab_paired_w<T>(P.w_g, cw, col0, wg, kC, cw);
+    load_wslab_paired_w<T>(P.w_o, kC, col0, wo, cw, kC);
+    if (gated) stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
+  } else {
+    if (gated) load_wslab_paired<T>(P.w_g, col0, wg);
+    load_wslab_paired<T>(P.w_o, col0, wo);
+    if (gated) stage_ln<T>(P.ln_w, P.ln_b, ln);
+  }
 
   auto orig_of = [&](const TileRS& tl, int pp) -> int64_t {
     const int64_t s = tl.s0 + pp;
@@ -496,7 +537,11 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
   auto fetch = [&](int64_t tile) {
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
-    if (need_x) load_row_part<T>(p < nvalid ? P.x + orig_of(tl, p) * kC : nullptr, xr);
+    if constexpr (kNarrow) {
+      if (need_x) load_row_part_w<T>(p < nvalid ? P.x + orig_of(tl, p) * cw : nullptr, xr, cw);
+    } else {
+      if (need_x) load_row_part<T>(p < nvalid ? P.x + orig_of(tl, p) * kC : nullptr, xr);
+    }
     const T* osrc = P.o + ((int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0) * kC;
 #pragma unroll
     for (int rt = 0; rt < kTE / 16; ++rt) {
@@ -531,7 +576,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
       for (int rt = 0; rt < kTE / 16; ++rt) keep |= to_f32(om[rt]) != 0.f ? 1u << rt : 0u;
     }
     if (gated) {
-      ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+      ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
       __syncthreads();
 #pragma unroll
       for (int rt = 0; rt < kTE / 16; ++rt) {
@@ -551,13 +596,13 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
 #pragma unroll 2
-    for (int rt = 0; rt < kTE / 16; ++rt) {
+    for (int rt = 0; rt < (active ? kTE / 16 : 0); ++rt) {
       f32x4 acc[2];
       tile_mma<T, true>(xo, rt, wo, acc);
       const int pp = 16 * rt + (lane & 15);
       if (pp < nvalid) {
         const int c = col0 + 8 * (lane >> 4);
-        const int64_t off = orig_of(tl, pp) * kC + c;
+        const int64_t off = orig_of(tl, pp) * cw + c;
         float y[8];
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
@@ -585,43 +630,38 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
 // ---------------------------------------------------------------------------
 // host-side launchers
 // ---------------------------------------------------------------------------
+// a persistent launch of one kernel instance over ntiles tiles
+template <typename P>
+void launch_persistent(void (*kern)(P, int64_t), const P& p, int threads, int64_t ntiles, hipStream_t st) {
+  const void* k = reinterpret_cast<const void*>(kern);
+  hipLaunchKernelGGL(kern, dim3(persistent_grid(k, threads, ntiles)), dim3(threads), 0, st, p, ntiles);
+}
+
 template <typename T>
 void launch_trimul_prologue(const TriMulPrologueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
-  const void* k = reinterpret_cast<const void*>(&trimul_prologue_kernel<T>);
-  hipLaunchKernelGGL(trimul_prologue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
+  launch_persistent(p.cw ? trimul_prologue_kernel<T, true> : trimul_prologue_kernel<T, false>, p, 512, ntiles, st);
 }
 template <typename T>
 void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.np + kTP - 1) / kTP * p.n * batch;
-  const void* k = reinterpret_cast<const void*>(&triattn_prologue_kernel<T>);
-  hipLaunchKernelGGL(triattn_prologue_kernel<T>, dim3(persistent_grid(k, 512, ntiles)), dim3(512), 0, st, p, ntiles);
+  launch_persistent(p.cw ? triattn_prologue_kernel<T, true> : triattn_prologue_kernel<T, false>, p, 512, ntiles, st);
 }
 template <typename T>
 void launch_trimul_epilogue(const TriMulEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
-  if (p.residual && p.residual == p.x) {
-    const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T, true>);
-    hipLaunchKernelGGL((trimul_epilogue_kernel<T, true>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
-                       ntiles);
-  } else {
-    const void* k = reinterpret_cast<const void*>(&trimul_epilogue_kernel<T, false>);
-    hipLaunchKernelGGL((trimul_epilogue_kernel<T, false>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
-                       ntiles);
-  }
+  const bool res_x = p.residual && p.residual == p.x;
+  auto kern = res_x ? (p.cw ? trimul_epilogue_kernel<T, true, true> : trimul_epilogue_kernel<T, true, false>)
+                    : (p.cw ? trimul_epilogue_kernel<T, false, true> : trimul_epilogue_kernel<T, false, false>);
+  launch_persistent(kern, p, 256, ntiles, st);
 }
 template <typename T>
 void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
-  if (p.residual && p.residual == p.x) {
-    const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T, true>);
-    hipLaunchKernelGGL((triattn_epilogue_kernel<T, true>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
-                       ntiles);
-  } else {
-    const void* k = reinterpret_cast<const void*>(&triattn_epilogue_kernel<T, false>);
-    hipLaunchKernelGGL((triattn_epilogue_kernel<T, false>), dim3(persistent_grid(k, 256, ntiles)), dim3(256), 0, st, p,
-                       ntiles);
-  }
+  const bool res_x = p.residual && p.residual == p.x;
+  auto kern = res_x ? (p.cw ? triattn_epilogue_kernel<T, true, true> : triattn_epilogue_kernel<T, true, false>)
+                    : (p.cw ? triattn_epilogue_kernel<T, false, true> : triattn_epilogue_kernel<T, false, false>);
+  launch_persistent(kern, p, 256, ntiles, st);
 }
 
 #define FJX_INST(T)                                                                                 \

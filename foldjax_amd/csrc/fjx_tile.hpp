@@ -30,6 +30,16 @@ __device__ __forceinline__ void stage_ln(const T* __restrict__ ln_w, const T* __
   if (t < kC) l.w[t] = to_f32(ln_w[t]);
   else if (t < 2 * kC) l.b[t - kC] = to_f32(ln_b[t - kC]);
 }
+// A narrow width cw < 128 (a multiple of 32) runs the 128-channel kernels
+// with the channels past cw held at zero: the affine is zero there, so the
+// LayerNorm writes zeros into them and they add nothing to any product.
+template <typename T>
+__device__ __forceinline__ void stage_ln_w(const T* __restrict__ ln_w, const T* __restrict__ ln_b, LnAffine& l,
+                                           int cw) {
+  const int t = threadIdx.x;
+  if (t < kC) l.w[t] = t < cw ? to_f32(ln_w[t]) : 0.f;
+  else if (t < 2 * kC) l.b[t - kC] = t - kC < cw ? to_f32(ln_b[t - kC]) : 0.f;
+}
 
 // The 32 channels [32*part, +32) of one pair-tensor row (part = threadIdx.x % 4),
 // raw, or zeros when src is null (a position outside the grid)
@@ -53,6 +63,14 @@ __device__ __forceinline__ void load_row_part(const T* __restrict__ src, RowPart
     for (int q = 0; q < 4; ++q) r.f[q] = pack8<T>(z);
   }
 }
+// the same for a row of cw channels (a multiple of 32): the chunks past cw
+// are zero
+template <typename T>
+__device__ __forceinline__ void load_row_part_w(const T* __restrict__ src, RowPart<T>& r, int cw) {
+  const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) r.f[q] = src && 32 * q < cw ? load8(src + row_chunk(q)) : pack8<T>(z);
+}
 template <typename T>
 __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restrict__ dst_row) {
 #pragma unroll
@@ -60,9 +78,11 @@ __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restric
 }
 
 // LayerNorm of 128 channels held by 4 consecutive threads (the chunks of
-// load_row_part); put(c, o) receives the 8 outputs of channels c .. c+7
+// load_row_part); put(c, o) receives the 8 outputs of channels c .. c+7.
+// cw < 128: the statistics are those of the first cw channels (the chunks
+// past cw hold zeros and are left out of the variance)
 template <typename T, typename Put>
-__device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine& l, float eps, Put put) {
+__device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine& l, float eps, Put put, int cw = kC) {
   float v[32];
 #pragma unroll
   for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
@@ -71,16 +91,17 @@ __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine&
   for (int e = 0; e < 32; ++e) s += v[e];
   s += shfl_xor(s, 1);
   s += shfl_xor(s, 2);
-  const float mean = s * (1.0f / kC);
+  const float inv_c = cw == kC ? 1.0f / kC : 1.0f / (float)cw;
+  const float mean = s * inv_c;
   float q2 = 0.f;
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
     const float d = v[e] - mean;
-    q2 += d * d;
+    if (cw == kC || 32 * (e / 8) < cw) q2 += d * d;
   }
   q2 += shfl_xor(q2, 1);
   q2 += shfl_xor(q2, 2);
-  const float rstd = __builtin_amdgcn_rsqf(q2 * (1.0f / kC) + eps);
+  const float rstd = __builtin_amdgcn_rsqf(q2 * inv_c + eps);
   const float shift = -mean * rstd;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -104,8 +125,9 @@ __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine&
 
 // ... written to the same channels of dst_row as TO
 template <typename T, typename TO>
-__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row) {
-  ln_quad_put(r, l, eps, [&](int c, const float* o) { store8(dst_row + c, pack8<TO>(o)); });
+__device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row,
+                                        int cw = kC) {
+  ln_quad_put(r, l, eps, [&](int c, const float* o) { store8(dst_row + c, pack8<TO>(o)); }, cw);
 }
 
 // One wave's 32 output channels col0..col0+31 of a [128][128] weight as MFMA
@@ -136,6 +158,36 @@ __device__ __forceinline__ void load_wslab_paired(const T* __restrict__ w, int c
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
       wf[ks][ct] = load8(w + (int64_t)(col0 + 8 * (li >> 2) + 4 * ct + (li & 3)) * kC + 32 * ks + 8 * (lane >> 4));
+}
+
+// the same two loaders for a weight with rows ld elements apart, rows >=
+// nrows and columns >= kmax read as zero (a narrow width's padding)
+template <typename T>
+__device__ __forceinline__ void load_wslab_w(const T* __restrict__ w, int64_t ld, int col0, WSlab<T>& wf, int nrows,
+                                             int kmax) {
+  const int lane = threadIdx.x & 63;
+  const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int row = col0 + 16 * ct + (lane & 15), k = 32 * ks + 8 * (lane >> 4);
+      wf[ks][ct] = row < nrows && k < kmax ? load8(w + (int64_t)row * ld + k) : pack8<T>(z);
+    }
+}
+template <typename T>
+__device__ __forceinline__ void load_wslab_paired_w(const T* __restrict__ w, int64_t ld, int col0, WSlab<T>& wf,
+                                                    int nrows, int kmax) {
+  const int lane = threadIdx.x & 63;
+  const int li = lane & 15;
+  const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int row = col0 + 8 * (li >> 2) + 4 * ct + (li & 3), k = 32 * ks + 8 * (lane >> 4);
+      wf[ks][ct] = row < nrows && k < kmax ? load8(w + (int64_t)row * ld + k) : pack8<T>(z);
+    }
 }
 
 // One 16-row tile against one slab, K = 128; `row` is the tile row this lane
@@ -245,6 +297,20 @@ __device__ __forceinline__ void load_wcol(const T* __restrict__ w, int64_t ldw, 
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) wf[ks] = load8(w + (int64_t)(row0 + (lane & 15)) * ldw + k0 + 32 * ks + 8 * (lane >> 4));
+}
+
+// the same with rows >= nrows and columns k >= kmax (multiples of 8) read as zero
+template <typename T>
+__device__ __forceinline__ void load_wcol_w(const T* __restrict__ w, int64_t ldw, int row0, int64_t k0, WCol<T>& wf,
+                                            int nrows, int64_t kmax) {
+  const int lane = threadIdx.x & 63;
+  const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int row = row0 + (lane & 15);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const int64_t k = k0 + 32 * ks + 8 * (lane >> 4);
+    wf[ks] = row < nrows && k < kmax ? load8(w + (int64_t)row * ldw + k) : pack8<T>(z);
+  }
 }
 
 // acc += rows 16rt.. of the tile against one 16-column tile, transposed form:

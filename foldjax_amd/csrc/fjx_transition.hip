@@ -177,7 +177,11 @@ __device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, 
 // ---------------------------------------------------------------------------
 // kPbF32: the fp32 pair-bias epilogue of a bf16 transition (a kernel of its
 // own, so the other paths compile exactly as without it)
-template <typename T, bool kPbF32>
+// kNarrow: x and out have cw = P.cw < 128 channels (a multiple of 32) and
+// the hidden width is 4 cw; the tile works at 128 channels with the ones past
+// cw at zero (zero affine, zero weight rows and columns), in cw / 32 hidden
+// chunks, and stores only the first cw channels
+template <typename T, bool kPbF32, bool kNarrow = false>
 __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P) {
   using namespace tile;
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];  // LN(x)
@@ -194,18 +198,25 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   const int lane = t & 63;
   const int p = t >> 2;
   const int col = 16 * wave;
+  const int cw = kNarrow ? P.cw : kC;  // channels of x and out
+  const int nch = kNarrow ? cw / 32 : 4;  // 128-wide hidden chunks (hidden = 4 cw)
 
   {
     RowPart<T> xr;
-    load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
-    stage_ln<T>(P.ln_w, P.ln_b, ln);
-    if (P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
+    if constexpr (kNarrow) {
+      load_row_part_w<T>(p < nvalid ? P.x + (m0 + p) * cw : nullptr, xr, cw);
+      stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
+    } else {
+      load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
+      stage_ln<T>(P.ln_w, P.ln_b, ln);
+    }
+    if (!kNarrow && P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
     if constexpr (kPbF32) {
       stage_ln<float>(P.pbf_ln_w, P.pbf_ln_b, pb_ln);
       stage_wz_split(P, wz);
     }
     __syncthreads();
-    ln_quad<T>(xr, ln, P.eps, &xs[p][0]);
+    ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
   }
   __syncthreads();
 
@@ -214,11 +225,17 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   for (int rt = 0; rt < 8; ++rt) out[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll 1
-  for (int ch = 0; ch < 4; ++ch) {
+  for (int ch = 0; ch < nch; ++ch) {
     WCol<T> wa, wb, wo;
-    load_wcol<T>(P.w_a, kC, ch * kC + col, 0, wa);
-    load_wcol<T>(P.w_b, kC, ch * kC + col, 0, wb);
-    load_wcol<T>(P.w_o, 4 * kC, col, ch * kC, wo);
+    if constexpr (kNarrow) {
+      load_wcol_w<T>(P.w_a, cw, ch * kC + col, 0, wa, 4 * cw, cw);
+      load_wcol_w<T>(P.w_b, cw, ch * kC + col, 0, wb, 4 * cw, cw);
+      load_wcol_w<T>(P.w_o, 4 * cw, col, ch * kC, wo, cw, 4 * cw);
+    } else {
+      load_wcol<T>(P.w_a, kC, ch * kC + col, 0, wa);
+      load_wcol<T>(P.w_b, kC, ch * kC + col, 0, wb);
+      load_wcol<T>(P.w_o, 4 * kC, col, ch * kC, wo);
+    }
 #pragma unroll 2
     for (int rt = 0; rt < 8; ++rt) {
       f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -238,7 +255,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   // the pair-bias weight (rows = heads, zero past pb_heads) is fetched ahead
   // of the output stores so that its latency is not exposed after them
   WCol<T> pb_wf;
-  if (!kPbF32 && P.pb_out) {
+  if (!kPbF32 && !kNarrow && P.pb_out) {
     const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     const int h = lane & 15;
 #pragma unroll
@@ -257,11 +274,13 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
 #pragma unroll
     for (int q = 0; q < 4; ++q) res[rt][q] = 0.f;
   }
+  // a narrow form's waves past cw hold only zero channels: nothing to store
+  if (kNarrow && col >= cw) return;
   if (P.residual) {
 #pragma unroll
     for (int rt = 0; rt < 8; ++rt) {
       const int row = min(16 * rt + (lane & 15), nvalid - 1);
-      load4f(P.residual + (m0 + row) * kC + col + 4 * (lane >> 4), res[rt]);
+      load4f(P.residual + (m0 + row) * cw + col + 4 * (lane >> 4), res[rt]);
     }
   }
   if (P.row_mask) {
@@ -283,7 +302,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   for (int rt = 0; rt < 8; ++rt) {
     const int row = 16 * rt + (lane & 15);
     if (row < nvalid) {
-      const int64_t off = (m0 + row) * kC + col + 4 * (lane >> 4);
+      const int64_t off = (m0 + row) * cw + col + 4 * (lane >> 4);
       float y[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) y[q] = round_to<T>(out[rt][q] * msk[rt]);
@@ -294,12 +313,12 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
 #pragma unroll
       for (int q = 0; q < 4; ++q) y[q] *= gate[rt];
       store4f(P.out + off, y);
-      if (kPbF32 || P.pb_out) store4f(&xs[row][col + 4 * (lane >> 4)], y);  // xs is free after the last chunk
+      if (kPbF32 || (!kNarrow && P.pb_out)) store4f(&xs[row][col + 4 * (lane >> 4)], y);  // xs is free after the last chunk
     }
   }
   if constexpr (kPbF32) {
     pair_bias_epilogue_f32(P, xs, hs, pb_ln, wz, m0, nvalid);
-  } else {
+  } else if constexpr (!kNarrow) {
     if (P.pb_out) pair_bias_epilogue<T>(P, xs, pb_ln, pb_wf, m0, nvalid);
   }
 }
@@ -308,6 +327,10 @@ template <typename T>
 __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> P) {
   transition128_body<T, false>(P);
 }
+template <typename T>
+__global__ __launch_bounds__(512) void transition_narrow_kernel(TransitionParams<T> P) {
+  transition128_body<T, false, true>(P);
+}
 // two 512-thread workgroups (70 KB of LDS each) share a CU only at 4 waves
 // per SIMD, so this variant is held to 128 VGPRs as the plain one fits
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4)))
@@ -315,13 +338,17 @@ void transition128_pbf32_kernel(TransitionParams<bf16> P) {
   transition128_body<bf16, true>(P);
 }
 
-// C = 128 only; other widths take the general path of the C ABI layer (row
-// LayerNorm and three GEMMs), which also measured faster than a fused kernel
-// for the single track's C = 384 at every row count tried (1 K to 1 M rows).
+// C = 128, or a narrow C (32, 64, 96: p.cw) with a 4C hidden width; other
+// widths take the general path of the C ABI layer (row LayerNorm and three
+// GEMMs), which also measured faster than a fused kernel for the single
+// track's C = 384 at every row count tried (1 K to 1 M rows).
 template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st) {
-  (void)c;
   const dim3 grid((unsigned)((p.rows + tile::kTP - 1) / tile::kTP));
+  if (c < tile::kC) {
+    hipLaunchKernelGGL(transition_narrow_kernel<T>, grid, dim3(512), 0, st, p);
+    return;
+  }
   if constexpr (std::is_same<T, bf16>::value) {
     if (p.pbf_out) {
       hipLaunchKernelGGL(transition128_pbf32_kernel, grid, dim3(512), 0, st, p);

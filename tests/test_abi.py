@@ -82,13 +82,20 @@ def test_workspace_sizes_are_host_only(lib):
     assert lib.fjx_trimul_workspace_size(0, 8, 128, 128, 0) == 0
     assert lib.fjx_triattn_workspace_size(1, 384, 128, 4, 32, _lib.FJX_DTYPE_BF16) > 0
     assert lib.fjx_triattn_core_workspace_size(1, 3, 4, 70, 32, _lib.FJX_DTYPE_F32) > 0
-    # the general-width paths (e.g. the template stack's c_z = 64) take their own, larger workspace
+    # the narrow fused forms (c_z 32, 64, 96 with c_h = 128: the template
+    # stack's 64) take the c = 128 workspace; the general-width paths (c_z
+    # not a multiple of 32, c_h != 128) their own, larger one
     fused = lib.fjx_trimul_workspace_size(1, 64, 128, 128, _lib.FJX_DTYPE_BF16)
-    assert lib.fjx_trimul_workspace_size(1, 64, 64, 128, _lib.FJX_DTYPE_BF16) > fused
-    assert lib.fjx_triattn_workspace_size(1, 64, 64, 4, 32, _lib.FJX_DTYPE_BF16) > 0
+    assert lib.fjx_trimul_workspace_size(1, 64, 64, 128, _lib.FJX_DTYPE_BF16) == fused
+    assert lib.fjx_trimul_workspace_size(1, 64, 48, 128, _lib.FJX_DTYPE_BF16) > fused
+    assert lib.fjx_trimul_workspace_size(1, 64, 64, 64, _lib.FJX_DTYPE_BF16) > 0
+    fused_a = lib.fjx_triattn_workspace_size(1, 64, 128, 4, 32, _lib.FJX_DTYPE_BF16)
+    assert lib.fjx_triattn_workspace_size(1, 64, 64, 4, 32, _lib.FJX_DTYPE_BF16) == fused_a
+    assert lib.fjx_triattn_workspace_size(1, 64, 64, 2, 32, _lib.FJX_DTYPE_BF16) > 0
     assert lib.fjx_transition_workspace_size(100, 128, 0, _lib.FJX_DTYPE_BF16) == 0  # fused: none
+    assert lib.fjx_transition_workspace_size(100, 64, 0, _lib.FJX_DTYPE_BF16) == 0  # narrow fused: none
     assert lib.fjx_transition_workspace_size(100, 384, 1536, _lib.FJX_DTYPE_BF16) > 0  # single track: general path
-    assert lib.fjx_transition_workspace_size(100, 64, 0, _lib.FJX_DTYPE_BF16) >= 100 * (64 + 256 + 64) * 2
+    assert lib.fjx_transition_workspace_size(100, 48, 0, _lib.FJX_DTYPE_BF16) >= 100 * (48 + 192 + 48) * 2
     # the prepared pair bias: [batch, heads, Np, Np], Np = n rounded up to 64
     assert lib.fjx_pair_bias_size(2, 1000, 16, _lib.FJX_DTYPE_BF16) == 2 * 16 * 1024 * 1024 * 2
     assert lib.fjx_pair_bias_size(1, 64, 4, _lib.FJX_DTYPE_F32) == 4 * 64 * 64 * 4

@@ -110,20 +110,21 @@ def test_single_attention_fp32_over_bf16_pair():
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
-@pytest.mark.parametrize("c", [128, 64])
-def test_out_mask_gates_every_pair_kernel(dt, c):
+@pytest.mark.parametrize("c,c_h,heads", [(128, 128, 4), (64, 128, 4), (64, 64, 2)])
+def test_out_mask_gates_every_pair_kernel(dt, c, c_h, heads):
     """``out_mask`` multiplies each written position by ``out_mask != 0``,
     residual included: the gated call equals the ungated one with the masked
-    positions zeroed, bit for bit (fused kernels at c=128, general-width
-    paths at c=64)."""
+    positions zeroed, bit for bit (fused kernels at c=128, their narrow forms
+    at c=64 with c_h=128 and 4 heads, the general-width paths at c_h=64 and
+    2 heads)."""
     dtype = DTYPES[dt]
     n = 33
-    say(f"out_mask pair kernels c={c} n={n} {dt}")
+    say(f"out_mask pair kernels c={c} c_h={c_h} heads={heads} n={n} {dt}")
     z = device_tensor(syn.pair_input(n, c, seed=70, batch=1), dtype)
     pm = device_tensor(_holey_pair_mask(n, 29), dtype)
     keep = (pm != 0)[..., None]
-    tm = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(c, c, seed=71)), dtype, "cuda")
-    ta = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(c, c // 32, 32, seed=72)), dtype, "cuda")
+    tm = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(c, c_h, seed=71)), dtype, "cuda")
+    ta = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(c, heads, 32, seed=72)), dtype, "cuda")
     tr = P.pack_transition_torch(P.transition_to_protenix(syn.transition_weights(c, seed=73)), dtype, "cuda")
     cases = [
         ("trimul out", lambda **k: kernels.trimul(z, pm, tm, "outgoing", residual=z, **k)),

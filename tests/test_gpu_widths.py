@@ -1,8 +1,12 @@
-"""GPU parity of the general-width paths, the shapes the fused kernels are not
-built for: the Protenix template stack (c_z = 64 with c_h = 128 for tri-mul,
-``PXT/triangle.py:131-137``; c_z = 64 tri-attn), a c = 384 track (OpenDDE's
-c_z = c_h = 384) and transitions of other widths and expansions, against the
-CPU oracle on the same values (fp32: max-abs <= 1e-4; bf16: relative <= 2e-2)."""
+"""GPU parity at pair widths other than 128, against the CPU oracle on the
+same values (fp32: max-abs <= 1e-4; bf16: relative <= 2e-2):
+
+- the narrow forms of the fused kernels, c_z in {32, 64, 96} with c_h = 128
+  (tri-mul), 4 heads of 32 (tri-attn) and a 4x transition -- the Protenix
+  template stack is c_z = 64 with c_h = 128 (``PXT/triangle.py:131-137``);
+- the general-width paths for every other shape: c_z = 48 (not a multiple of
+  32), c_h = 64 or 2 heads with c_z = 64, a c = 384 track (OpenDDE's
+  c_z = c_h = 384) and transitions of other widths and expansions."""
 
 from __future__ import annotations
 
@@ -24,6 +28,8 @@ DTYPES = {"fp32": torch.float32, "bf16": torch.bfloat16}
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 @pytest.mark.parametrize("direction", ["outgoing", "incoming"])
 @pytest.mark.parametrize("c_z,c_h,n,mask_kind", [(64, 128, 33, "tail"), (64, 128, 70, "random"),
+                                                 (32, 128, 40, "random"), (96, 128, 17, "row0"),
+                                                 (48, 128, 20, "random"), (64, 64, 24, "tail"),
                                                  (384, 384, 20, "random")])
 def test_trimul_widths(dt, direction, c_z, c_h, n, mask_kind):
     dtype = DTYPES[dt]
@@ -41,7 +47,8 @@ def test_trimul_widths(dt, direction, c_z, c_h, n, mask_kind):
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
 @pytest.mark.parametrize("starting", [True, False])
-@pytest.mark.parametrize("c_z,heads,n", [(64, 4, 33), (64, 2, 70), (384, 8, 20)])
+@pytest.mark.parametrize("c_z,heads,n", [(64, 4, 33), (32, 4, 40), (96, 4, 70), (64, 2, 70), (48, 4, 20),
+                                         (384, 8, 20)])
 def test_triattn_widths(dt, starting, c_z, heads, n):
     dtype = DTYPES[dt]
     say(f"triattn widths c_z={c_z} heads={heads} n={n} {dt} starting={starting}")
@@ -60,7 +67,8 @@ def test_triattn_widths(dt, starting, c_z, heads, n):
 
 
 @pytest.mark.parametrize("dt", ["fp32", "bf16"])
-@pytest.mark.parametrize("c,expansion,rows,masked", [(64, 4, 300, False), (64, 2, 77, True), (256, 4, 130, True)])
+@pytest.mark.parametrize("c,expansion,rows,masked", [(64, 4, 300, False), (32, 4, 100, True), (96, 4, 77, False),
+                                                     (64, 2, 77, True), (48, 4, 50, False), (256, 4, 130, True)])
 def test_transition_widths(dt, c, expansion, rows, masked):
     dtype = DTYPES[dt]
     say(f"transition widths c={c} x{expansion} rows={rows} {dt} masked={masked}")
@@ -79,8 +87,8 @@ def test_transition_widths(dt, c, expansion, rows, masked):
 
 def test_template_stack_pair_block_bf16():
     """One pair block at the template stack's widths (c_z = 64, c_h = 128,
-    4 heads of 32, transition x4) through the general paths, each residual
-    added by the kernels, against the oracle composition."""
+    4 heads of 32, transition x4) through the narrow fused kernels, each
+    residual added by the kernels, against the oracle composition."""
     dtype = DTYPES["bf16"]
     n, n_real, c_z = 40, 36, 64
     say(f"template pair block c_z={c_z} n={n} bf16")
@@ -127,3 +135,39 @@ def test_tiny_n_fused_and_general(c_z, c_h, n):
                                           num_heads=4, starting=starting)
         want = O.protenix_triangle_attention(prep(z, dtype), m, prep_tree(wa, dtype), num_heads=4, starting=starting)
         assert_parity(to_np(got), want, dtype, f"tiny triattn starting={starting}")
+
+
+@pytest.mark.parametrize("dt", ["fp32", "bf16"])
+@pytest.mark.parametrize("c_z", [64, 96])
+def test_narrow_separate_residual_and_out_mask(dt, c_z):
+    """The narrow kernels with a residual that is not x (the epilogues' global
+    residual read) and an output mask: out = (residual + update) * (mask != 0),
+    tri-mul both directions and tri-attn both nodes, against the oracle."""
+    dtype = DTYPES[dt]
+    n = 37
+    say(f"narrow residual/out_mask c_z={c_z} n={n} {dt}")
+    z = syn.pair_input(n, c_z, seed=31)
+    r = syn.pair_input(n, c_z, seed=32)
+    m = mask_case("random", n)
+    om = mask_case("tail", n)
+    wm = syn.trimul_weights(c_z, 128, seed=33)
+    wa = syn.triattn_weights(c_z, 4, 32, seed=34)
+    tm = P.pack_trimul_torch(P.trimul_to_protenix(wm), dtype, "cuda")
+    ta = P.pack_triattn_protenix(P.triattn_to_protenix(wa), dtype, "cuda")
+    zt, rt, mt, omt = (device_tensor(a, dtype) for a in (z, r, m, om))
+    zr, rr, mr = prep(z, dtype), prep(r, dtype), prep(m, dtype)
+    keep = (prep(om, dtype) != 0)[..., None]
+    for direction in ("outgoing", "incoming"):
+        got = kernels.trimul(zt, mt, tm, direction, residual=rt, out_mask=omt)
+        torch.cuda.synchronize()
+        want = (rr + O.protenix_triangle_multiplication(zr, mr, prep_tree(wm, dtype), direction)) * keep
+        assert_parity(to_np(got), want, dtype, f"narrow trimul {direction} residual")
+    for starting in (True, False):
+        got = kernels.triattn(zt, mt, ta, starting=starting, residual=rt, out_mask=omt)
+        torch.cuda.synchronize()
+        want = (rr + O.protenix_triangle_attention(zr, mr, prep_tree(wa, dtype), num_heads=4,
+                                                   starting=starting)) * keep
+        mv = m if starting else m.T
+        rows = mv.max(axis=1) > 0
+        g, w_ = (to_np(got)[rows], want[rows]) if starting else (to_np(got)[:, rows], want[:, rows])
+        assert_parity(g, w_, dtype, f"narrow triattn starting={starting} residual")
