@@ -142,11 +142,10 @@ __global__ void transpose_v_kernel(const T* __restrict__ src, T* __restrict__ ds
     dst[idx] = s < n ? src[(hr * n + s) * 32 + d] : from_f32<T>(0.f);
   }
 }
-// bias [B][H][n][n] -> [B][H][np][np] times log2 e, zeros outside; also
-// in fp32 into dstf when it is set
+// bias [B][H][n][n] -> [B][H][np][np] times log2 e, zeros outside
 template <typename T>
-__global__ void pad_bias_kernel(const T* __restrict__ src, T* __restrict__ dst, float* __restrict__ dstf, int64_t n,
-                                int64_t np, int64_t planes) {
+__global__ void pad_bias_kernel(const T* __restrict__ src, T* __restrict__ dst, int64_t n, int64_t np,
+                                int64_t planes) {
   const int64_t total = planes * np * np;
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
        idx += (int64_t)gridDim.x * blockDim.x) {
@@ -155,7 +154,6 @@ __global__ void pad_bias_kernel(const T* __restrict__ src, T* __restrict__ dst, 
     const int64_t pl = idx / (np * np);
     const float v = (q < n && k < n) ? to_f32(src[(pl * n + q) * n + k]) * kLog2e : 0.f;
     dst[idx] = from_f32<T>(v);
-    if (dstf) dstf[idx] = v;
   }
 }
 // mask bias [B][R][n] fp32 -> [B][R][np] times log2 e, -inf for padded keys
@@ -192,7 +190,7 @@ TriMulWs trimul_ws(int64_t batch, int64_t n, int32_t dtype) {
 }
 
 struct TriAttnWs {
-  size_t q, k, vt, bias, biasf, mb, o, flags, total;
+  size_t q, k, vt, bias, mb, o, flags, total;
 };
 // one flag per workgroup of the flash launch (4 rows x 64 or 128 queries)
 size_t flash_flags_bytes(int64_t batch, int64_t rows, int64_t heads, int64_t np) {
@@ -212,9 +210,6 @@ TriAttnWs triattn_ws(int64_t batch, int64_t rows, int64_t n, int64_t heads, int3
   off += qk;
   w.bias = off;
   off += align_up((size_t)batch * heads * np * np * es);
-  // bf16: the bias again in fp32, which the pipelined flash kernel stages by LDS DMA
-  w.biasf = off;
-  if (dtype == FJX_DTYPE_BF16) off += align_up((size_t)batch * heads * np * np * sizeof(float));
   w.mb = off;
   off += align_up((size_t)batch * rows * np * sizeof(float));
   w.o = off;
@@ -315,7 +310,6 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   pp.k = at<T>(W, ws.k);
   pp.vt = at<T>(W, ws.vt);
   pp.bias = at<T>(W, ws.bias);
-  pp.biasf = a->dtype == FJX_DTYPE_BF16 ? at<float>(W, ws.biasf) : nullptr;
   pp.mb = at<float>(W, ws.mb);
   pp.n = n;
   pp.np = np;
@@ -332,7 +326,6 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   fp.k = pp.k;
   fp.vt = pp.vt;
   fp.bias = pp.bias;
-  fp.biasf = pp.biasf;
   fp.mb = pp.mb;
   fp.out = at<T>(W, ws.o);
   fp.n = n;
@@ -376,7 +369,6 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   T* k = at<T>(W, ws.k);
   T* vt = at<T>(W, ws.vt);
   T* bias = at<T>(W, ws.bias);
-  float* biasf = a->dtype == FJX_DTYPE_BF16 ? at<float>(W, ws.biasf) : nullptr;
   float* mb = at<float>(W, ws.mb);
   int rc = timed(K_TRIATTN_CORE_PREP, st, "triattn_core_prep", [&] {
     hipLaunchKernelGGL(pad_qk_kernel<T>, grid_for(hr * np * 32), dim3(256), 0, st,
@@ -386,7 +378,7 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
     hipLaunchKernelGGL(transpose_v_kernel<T>, grid_for(hr * np * 32), dim3(256), 0, st,
                        static_cast<const T*>(a->v), vt, n, np, hr);
     hipLaunchKernelGGL(pad_bias_kernel<T>, grid_for(a->batch * a->heads * np * np), dim3(256), 0, st,
-                       static_cast<const T*>(a->tri_bias), bias, biasf, n, np, a->batch * a->heads);
+                       static_cast<const T*>(a->tri_bias), bias, n, np, a->batch * a->heads);
     hipLaunchKernelGGL(pad_mb_kernel, grid_for(a->batch * a->rows * np), dim3(256), 0, st, a->mask_bias, mb, n,
                        np, a->batch * a->rows);
   });
@@ -397,7 +389,6 @@ int core_run(const fjx_triattn_core_args* a, hipStream_t st) {
   fp.k = k;
   fp.vt = vt;
   fp.bias = bias;
-  fp.biasf = biasf;
   fp.mb = mb;
   fp.out = static_cast<T*>(a->out);
   fp.n = n;

@@ -22,12 +22,14 @@
 // tile t-1 interleaved with the exponentials of tile t, then the score MFMAs
 // of tile t+1; the pipeline runs across key blocks without draining.
 //
-// Memory: the triangle bias arrives in fp32 (times log2 e) and is copied
-// global -> LDS by DMA (global_load_lds_dwordx4: no registers, no
-// conversion), double-buffered, one block ahead; chunk c of bias row r sits in
-// LDS slot 16 r + (c ^ (r & 15)), so the 16-byte reads of 16 rows by 16 lanes
-// hit 16 distinct bank groups. K and V are loaded straight into registers one
-// block ahead (two register sets). Masked keys: see block_mask below.
+// Memory: the triangle bias (bf16, times log2 e) is copied global -> LDS by
+// DMA (global_load_lds_dwordx4: no registers), double-buffered, one block
+// ahead; the 16-byte chunk c (8 keys) of bias row r sits in LDS slot
+// 8 r + (c ^ ((r >> 1) & 7)), so the 16-byte reads of 16 rows by 16 lanes hit
+// 16 distinct bank groups. A lane widens its 8 bf16 to the fp32 score
+// accumulators with one shift or mask each. K and V are loaded straight into
+// registers one block ahead (two register sets). Masked keys: see block_mask
+// below.
 #include <type_traits>
 
 #include "fjx_common.hpp"
@@ -76,8 +78,8 @@ __device__ __forceinline__ bf16x8 buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t v
 __global__ __launch_bounds__(64 * kPWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   constexpr int NQT = kPNqt;
-  constexpr int NDMA = kPQwg / kPWaves / 4;  // DMA instructions per wave per block (4 bias rows of 256 B each)
-  __shared__ __attribute__((aligned(16))) f32x4 bias_s[2][kPQwg * 16];
+  constexpr int NDMA = kPQwg / kPWaves / 8;  // DMA instructions per wave per block (8 bias rows of 128 B each)
+  __shared__ __attribute__((aligned(16))) u32x4 bias_s[2][kPQwg * 8];
 
   const int64_t n = P.n;
   const int64_t np = P.np;
@@ -111,11 +113,11 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   const bf16* K = P.k + head_off * kPD;
   const bf16* VT = P.vt + ((b * P.rows + i) * H * kPD + h * kPD) * np;
   const float* MB = P.mb + (b * P.rows + i) * np;
-  const float* BIAS = P.biasf + b * P.bias_stride_b + (h * np + q0) * np;
+  const bf16* BIAS = P.bias + b * P.bias_stride_b + (h * np + q0) * np;
   const __amdgpu_buffer_rsrc_t rk = buf_rsrc(K, (uint32_t)(np * kPD * 2));
   const __amdgpu_buffer_rsrc_t rv = buf_rsrc(VT, (uint32_t)(kPD * np * 2));
   const __amdgpu_buffer_rsrc_t rm = buf_rsrc(MB, (uint32_t)(np * 4));
-  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(BIAS, (uint32_t)(kPQwg * np * 4));
+  const __amdgpu_buffer_rsrc_t rb = buf_rsrc(BIAS, (uint32_t)(kPQwg * np * 2));
   const int64_t nblk = np / kPKB;  // even: np is a multiple of 128
 
   // a row with every key masked would sum to 0; its softmax is that of the
@@ -137,24 +139,24 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   const bool full_row = !any_valid;
 
   // DMA of a block's bias tile: wave w copies RPW bias rows of the
-  // workgroup's 128; instruction j covers rows RPW w + 4j + lane/16, and lane
-  // fetches the chunk that belongs in slot lane%16: (lane%16) ^ (row & 15)
+  // workgroup's 128; instruction j covers rows RPW w + 8j + lane/8, and lane
+  // fetches the chunk that belongs in slot lane%8: (lane%8) ^ ((row >> 1) & 7)
   constexpr int RPW = kPQwg / kPWaves;  // bias rows each wave copies
-  // row & 15 of instruction j depends on j only through j % 4 (RPW and 16
-  // are multiples of 16 rows apart): four per-lane offsets, the rest uniform
-  uint32_t dma_off[4];
+  // (row >> 1) & 7 of instruction j depends on j only through j % 2 (RPW is
+  // a multiple of 16): two per-lane offsets, the rest uniform
+  uint32_t dma_off[2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = RPW * wave + 4 * j + (lane >> 4);
-    const int c = (lane & 15) ^ (r & 15);
-    dma_off[j] = (uint32_t)(r * np * 4 + 16 * c);
+  for (int j = 0; j < 2; ++j) {
+    const int r = RPW * wave + 8 * j + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> 1) & 7);
+    dma_off[j] = (uint32_t)(r * np * 2 + 16 * c);
   }
   auto dma_bias = [&](int64_t blk, auto buf) {
 #pragma unroll
     for (int j = 0; j < NDMA; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rb, (__attribute__((address_space(3))) void*)(&bias_s[decltype(buf)::value][(RPW * wave + 4 * j) * 16]),
-          16, dma_off[j & 3], (uint32_t)(blk * kPKB * 4 + (j >> 2) * 16 * np * 4), 0, 0);
+          rb, (__attribute__((address_space(3))) void*)(&bias_s[decltype(buf)::value][(RPW * wave + 8 * j) * 8]),
+          16, dma_off[j & 1], (uint32_t)(blk * kPKB * 2 + (j >> 1) * 16 * np * 2), 0, 0);
   };
 
   // Q of the wave's tiles, in registers for the whole row
@@ -225,13 +227,22 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   };
   bool masked = block_mask(mbn[0]);
 
-  // bias tile of this wave's query tile qt from LDS buffer buf, as the score accumulators
+  // bias tile of this wave's query tile qt from LDS buffer buf, as the score
+  // accumulators: chunk lg (keys 8 lg .. +7) holds key tiles 0 and 1, chunk
+  // 4 + lg key tiles 2 and 3; bf16 -> fp32 is the 16-bit word moved to the
+  // high half
   auto read_bias = [&](f32x4 (&s)[4], auto buf, int qt) {
     const int r = qw + 16 * qt + li;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const int c = 8 * (kt >> 1) + 2 * lg + (kt & 1);
-      s[kt] = bias_s[decltype(buf)::value][16 * r + (c ^ li)];
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const u32x4 w = bias_s[decltype(buf)::value][8 * r + ((4 * h2 + lg) ^ ((r >> 1) & 7))];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        s[2 * h2 + j][0] = __uint_as_float(w[2 * j] << 16);
+        s[2 * h2 + j][1] = __uint_as_float(w[2 * j] & 0xFFFF0000u);
+        s[2 * h2 + j][2] = __uint_as_float(w[2 * j + 1] << 16);
+        s[2 * h2 + j][3] = __uint_as_float(w[2 * j + 1] & 0xFFFF0000u);
+      }
     }
   };
   auto scores = [&](f32x4 (&s)[4], auto set, int qt) {
@@ -284,7 +295,7 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   // has arrived by then). The next step's exponentials read those scores
   // only after its own product MFMAs.
   auto products_phase = [&](bool with_reads) {
-    if (with_reads) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read
+    if (with_reads) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
 #pragma unroll
     for (int m = 0; m < 6; ++m) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -400,10 +411,10 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
 }
 
 bool launch_flash_pipe(const FlashParams<bf16>& p, int64_t batch, hipStream_t st) {
-  // needs the fp32 bias, the fallback flags (the offset kernel recomputes
-  // what this pass flags) and a padded length that is a multiple of 128;
-  // launches the grid of the fallback kernel
-  if (!p.biasf || !p.fallback || p.rows < 2 || p.np % kPQwg != 0) return false;
+  // needs the fallback flags (the offset kernel recomputes what this pass
+  // flags) and a padded length that is a multiple of 128; launches the grid
+  // of the fallback kernel
+  if (!p.fallback || p.rows < 2 || p.np % kPQwg != 0) return false;
   const int64_t rg = (p.rows + kPRows - 1) / kPRows;
   const dim3 grid((unsigned)(batch * p.heads * rg * (p.np / kPQwg)));
   hipLaunchKernelGGL(flash_pipe_kernel_bf16, grid, dim3(64 * kPWaves), 0, st, p);

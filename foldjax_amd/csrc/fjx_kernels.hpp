@@ -37,7 +37,6 @@ struct TriAttnPrologueParams {
   T* k;
   T* vt;            // [B][N][128][Np]
   T* bias;          // [B][4][Np][Np]
-  float* biasf;     // null, or the same bias in fp32 (for the pipelined flash kernel)
   float* mb;        // [B][N][Np]
   int64_t n;
   int64_t np;
@@ -148,7 +147,6 @@ struct FlashParams {
   const T* k;        // [B][N][H][Np][32]
   const T* vt;       // [B][N][H*32][Np]
   const T* bias;     // [B][H][Np][Np], already times log2 e
-  const float* biasf;  // null, or the same bias in fp32: the pipelined bf16 kernel stages it by LDS DMA
   const float* mb;   // [B][N][Np], already times log2 e; -inf for padded keys
   T* out;            // out[b][i][q][h*32+d] via the strides below
   int64_t n;

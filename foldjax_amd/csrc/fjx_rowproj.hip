@@ -297,21 +297,12 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
           const int64_t boff = (((int64_t)tl.b * H + hd) * np + tl.r) * np + tl.s0 + p0;
           T* brow = P.bias + boff;
           store8(brow, pack8<T>(v));
-          if (P.biasf) {
-            *reinterpret_cast<f32x4*>(P.biasf + boff) = f32x4{v[0], v[1], v[2], v[3]};
-            *reinterpret_cast<f32x4*>(P.biasf + boff + 4) = f32x4{v[4], v[5], v[6], v[7]};
-          }
           // the bias rows of the padded queries n .. np-1 (whose outputs are
           // dropped) are zeroed too, so the attention never reads stale
           // workspace memory
           const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
           for (int64_t rz = n + tl.r; rz < np; rz += n) {
             store8(brow + (rz - tl.r) * np, pack8<T>(zero));
-            if (P.biasf) {
-              float* fz = P.biasf + boff + (rz - tl.r) * np;
-              *reinterpret_cast<f32x4*>(fz) = f32x4{0.f, 0.f, 0.f, 0.f};
-              *reinterpret_cast<f32x4*>(fz + 4) = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
           }
         }
       }
