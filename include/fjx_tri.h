@@ -81,10 +81,10 @@ enum {
  * contraction runs on bf16 MFMA with fp32 accumulation (the reference's
  * fp32-upcast contraction of bf16 values, B2T/triangle.py:95-97) and o is
  * rounded to bf16 before LN_out (B2T/triangle.py:124). Fused kernels serve
- * c_z == c_h == 128; other widths (c_z, c_h multiples of 8 up to 1024, e.g.
- * the Protenix template stack's c_z = 64, c_h = 128, protenix/models/triangle/
- * triangle.py:131-137) run a general path of row LayerNorms, GEMMs and the same
- * contraction, with a larger workspace.
+ * c_h == 128 with c_z of 128 or 32, 64, 96 (the Protenix template stack's
+ * c_z = 64, c_h = 128, protenix/models/triangle/triangle.py:131-137); other
+ * widths (c_z, c_h multiples of 8 up to 1024) run a general path of row
+ * LayerNorms, GEMMs and the same contraction, with a larger workspace.
  */
 typedef struct fjx_trimul_args {
   int64_t batch;
@@ -150,10 +150,11 @@ int fjx_trimul_fwd_noalloc(const fjx_trimul_args* args, hipStream_t stream);
  *   out       = (sigmoid(g) * o) w_o^T                 (+ residual)
  *
  * Weights are PyTorch [out, in]. The softmax runs in fp32 with exp2 and the
- * log2(e) factor folded into q and the biases. Fused kernels serve c_z == 128,
- * heads * head_dim == 128, head_dim == 32; other widths (c_z a multiple of 8
- * up to 1024, any heads, head_dim == 32) run a general path of row
- * LayerNorms, GEMMs and the same flash core, with a larger workspace.
+ * log2(e) factor folded into q and the biases. Fused kernels serve c_z of 128
+ * or 32, 64, 96 with heads * head_dim == 128, head_dim == 32; other widths
+ * (c_z a multiple of 8 up to 1024, any heads, head_dim == 32) run a general
+ * path of row LayerNorms, GEMMs and the same flash core, with a larger
+ * workspace.
  */
 typedef struct fjx_triattn_args {
   int64_t batch;
@@ -225,7 +226,8 @@ int fjx_triattn_core(const fjx_triattn_core_args* args, hipStream_t stream);
  * and openfold3/models/primitives.py:133-150 (row_mask = the OpenFold3 mask).
  * Weights PyTorch [out, in]: w_a, w_b [hidden, c]; w_o [c, hidden]; hidden = 0
  * means 4c. A fused kernel (the hidden activations never leave the chip)
- * serves c == 128 with hidden == 4c and needs no workspace; every other width
+ * serves c of 128 or 32, 64, 96 with hidden == 4c and needs no workspace;
+ * every other width
  * (c and hidden multiples of 8, c <= 1024; the single track's c = 384
  * included) runs a general path of GEMMs through the workspace of
  * fjx_transition_workspace_size.
