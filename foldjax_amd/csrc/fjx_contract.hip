@@ -489,6 +489,9 @@ bool launch_contract(const bf16* a, const bf16* b, bf16* o, int64_t n, int64_t b
 
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st) {
+  if constexpr (std::is_same<T, bf16>::value && std::is_same<TO, bf16>::value) {
+    if (launch_gemm_dma(p, st)) return;
+  }
   auto tiles = [&](int64_t bm) { return p.batches * ((p.m + bm - 1) / bm) * ((p.n + bm - 1) / bm); };
   // 128-wide tiles unless they would leave most of the 256 CUs idle
   if (tiles(128) >= 512)

@@ -1,0 +1,255 @@
+// General bf16 "NT" GEMM on the LDS-DMA pipeline of the triangle contraction:
+// for every batch b
+//     C[i][j] = epilogue( sum_k A[i][k] * B[j][k] )
+// with both operands k-contiguous (B a PyTorch [out, in] weight), the epilogue
+// of gemm_nt_kernel (fjx_contract.hip): + bias[j], sigmoid or SiLU on the
+// columns from act_col0, * gate[i][j], + residual[i][j], rows whose row_gate
+// is 0 written as 0. It serves the projections of the general-width paths,
+// whose row counts are the pair grid's (B N^2) and whose K is a layer width.
+//
+// Tiling as contract_dma_kernel: a 256 x 256 output tile per 512-thread
+// workgroup (8 waves of 128 x 64), k in stages of 64 copied global -> LDS by
+// DMA (buffer_load ... lds: no registers, no LDS write instructions), two
+// stages in 128 KB of LDS, chunk c of row r in slot 8 r + (c ^ ((r / 2) % 8))
+// so the fragment reads of 16 consecutive rows hit 16 bank groups. The DMA
+// goes through buffer resources sized to the operands, and a lane whose chunk
+// lies past K gets an offset past the resource's end: rows past M or N and
+// the k tail read as zero, so any M, N and K (K a multiple of 8) work.
+//
+// Persistent: one workgroup per CU walks its XCD's contiguous share of the
+// tiles, n-tiles fastest, so an A row block is reused from that XCD's L2 by
+// its consecutive n-tiles; the next tile's first stage goes out during the
+// last k-step. Accumulators are transposed (A operand = B rows), so a lane
+// holds 4 consecutive output columns of one row: 8-byte epilogue accesses.
+#include <algorithm>
+
+#include "fjx_common.hpp"
+#include "fjx_kernels.hpp"
+#include "fjx_tile.hpp"
+
+namespace fjx {
+namespace {
+
+constexpr int kGT = 256;         // output tile rows and columns
+constexpr int kGDK = 64;         // k per stage
+constexpr int kGCH = kGDK / 8;   // 16-byte chunks per tile row in a stage
+constexpr int kGRPI = 64 / kGCH; // tile rows per DMA instruction (1 KB)
+constexpr int kGNI = kGCH / 2;   // DMA instructions per wave per operand per stage (32 rows)
+constexpr int kGXcd = 8;
+constexpr uint32_t kGOob = 0x80000000u;  // a lane offset past every resource's end
+// fewer 256 x 256 tiles than this go to gemm_nt_kernel's 128- or 64-wide tiles
+constexpr int64_t kMinTiles = 64;
+
+__device__ __forceinline__ int gswz(int r) { return (r / (16 / kGCH)) % kGCH; }
+__device__ __forceinline__ int gslot(int r, int c) { return kGCH * r + (c ^ gswz(r)); }
+
+// raw buffer resource over `bytes` bytes from `base` (at most 2^31 - 1: the
+// tiles address their operands from a per-tile base)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t grsrc(const void* base, int64_t bytes) {
+  const int64_t b = bytes < 0 ? 0 : (bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)b, 0x00020000);
+}
+
+__global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P) {
+  __shared__ __attribute__((aligned(16))) bf16 S[2][2][kGT * kGDK];  // [stage][A, B][256 rows x 64]
+
+  const int64_t M = P.m, N = P.n, K = P.k;
+  const int64_t tm = (M + kGT - 1) / kGT;
+  const int64_t tn = (N + kGT - 1) / kGT;
+  const int64_t total = P.batches * tm * tn;
+  const int64_t per_xcd = gridDim.x / kGXcd;  // the grid is a multiple of 8
+  const int64_t xcd = blockIdx.x % kGXcd;
+  const int64_t hi = (xcd + 1) * total / kGXcd;
+
+  const int t = threadIdx.x;
+  const int wave = t >> 6;
+  const int lane = t & 63;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int wm = (wave >> 2) * 128;
+  const int wn = (wave & 3) * 64;
+
+  // this lane's DMA rows and chunks: instruction j copies tile row
+  // r = 32 wave + 8 j + lane / 8, chunk c (k = 8 c). The swizzle of r depends
+  // on j only through j % 2, so two per-lane offsets per operand serve all
+  // four instructions, the rest (16 rows per two instructions) is uniform
+  uint32_t aoff[2], boff[2];
+  int kc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 32 * wave + kGRPI * j + lane / kGCH;
+    const int c = (lane % kGCH) ^ gswz(r);
+    kc[j] = 8 * c;
+    aoff[j] = (uint32_t)(r * P.lda * 2 + 16 * c);
+    boff[j] = (uint32_t)(r * P.ldb * 2 + 16 * c);
+  }
+  const uint32_t astep = (uint32_t)(2 * kGRPI * P.lda * 2), bstep = (uint32_t)(2 * kGRPI * P.ldb * 2);
+
+  struct Tile {
+    int64_t bat, m0, n0;
+    __amdgpu_buffer_rsrc_t ra, rb;
+  };
+  auto tile_of = [&](int64_t lid) {
+    Tile tl;
+    tl.bat = lid / (tm * tn);
+    const int64_t r = lid % (tm * tn);
+    tl.m0 = (r / tn) * kGT;
+    tl.n0 = (r % tn) * kGT;
+    tl.ra = grsrc(P.a + tl.bat * P.sa + tl.m0 * P.lda, (M - tl.m0) * P.lda * 2);
+    tl.rb = grsrc(P.b + tl.bat * P.sb + tl.n0 * P.ldb, (N - tl.n0) * P.ldb * 2);
+    return tl;
+  };
+  // stage st <- k-tile kt of tile tl (st a compile-time constant at every call)
+  auto issue = [&](const Tile& tl, int64_t kt, int st) {
+    const int64_t k0 = kt * kGDK;
+    // the k offset and the uniform row offset go in the scalar offset; a
+    // lane whose chunk lies past K reads from past the resource's end
+    const bool in0 = k0 + kc[0] < K, in1 = k0 + kc[1] < K;
+    const uint32_t ao[2] = {in0 ? aoff[0] : kGOob, in1 ? aoff[1] : kGOob};
+    const uint32_t bo[2] = {in0 ? boff[0] : kGOob, in1 ? boff[1] : kGOob};
+#pragma unroll
+    for (int j = 0; j < kGNI; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          tl.ra, (__attribute__((address_space(3))) void*)(&S[st][0][(32 * wave + kGRPI * j) * kGDK]), 16,
+          ao[j & 1], (uint32_t)(2 * k0) + (uint32_t)(j >> 1) * astep, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          tl.rb, (__attribute__((address_space(3))) void*)(&S[st][1][(32 * wave + kGRPI * j) * kGDK]), 16,
+          bo[j & 1], (uint32_t)(2 * k0) + (uint32_t)(j >> 1) * bstep, 0, 0);
+    }
+  };
+
+  const int64_t ktiles = (K + kGDK - 1) / kGDK;
+  int64_t lid = xcd * total / kGXcd + blockIdx.x / kGXcd;
+  if (lid >= hi) return;
+  Tile cur = tile_of(lid);
+  issue(cur, 0, 0);
+  for (;;) {
+    const int64_t next_lid = lid + per_xcd;
+    const bool has_next = next_lid < hi;
+    const Tile nxt = tile_of(has_next ? next_lid : lid);
+
+    f32x4 acc[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // k-tile kt uses stage kt % 2; every tile starts in stage 0, so the
+    // next tile's first stage goes to the stage after the last k-tile's
+    auto kstep = [&](int64_t kt, auto stc) {
+      constexpr int st = decltype(stc)::value;
+      // this wave's DMA of stage st (and everything before it) is complete
+      __builtin_amdgcn_s_waitcnt(0xF70);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");  // no LDS read moves above the barrier
+      if (kt + 1 < ktiles) issue(cur, kt + 1, st ^ 1);
+      else if (has_next && st == 1) issue(nxt, 0, 0);
+      const bf16* As_ = &S[st][0][0];
+      const bf16* Bs_ = &S[st][1][0];
+#pragma unroll
+      for (int ks = 0; ks < kGDK / 32; ++ks) {
+        bf16x8 af[8], bfr[4];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * gslot(wm + 16 * i + li, 4 * ks + lg));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * gslot(wn + 16 * j + li, 4 * ks + lg));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) mma(acc[j][i], bfr[j], af[i]);
+      }
+    };
+    int64_t kt = 0;
+    for (; kt + 1 < ktiles; kt += 2) {
+      kstep(kt, std::integral_constant<int, 0>());
+      kstep(kt + 1, std::integral_constant<int, 1>());
+    }
+    if (kt < ktiles) {
+      // an odd number of k-tiles: the last one is in stage 0, and the next
+      // tile's first stage (stage 0 again) is issued once every wave is past
+      // its reads (below)
+      kstep(kt, std::integral_constant<int, 0>());
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (has_next) issue(nxt, 0, 0);
+    }
+
+    // epilogue: this lane holds row m0 + wm + 16 i + li, columns
+    // n0 + wn + 16 j + 4 lg .. +3 of acc[j][i]
+    bf16* O = P.c + cur.bat * P.sc;
+    const bf16* G = P.gate ? P.gate + cur.bat * P.sc : nullptr;
+    const bf16* R = P.residual ? P.residual + cur.bat * P.sc : nullptr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = cur.n0 + wn + 16 * j + 4 * lg;
+      if (col >= N) continue;  // N is a multiple of 4 (checked by the launcher)
+      float bias[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bias[q] = P.bias && (P.bias_n == 0 || col + q < P.bias_n) ? to_f32(P.bias[col + q]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t row = cur.m0 + wm + 16 * i + li;
+        if (row >= M) continue;
+        const bool zero_row = P.row_gate && to_f32(P.row_gate[row]) == 0.f;
+        const int64_t off = row * P.ldc + col;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float x = acc[j][i][q] + bias[q];
+          const int act = col + q >= P.act_col0 ? P.act : 0;
+          if (act == 1) x = fast_sigmoid(x);
+          else if (act == 2) x *= fast_sigmoid(x);  // silu
+          v[q] = x;
+        }
+        if (G) {
+          float g[4];
+          load4f(G + off, g);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] *= g[q];
+        }
+        if (R) {
+          float r[4];
+          load4f(R + off, r);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] += r[q];
+        }
+        if (zero_row) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] *= 0.f;
+        }
+        store4f(O + off, v);
+      }
+    }
+    if (!has_next) break;
+    lid = next_lid;
+    cur = nxt;
+  }
+  // the last tile's clamped prefetch is not issued (has_next is false), so
+  // no DMA is in flight here
+}
+
+}  // namespace
+
+bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st) {
+  // 16-byte rows for the DMA, 8-byte output groups, and enough rows to fill
+  // the device with 256 x 256 tiles
+  const bool ok = p.k % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.n % 4 == 0 && p.ldc % 4 == 0 &&
+                  (reinterpret_cast<uintptr_t>(p.a) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(p.c) & 7) == 0 && (!p.gate || (reinterpret_cast<uintptr_t>(p.gate) & 7) == 0) &&
+                  (!p.residual || (reinterpret_cast<uintptr_t>(p.residual) & 7) == 0) &&
+                  (p.batches == 1 || (p.sa % 8 == 0 && p.sb % 8 == 0 && p.sc % 4 == 0)) &&
+                  p.lda * 2 * (int64_t)kGT < (int64_t)kGOob && p.ldb * 2 * (int64_t)kGT < (int64_t)kGOob &&
+                  p.ldc * 2 * (int64_t)kGT < (int64_t)kGOob;
+  const int64_t total = p.batches * ((p.m + kGT - 1) / kGT) * ((p.n + kGT - 1) / kGT);
+  if (!ok || total < kMinTiles) return false;
+  const void* k = reinterpret_cast<const void*>(&gemm_dma_kernel);
+  const int64_t cap = std::max<int64_t>(kGXcd, tile::resident_blocks(k, 512) / kGXcd * kGXcd);
+  const int64_t grid = std::min<int64_t>(cap, (total + kGXcd - 1) / kGXcd * kGXcd);
+  hipLaunchKernelGGL(gemm_dma_kernel, dim3((unsigned)grid), dim3(512), 0, st, p);
+  return true;
+}
+
+}  // namespace fjx

@@ -173,6 +173,9 @@ template <typename T>
 void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st);
 template <typename T, typename TO>
 void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st);
+// the bf16 GEMM on the LDS-DMA pipeline (fjx_gemm_dma.hip); false when the
+// shape or alignment does not suit it (the caller then runs gemm_nt_kernel)
+bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st);
 // triangle contraction, bf16: o[c] = a[c] b[c]^T for c < batches, each n x n
 // blocked: write o tile-blocked, [batches / 128][N*N/256][128][256] (needs
 // batches a multiple of 128 and n a multiple of 256), else [batches][N*N];

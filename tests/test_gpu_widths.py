@@ -171,3 +171,62 @@ def test_narrow_separate_residual_and_out_mask(dt, c_z):
         rows = mv.max(axis=1) > 0
         g, w_ = (to_np(got)[rows], want[rows]) if starting else (to_np(got)[:, rows], want[:, rows])
         assert_parity(g, w_, dtype, f"narrow triattn starting={starting} residual")
+
+
+@pytest.mark.parametrize("c,rows,masked", [(384, 8300, True), (264, 8300, False)])
+def test_transition_wide_rows_dma_gemm_bf16(c, rows, masked):
+    """Wide transitions over enough rows that their GEMMs run on the LDS-DMA
+    kernel (64 or more 256 x 256 tiles): c = 384 (K = 384 and 1536, even
+    stage counts) and c = 264 (K = 264 and 1056: odd stage counts, a k tail
+    of 8 and 32, and an output width that ends 8 columns into a tile)."""
+    dtype = DTYPES["bf16"]
+    say(f"transition dma gemm c={c} rows={rows} masked={masked}")
+    rng = np.random.default_rng(c + 7)
+    x = rng.standard_normal((rows, c)).astype(np.float32)
+    w = syn.transition_weights(c, 4, seed=19)
+    rm = (rng.random(rows) > 0.3).astype(np.float32) if masked else None
+    tw = P.pack_transition_torch({k: w[k] for k in ("layer_norm", "linear_a", "linear_b", "linear_out")}, dtype, "cuda")
+    xt = device_tensor(x, dtype)
+    got = kernels.transition(xt, tw, row_mask=None if rm is None else device_tensor(rm, dtype), residual=xt)
+    torch.cuda.synchronize()
+    xr = prep(x, dtype)
+    want = xr + O.transition(xr, prep_tree(w, dtype), mask=rm)
+    assert_parity(to_np(got), want, dtype, f"transition c={c} rows={rows}")
+
+
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_wide_dma_gemm_bf16(direction):
+    """c_z = c_h = 384 at n = 96: the projections (9216 rows) run on the
+    LDS-DMA GEMM, against the oracle."""
+    dtype = DTYPES["bf16"]
+    n, c = 96, 384
+    say(f"trimul dma gemm c={c} n={n} {direction}")
+    z = syn.pair_input(n, c, seed=41)
+    m = mask_case("tail", n)
+    w = syn.trimul_weights(c, c, seed=42)
+    got = protenix.triangle_multiplication(device_tensor(z, dtype), device_tensor(m, dtype),
+                                           P.trimul_to_protenix(w), direction)
+    torch.cuda.synchronize()
+    want = O.protenix_triangle_multiplication(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), direction)
+    assert_parity(to_np(got), want, dtype, f"trimul c={c} n={n} {direction}")
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_triattn_wide_dma_gemm_bf16(starting):
+    """c_z = 384 with 8 heads of 32 at n = 96: the q/k/v/g and output
+    projections run on the LDS-DMA GEMM, against the oracle."""
+    dtype = DTYPES["bf16"]
+    n, c, heads = 96, 384, 8
+    say(f"triattn dma gemm c={c} heads={heads} n={n} starting={starting}")
+    z = syn.pair_input(n, c, seed=43)
+    m = mask_case("tail", n)
+    w = syn.triattn_weights(c, heads, 32, seed=44)
+    got = protenix.triangle_attention(device_tensor(z, dtype), device_tensor(m, dtype), P.triattn_to_protenix(w),
+                                      num_heads=heads, starting=starting)
+    torch.cuda.synchronize()
+    want = O.protenix_triangle_attention(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), num_heads=heads,
+                                         starting=starting)
+    mv = m if starting else m.T
+    rows = mv.max(axis=1) > 0
+    g, w_ = (to_np(got)[rows], want[rows]) if starting else (to_np(got)[:, rows], want[:, rows])
+    assert_parity(g, w_, dtype, f"triattn c={c} n={n} starting={starting}")
