@@ -671,7 +671,7 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
 }
 
 struct GenTransitionWs {
-  size_t xn, h, y, total;
+  size_t xn, h, wcat, total;
 };
 GenTransitionWs gen_transition_ws(int64_t rows, int64_t c, int64_t hidden, int32_t dtype) {
   const size_t es = esize(dtype);
@@ -684,7 +684,7 @@ GenTransitionWs gen_transition_ws(int64_t rows, int64_t c, int64_t hidden, int32
   };
   w.xn = take((size_t)rows * c * es);
   w.h = take((size_t)rows * hidden * es);
-  w.y = take((size_t)rows * c * es);
+  w.wcat = take((size_t)2 * hidden * c * es);  // W_a and W_b interleaved by 128 rows (the fused SwiGLU GEMM)
   w.total = off;
   return w;
 }
@@ -696,21 +696,42 @@ int transition_generic_run(const fjx_transition_args* a, hipStream_t st) {
   void* W = a->workspace;
   T* xn = at<T>(W, ws.xn);
   T* h = at<T>(W, ws.h);
-  T* y = at<T>(W, ws.y);
   // the 384-channel single track is timed apart from the pair track
   const int id = c == 384 ? K_SINGLE_TRANSITION : K_TRANSITION;
   return timed(id, st, "transition", [&] {
     launch_layernorm_rows<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_weight),
                              static_cast<const T*>(a->norm_bias), xn, rows, (int)c, a->eps, st);
-    GemmParams<T, T> g = rows_gemm<T>(xn, rows, c, a->w_a, hid, h, hid);
-    g.act = 2;
+    bool fused = false;
+    if constexpr (std::is_same<T, bf16>::value) {
+      // silu(x W_a^T) * (x W_b^T) as one GEMM over the interleaved weights
+      T* wcat = at<T>(W, ws.wcat);
+      GemmParams<T, T> g = rows_gemm<T>(xn, rows, c, wcat, 2 * hid, h, hid);
+      g.swiglu = 1;
+      if (hid % 128 == 0 && gemm_dma_ok(g)) {
+        const size_t blk = (size_t)128 * c * sizeof(T);  // one block of 128 weight rows
+        fused = hipMemcpy2DAsync(wcat, 2 * blk, a->w_a, blk, blk, hid / 128, hipMemcpyDeviceToDevice, st) ==
+                    hipSuccess &&
+                hipMemcpy2DAsync(reinterpret_cast<char*>(wcat) + blk, 2 * blk, a->w_b, blk, blk, hid / 128,
+                                 hipMemcpyDeviceToDevice, st) == hipSuccess &&
+                launch_gemm_dma(g, st);
+      }
+    }
+    if (!fused) {
+      GemmParams<T, T> g = rows_gemm<T>(xn, rows, c, a->w_a, hid, h, hid);
+      g.act = 2;
+      launch_gemm<T, T>(g, st);
+      g = rows_gemm<T>(xn, rows, c, a->w_b, hid, h, hid);
+      g.gate = h;  // in place
+      launch_gemm<T, T>(g, st);
+    }
+    // the output projection with the row mask, the residual and the output
+    // mask in its epilogue (rows map to themselves)
+    GemmParams<T, T> g = rows_gemm<T>(h, rows, hid, a->w_o, c, static_cast<T*>(a->out), c);
+    g.proj_round = 1;
+    g.row_scale = static_cast<const T*>(a->row_mask);
+    g.residual = static_cast<const T*>(a->residual);
+    g.row_gate = static_cast<const T*>(a->out_mask);
     launch_gemm<T, T>(g, st);
-    g = rows_gemm<T>(xn, rows, c, a->w_b, hid, h, hid);
-    g.gate = h;  // in place
-    launch_gemm<T, T>(g, st);
-    launch_gemm<T, T>(rows_gemm<T>(h, rows, hid, a->w_o, c, y, c), st);
-    launch_scatter_add<T>(y, static_cast<const T*>(a->row_mask), static_cast<const T*>(a->residual),
-                          static_cast<const T*>(a->out_mask), static_cast<T*>(a->out), rows, 1, (int)c, 0, st);
   });
 }
 

@@ -163,6 +163,10 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
         else if (act == 2) v *= fast_sigmoid(v);  // silu
         const int64_t off = row * P.ldc + col;
         if (G) v *= to_f32(G[off]);
+        if (P.proj_round) {
+          v = round_to<TO>(v);
+          if (P.row_scale) v = round_to<TO>(v * to_f32(P.row_scale[row]));
+        }
         if (R) v += to_f32(R[off]);
         if (P.row_gate && to_f32(P.row_gate[row]) == 0.f) v *= 0.f;
         O[off] = from_f32<TO>(v);

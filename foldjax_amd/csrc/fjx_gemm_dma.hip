@@ -176,6 +176,57 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
       if (has_next) issue(nxt, 0, 0);
     }
 
+    if (P.swiglu) {
+      // the tile's columns 0..127 are a, 128..255 b of the same 128 hidden
+      // units: the b waves hand their values (rounded to bf16) to the a
+      // waves of the same rows through stage 1 of LDS -- free: the next
+      // tile's first stage goes to stage 0 -- once every wave is past its
+      // last k-step's reads
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      bf16* X = &S[1][0][0];  // 64 KB: 4 b waves x 32 groups x 64 lanes x 4 values
+      const bool bwave = (wave & 3) >= 2;
+      const int pair = (wave >> 2) * 2 + (wave & 3) - (bwave ? 2 : 0);
+      if (bwave) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            bf16x4 v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = static_cast<bf16>(acc[j][i][q]);
+            *reinterpret_cast<bf16x4*>(X + 4 * ((pair * 32 + j * 8 + i) * 64 + lane)) = v;
+          }
+      }
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (!bwave) {
+        bf16* O = P.c + cur.bat * P.sc;
+        const int64_t hid = N / 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t col = cur.n0 / 2 + wn + 16 * j + 4 * lg;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const bf16x4 b = *reinterpret_cast<const bf16x4*>(X + 4 * ((pair * 32 + j * 8 + i) * 64 + lane));
+            const int64_t row = cur.m0 + wm + 16 * i + li;
+            if (row >= M || col >= hid) continue;
+            float v[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float a = round_to<bf16>(acc[j][i][q]);
+              v[q] = a * fast_sigmoid(a) * static_cast<float>(b[q]);
+            }
+            store4f(O + row * P.ldc + col, v);
+          }
+        }
+      }
+      if (!has_next) break;
+      lid = next_lid;
+      cur = nxt;
+      continue;
+    }
+
     // epilogue: this lane holds row m0 + wm + 16 i + li, columns
     // n0 + wn + 16 j + 4 lg .. +3 of acc[j][i]
     bf16* O = P.c + cur.bat * P.sc;
@@ -210,6 +261,11 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] *= g[q];
         }
+        if (P.proj_round) {
+          const float rs = P.row_scale ? to_f32(P.row_scale[row]) : 1.f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = round_to<bf16>(round_to<bf16>(v[q]) * rs);
+        }
         if (R) {
           float r[4];
           load4f(R + off, r);
@@ -233,7 +289,7 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
 
 }  // namespace
 
-bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st) {
+bool gemm_dma_ok(const GemmParams<bf16, bf16>& p) {
   // 16-byte rows for the DMA, 8-byte output groups, and enough rows to fill
   // the device with 256 x 256 tiles
   const bool ok = p.k % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.n % 4 == 0 && p.ldc % 4 == 0 &&
@@ -244,7 +300,12 @@ bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st) {
                   p.lda * 2 * (int64_t)kGT < (int64_t)kGOob && p.ldb * 2 * (int64_t)kGT < (int64_t)kGOob &&
                   p.ldc * 2 * (int64_t)kGT < (int64_t)kGOob;
   const int64_t total = p.batches * ((p.m + kGT - 1) / kGT) * ((p.n + kGT - 1) / kGT);
-  if (!ok || total < kMinTiles) return false;
+  return ok && total >= kMinTiles && (!p.swiglu || (p.n % kGT == 0 && !p.gate && !p.residual && !p.proj_round));
+}
+
+bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st) {
+  if (!gemm_dma_ok(p)) return false;
+  const int64_t total = p.batches * ((p.m + kGT - 1) / kGT) * ((p.n + kGT - 1) / kGT);
   const void* k = reinterpret_cast<const void*>(&gemm_dma_kernel);
   const int64_t cap = std::max<int64_t>(kGXcd, tile::resident_blocks(k, 512) / kGXcd * kGXcd);
   const int64_t grid = std::min<int64_t>(cap, (total + kGXcd - 1) / kGXcd * kGXcd);

@@ -102,6 +102,16 @@ struct GemmParams {
   const TO* gate;      // indexed like c, or null
   const TO* residual;  // indexed like c, or null (may alias c)
   const TO* row_gate;  // [m] per output row, or null: rows where it is 0 are written as 0 (after the residual)
+  // proj_round: the product is a projection output -- rounded to TO, times
+  // row_scale[row] when set, rounded again -- before the residual is added
+  // (the order of a transition's row mask and residual)
+  int proj_round;
+  const TO* row_scale;  // [m] or null (with proj_round)
+  // swiglu (launch_gemm_dma only): B is W_a and W_b interleaved in blocks of
+  // 128 rows (a block, then the b block of the same 128 hidden units), n =
+  // 2 hidden, and C[i][h] = silu(a[i][h]) * b[i][h] with a and b rounded to
+  // TO first; C has hidden columns
+  int swiglu;
 };
 
 template <typename T>
@@ -176,6 +186,8 @@ void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st);
 // the bf16 GEMM on the LDS-DMA pipeline (fjx_gemm_dma.hip); false when the
 // shape or alignment does not suit it (the caller then runs gemm_nt_kernel)
 bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st);
+// whether launch_gemm_dma takes p (shape, alignment and size)
+bool gemm_dma_ok(const GemmParams<bf16, bf16>& p);
 // triangle contraction, bf16: o[c] = a[c] b[c]^T for c < batches, each n x n
 // blocked: write o tile-blocked, [batches / 128][N*N/256][128][256] (needs
 // batches a multiple of 128 and n a multiple of 256), else [batches][N*N];
