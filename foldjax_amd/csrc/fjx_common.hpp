@@ -119,4 +119,37 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
 // wave-wide xor shuffle of a float (64 lanes)
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// LayerNorm of one row of c <= 512 channels by one wave, lane l holding
+// channels 8 l .. 8 l + 7
+template <typename T>
+__device__ __forceinline__ void ln_row8(const T* __restrict__ xr, const T* __restrict__ w, const T* __restrict__ b,
+                                        T* __restrict__ yr, int c, float eps, int lane) {
+  const int c0 = 8 * lane;
+  const bool on = c0 < c;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (on) to_f32x8(load8(xr + c0), v);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) s += v[e];
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) s += shfl_xor(s, o);
+  const float mean = s / c;
+  float q2 = 0.f;
+  if (on) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q2 += (v[e] - mean) * (v[e] - mean);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) q2 += shfl_xor(q2, o);
+  const float rstd = __builtin_amdgcn_rsqf(q2 / c + eps);
+  if (on) {
+    float wv[8], bv[8], o[8];
+    to_f32x8(load8(w + c0), wv);
+    to_f32x8(load8(b + c0), bv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (v[e] - mean) * rstd * wv[e] + bv[e];
+    store8(yr + c0, pack8<T>(o));
+  }
+}
+
 }  // namespace fjx

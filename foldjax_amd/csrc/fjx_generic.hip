@@ -153,20 +153,6 @@ __global__ void split_qk_kernel(const T* __restrict__ src, int64_t ld, int64_t c
   }
 }
 
-// v of the flash core, keys innermost: dst[br][hd][s] = src[br*n + s][c0 + hd]
-template <typename T>
-__global__ void split_vt_kernel(const T* __restrict__ src, int64_t ld, int64_t c0, T* __restrict__ dst, int64_t rows,
-                                int64_t n, int64_t np, int hd_total) {
-  const int64_t total = rows * hd_total * np;
-  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
-       idx += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t s = idx % np;
-    const int hd = (int)((idx / np) % hd_total);
-    const int64_t br = idx / (np * hd_total);
-    dst[idx] = s < n ? src[(br * n + s) * ld + c0 + hd] : from_f32<T>(0.f);
-  }
-}
-
 // triangle bias planes: dst[b][h][q][k] (np x np) = src[b][q*n + k][c0 + h] * log2 e, zeros outside
 template <typename T>
 __global__ void bias_planes_kernel(const T* __restrict__ src, int64_t ld, int64_t c0, T* __restrict__ dst,
@@ -236,14 +222,133 @@ __global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict_
   }
 }
 
+// ---- vectorized forms (8 contiguous elements, 16-byte accesses for bf16),
+// used when the widths and offsets are multiples of 8
+
+template <typename T>
+__global__ __launch_bounds__(256) void ln_grid8_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                       const T* __restrict__ b, T* __restrict__ y, int64_t rows,
+                                                       int64_t n, int c, float eps, int t) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t nn = n * n;
+  const int64_t bb = row / nn;
+  ln_row8<T>(x + (bb * nn + orig_pos(row - bb * nn, n, t)) * c, w, b, y + row * c, c, eps, threadIdx.x & 63);
+}
+
+// split_qk_kernel, 8 head dims per thread
+template <typename T>
+__global__ void split_qk8_kernel(const T* __restrict__ src, int64_t ld, int64_t c0, T* __restrict__ dst, int64_t rows,
+                                 int64_t n, int64_t np, int heads, float mul) {
+  const int64_t total = rows * heads * np * 4;
+  for (int64_t i8 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i8 < total;
+       i8 += (int64_t)gridDim.x * blockDim.x) {
+    const int d0 = (int)(i8 & 3) * 8;
+    int64_t r = i8 >> 2;
+    const int64_t s = r % np;
+    r /= np;
+    const int h = (int)(r % heads);
+    const int64_t br = r / heads;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (s < n) {
+      to_f32x8(load8(src + (br * n + s) * ld + c0 + 32 * h + d0), v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] *= mul;
+    }
+    store8(dst + i8 * 8, pack8<T>(v));
+  }
+}
+
+// v of the flash core, keys innermost: dst[br][hd][s] = src[br*n + s][c0 + hd] (zero for
+// s >= n), through 64 x 64 LDS tiles so that both sides move whole rows
+template <typename T>
+__global__ __launch_bounds__(256) void split_vt_tiled_kernel(const T* __restrict__ src, int64_t ld, int64_t c0,
+                                                             T* __restrict__ dst, int64_t n, int64_t np,
+                                                             int hd_total) {
+  __shared__ T tile[64][66];
+  const int htiles = (hd_total + 63) / 64;
+  const int64_t stiles = (np + 63) / 64;
+  int64_t id = blockIdx.x;
+  const int ht = (int)(id % htiles);
+  id /= htiles;
+  const int64_t st = id % stiles;
+  const int64_t br = id / stiles;
+  const int64_t s0 = st * 64;
+  const int h0 = ht * 64;
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int sl = e >> 6, hl = e & 63;
+    const int64_t s = s0 + sl;
+    const int hd = h0 + hl;
+    tile[sl][hl] = (s < n && hd < hd_total) ? src[(br * n + s) * ld + c0 + hd] : from_f32<T>(0.f);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 64 * 64; e += 256) {
+    const int hl = e >> 6, sl = e & 63;
+    const int64_t s = s0 + sl;
+    const int hd = h0 + hl;
+    if (s < np && hd < hd_total) dst[(br * hd_total + hd) * np + s] = tile[sl][hl];
+  }
+}
+
+// gate_rows_kernel, 8 columns per thread
+template <typename T>
+__global__ void gate_rows8_kernel(T* __restrict__ o, const T* __restrict__ g, int64_t ldg, int64_t c0, int64_t rows,
+                                  int width) {
+  const int w8 = width / 8;
+  const int64_t total = rows * w8;
+  for (int64_t i8 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i8 < total;
+       i8 += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = i8 / w8;
+    const int j = (int)(i8 - i * w8) * 8;
+    float ov[8], gv[8];
+    to_f32x8(load8(o + i * width + j), ov);
+    to_f32x8(load8(g + i * ldg + c0 + j), gv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ov[e] *= gv[e];
+    store8(o + i * width + j, pack8<T>(ov));
+  }
+}
+
+// scatter_add_kernel, 8 channels per thread
+template <typename T>
+__global__ void scatter_add8_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
+                                    const T* __restrict__ residual, const T* __restrict__ out_mask,
+                                    T* __restrict__ out, int64_t rows, int64_t n, int c, int t) {
+  const int c8 = c / 8;
+  const int64_t total = rows * c8;
+  const int64_t nn = n * n;
+  for (int64_t i8 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i8 < total;
+       i8 += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i8 / c8;
+    const int ch = (int)(i8 - row * c8) * 8;
+    const int64_t bb = row / nn;
+    const int64_t o = bb * nn + orig_pos(row - bb * nn, n, t);
+    float v[8];
+    to_f32x8(load8(y + row * c + ch), v);
+    const float m = row_mask ? to_f32(row_mask[o]) : 1.f;
+    const float g = out_mask && to_f32(out_mask[o]) == 0.f ? 0.f : 1.f;
+    float r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (residual) to_f32x8(load8(residual + o * c + ch), r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (round_to<T>(v[e] * m) + r[e]) * g;
+    store8(out + o * c + ch, pack8<T>(v));
+  }
+}
+
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 template <typename T>
 void launch_ln_grid(const T* x, const T* w, const T* b, T* y, int64_t batch, int64_t n, int c, float eps, int t,
                     hipStream_t st) {
   const int64_t rows = batch * n * n;
-  hipLaunchKernelGGL(ln_grid_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows, n, c,
-                     eps, t);
+  if (c % 8 == 0 && c <= 512 && al16(x) && al16(w) && al16(b) && al16(y))
+    hipLaunchKernelGGL(ln_grid8_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows, n, c,
+                       eps, t);
+  else
+    hipLaunchKernelGGL(ln_grid_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows, n, c,
+                       eps, t);
 }
 template <typename T>
 void launch_to_channel_major(const T* src, int64_t ld, int c0, int C, const T* mask, T* dst, int64_t batch, int64_t n,
@@ -260,14 +365,19 @@ void launch_to_position_major(const T* src, int C, T* dst, int64_t batch, int64_
 template <typename T>
 void launch_split_qk(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int heads,
                      float mul, hipStream_t st) {
-  hipLaunchKernelGGL(split_qk_kernel<T>, stride_grid(rows * heads * np * 32), dim3(256), 0, st, src, ld, c0, dst,
-                     rows, n, np, heads, mul);
+  if (ld % 8 == 0 && c0 % 8 == 0 && al16(src) && al16(dst))
+    hipLaunchKernelGGL(split_qk8_kernel<T>, stride_grid(rows * heads * np * 4), dim3(256), 0, st, src, ld, c0, dst,
+                       rows, n, np, heads, mul);
+  else
+    hipLaunchKernelGGL(split_qk_kernel<T>, stride_grid(rows * heads * np * 32), dim3(256), 0, st, src, ld, c0, dst,
+                       rows, n, np, heads, mul);
 }
 template <typename T>
 void launch_split_vt(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int hd_total,
                      hipStream_t st) {
-  hipLaunchKernelGGL(split_vt_kernel<T>, stride_grid(rows * hd_total * np), dim3(256), 0, st, src, ld, c0, dst, rows,
-                     n, np, hd_total);
+  const int64_t blocks = rows * ((np + 63) / 64) * ((hd_total + 63) / 64);
+  hipLaunchKernelGGL(split_vt_tiled_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, ld, c0, dst, n, np,
+                     hd_total);
 }
 template <typename T>
 void launch_bias_planes(const T* src, int64_t ld, int64_t c0, T* dst, int64_t batch, int64_t n, int64_t np, int heads,
@@ -283,13 +393,21 @@ void launch_grid_mask_bias(const T* mask, float* mb, int64_t batch, int64_t n, i
 }
 template <typename T>
 void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, int width, hipStream_t st) {
-  hipLaunchKernelGGL(gate_rows_kernel<T>, stride_grid(rows * width), dim3(256), 0, st, o, g, ldg, c0, rows, width);
+  if (width % 8 == 0 && ldg % 8 == 0 && c0 % 8 == 0 && al16(o) && al16(g))
+    hipLaunchKernelGGL(gate_rows8_kernel<T>, stride_grid(rows * width / 8), dim3(256), 0, st, o, g, ldg, c0, rows,
+                       width);
+  else
+    hipLaunchKernelGGL(gate_rows_kernel<T>, stride_grid(rows * width), dim3(256), 0, st, o, g, ldg, c0, rows, width);
 }
 template <typename T>
 void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
                         int64_t n, int c, int t, hipStream_t st) {
-  hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out_mask,
-                     out, rows, n, c, t);
+  if (c % 8 == 0 && al16(y) && al16(out) && (!residual || al16(residual)))
+    hipLaunchKernelGGL(scatter_add8_kernel<T>, stride_grid(rows * c / 8), dim3(256), 0, st, y, row_mask, residual,
+                       out_mask, out, rows, n, c, t);
+  else
+    hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out_mask,
+                       out, rows, n, c, t);
 }
 
 #define FJX_INST(T)                                                                                                \

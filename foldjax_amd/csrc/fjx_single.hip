@@ -46,6 +46,16 @@ __global__ __launch_bounds__(256) void layernorm_rows_kernel(const T* __restrict
   }
 }
 
+// the same for c <= 512 channels, a multiple of 8 (ln_row8)
+template <typename T>
+__global__ __launch_bounds__(256) void layernorm_rows8_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                              const T* __restrict__ b, T* __restrict__ y,
+                                                              int64_t rows, int c, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  ln_row8<T>(x + row * c, w, b, y + row * c, c, eps, threadIdx.x & 63);
+}
+
 // qkv rows [B*N][ld] holding q | k | v (each heads*dh wide) ->
 //   q, k: [B][H][Np][32] (q times q_mul), vt: [B][H*32][Np]; zero padding in d and keys
 template <typename T>
@@ -243,8 +253,13 @@ dim3 grid_stride(int64_t total) {
 
 template <typename T>
 void launch_layernorm_rows(const T* x, const T* w, const T* b, T* y, int64_t rows, int c, float eps, hipStream_t st) {
-  hipLaunchKernelGGL(layernorm_rows_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows, c,
-                     eps);
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (c % 8 == 0 && c <= 512 && al16(x) && al16(w) && al16(b) && al16(y))
+    hipLaunchKernelGGL(layernorm_rows8_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows,
+                       c, eps);
+  else
+    hipLaunchKernelGGL(layernorm_rows_kernel<T>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, x, w, b, y, rows,
+                       c, eps);
 }
 template <typename T>
 void launch_split_heads(const T* qkv, int64_t ld, int64_t batch, int64_t n, int64_t np, int heads, int dh,
