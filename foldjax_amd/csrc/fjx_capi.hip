@@ -501,7 +501,7 @@ GemmParams<T, T> rows_gemm(const T* x, int64_t rows, int64_t k, const void* w, i
 }
 
 struct GenTriMulWs {
-  size_t xn, pg, acm, bcm, ocm, g2, total;
+  size_t xn, pg, acm, bcm, ocm, g2, wcat, total;
 };
 GenTriMulWs gen_trimul_ws(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, int32_t dtype) {
   const size_t pos = (size_t)batch * n * n * esize(dtype);
@@ -518,6 +518,7 @@ GenTriMulWs gen_trimul_ws(int64_t batch, int64_t n, int64_t c_z, int64_t c_h, in
   w.bcm = take(pos * c_h);
   w.ocm = take(pos * c_h);
   w.g2 = take(pos * c_z);
+  w.wcat = take((size_t)4 * c_h * c_z * esize(dtype));  // p_in and g_in interleaved by 128 rows (the pair GEMM)
   w.total = off;
   return w;
 }
@@ -539,12 +540,29 @@ int trimul_generic_run(const fjx_trimul_args* a, hipStream_t st) {
   int rc = timed(K_TRIMUL_PROLOGUE, st, "trimul_prologue", [&] {
     launch_ln_grid<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_in_weight),
                       static_cast<const T*>(a->norm_in_bias), xn, B, n, (int)cz, a->eps, 0, st);
-    GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, a->g_in_weight, 2 * ch, pg, 2 * ch);
-    g.act = 1;
-    launch_gemm<T, T>(g, st);
-    g = rows_gemm<T>(xn, rows, cz, a->p_in_weight, 2 * ch, pg, 2 * ch);
-    g.gate = pg;  // in place: each element reads its gate, then is overwritten
-    launch_gemm<T, T>(g, st);
+    bool fused = false;
+    if constexpr (std::is_same<T, bf16>::value) {
+      // (x p_in^T) * sigmoid(x g_in^T) as one GEMM over the interleaved weights
+      T* wcat = at<T>(W, ws.wcat);
+      GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, wcat, 4 * ch, pg, 2 * ch);
+      g.swiglu = 2;
+      if ((2 * ch) % 128 == 0 && gemm_dma_ok(g)) {
+        const size_t blk = (size_t)128 * cz * sizeof(T);
+        fused = hipMemcpy2DAsync(wcat, 2 * blk, a->p_in_weight, blk, blk, 2 * ch / 128, hipMemcpyDeviceToDevice,
+                                 st) == hipSuccess &&
+                hipMemcpy2DAsync(reinterpret_cast<char*>(wcat) + blk, 2 * blk, a->g_in_weight, blk, blk,
+                                 2 * ch / 128, hipMemcpyDeviceToDevice, st) == hipSuccess &&
+                launch_gemm_dma(g, st);
+      }
+    }
+    if (!fused) {
+      GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, a->g_in_weight, 2 * ch, pg, 2 * ch);
+      g.act = 1;
+      launch_gemm<T, T>(g, st);
+      g = rows_gemm<T>(xn, rows, cz, a->p_in_weight, 2 * ch, pg, 2 * ch);
+      g.gate = pg;  // in place: each element reads its gate, then is overwritten
+      launch_gemm<T, T>(g, st);
+    }
     launch_to_channel_major<T>(pg, 2 * ch, 0, (int)ch, mask, acm, B, n, t, st);
     launch_to_channel_major<T>(pg, 2 * ch, (int)ch, (int)ch, mask, bcm, B, n, t, st);
   });

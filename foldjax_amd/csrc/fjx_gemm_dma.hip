@@ -177,7 +177,7 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
     }
 
     if (P.swiglu) {
-      // the tile's columns 0..127 are a, 128..255 b of the same 128 hidden
+      // the tile's columns 0..127 are a, 128..255 b of the same 128 output
       // units: the b waves hand their values (rounded to bf16) to the a
       // waves of the same rows through stage 1 of LDS -- free: the next
       // tile's first stage goes to stage 0 -- once every wave is past its
@@ -215,7 +215,8 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
               const float a = round_to<bf16>(acc[j][i][q]);
-              v[q] = a * fast_sigmoid(a) * static_cast<float>(b[q]);
+              const float bb = static_cast<float>(b[q]);
+              v[q] = P.swiglu == 1 ? a * fast_sigmoid(a) * bb : a * round_to<bf16>(fast_sigmoid(bb));
             }
             store4f(O + row * P.ldc + col, v);
           }

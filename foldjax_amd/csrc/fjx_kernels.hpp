@@ -107,10 +107,11 @@ struct GemmParams {
   // (the order of a transition's row mask and residual)
   int proj_round;
   const TO* row_scale;  // [m] or null (with proj_round)
-  // swiglu (launch_gemm_dma only): B is W_a and W_b interleaved in blocks of
-  // 128 rows (a block, then the b block of the same 128 hidden units), n =
-  // 2 hidden, and C[i][h] = silu(a[i][h]) * b[i][h] with a and b rounded to
-  // TO first; C has hidden columns
+  // pair mode (launch_gemm_dma only): B holds two weights interleaved in
+  // blocks of 128 rows (a block of the first, then the block of the second
+  // for the same 128 output units), n = 2 units, and C[i][u] combines a and b
+  // (both rounded to TO first): 1 = silu(a) * b (SwiGLU), 2 = a * sigmoid(b)
+  // (a gated projection); C has `units` columns
   int swiglu;
 };
 
