@@ -335,6 +335,91 @@ __global__ void scatter_add8_kernel(const T* __restrict__ y, const T* __restrict
   }
 }
 
+// to_channel_major_kernel and to_position_major_kernel with 16-byte global
+// accesses (8 channels of a position, 8 positions of a channel per thread);
+// the float tile's 65-float rows keep both LDS phases conflict-free
+template <typename T>
+__global__ __launch_bounds__(256) void to_channel_major8_kernel(const T* __restrict__ src, int64_t ld, int c0, int C,
+                                                                const T* __restrict__ mask, T* __restrict__ dst,
+                                                                int64_t n, int t) {
+  __shared__ float tile[64][65];
+  const int64_t nn = n * n;
+  const int64_t vtiles = (nn + 63) / 64;
+  const int ctiles = (C + 63) / 64;
+  int64_t id = blockIdx.x;
+  const int ct = (int)(id % ctiles);
+  id /= ctiles;
+  const int64_t vt = id % vtiles;
+  const int64_t bb = id / vtiles;
+  const int64_t v0 = vt * 64;
+  const int cb = ct * 64;
+  for (int e = threadIdx.x; e < 512; e += 256) {
+    const int pv = e >> 3, cc = (e & 7) * 8;
+    const int64_t v = v0 + pv;
+    const int c = cb + cc;
+    float val[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (v < nn && c < C) {
+      const int64_t o = bb * nn + orig_pos(v, n, t);
+      to_f32x8(load8(src + o * ld + c0 + c), val);
+      if (mask) {
+        const float m = to_f32(mask[o]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) val[k] *= m;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tile[pv][cc + k] = val[k];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 512; e += 256) {
+    const int pc = e >> 3, vv = (e & 7) * 8;
+    const int64_t v = v0 + vv;
+    const int c = cb + pc;
+    if (v < nn && c < C) {
+      float o8[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o8[k] = tile[vv + k][pc];
+      store8(dst + (bb * C + c) * nn + v, pack8<T>(o8));
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void to_position_major8_kernel(const T* __restrict__ src, int C, T* __restrict__ dst,
+                                                                 int64_t nn) {
+  __shared__ float tile[64][65];
+  const int64_t vtiles = (nn + 63) / 64;
+  const int ctiles = (C + 63) / 64;
+  int64_t id = blockIdx.x;
+  const int ct = (int)(id % ctiles);
+  id /= ctiles;
+  const int64_t vt = id % vtiles;
+  const int64_t bb = id / vtiles;
+  const int64_t v0 = vt * 64;
+  const int cb = ct * 64;
+  for (int e = threadIdx.x; e < 512; e += 256) {
+    const int pc = e >> 3, vv = (e & 7) * 8;
+    const int64_t v = v0 + vv;
+    const int c = cb + pc;
+    float val[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (v < nn && c < C) to_f32x8(load8(src + (bb * C + c) * nn + v), val);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tile[pc][vv + k] = val[k];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < 512; e += 256) {
+    const int pv = e >> 3, cc = (e & 7) * 8;
+    const int64_t v = v0 + pv;
+    const int c = cb + cc;
+    if (v < nn && c < C) {
+      float o8[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) o8[k] = tile[cc + k][pv];
+      store8(dst + (bb * nn + v) * C + c, pack8<T>(o8));
+    }
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -354,13 +439,20 @@ template <typename T>
 void launch_to_channel_major(const T* src, int64_t ld, int c0, int C, const T* mask, T* dst, int64_t batch, int64_t n,
                              int t, hipStream_t st) {
   const int64_t blocks = batch * ((n * n + 63) / 64) * ((C + 63) / 64);
-  hipLaunchKernelGGL(to_channel_major_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, ld, c0, C, mask, dst,
-                     n, t);
+  if (C % 8 == 0 && ld % 8 == 0 && c0 % 8 == 0 && (n * n) % 8 == 0 && al16(src) && al16(dst))
+    hipLaunchKernelGGL(to_channel_major8_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, ld, c0, C, mask,
+                       dst, n, t);
+  else
+    hipLaunchKernelGGL(to_channel_major_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, ld, c0, C, mask, dst,
+                       n, t);
 }
 template <typename T>
 void launch_to_position_major(const T* src, int C, T* dst, int64_t batch, int64_t nn, hipStream_t st) {
   const int64_t blocks = batch * ((nn + 63) / 64) * ((C + 63) / 64);
-  hipLaunchKernelGGL(to_position_major_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, C, dst, nn);
+  if (C % 8 == 0 && nn % 8 == 0 && al16(src) && al16(dst))
+    hipLaunchKernelGGL(to_position_major8_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, C, dst, nn);
+  else
+    hipLaunchKernelGGL(to_position_major_kernel<T>, dim3((unsigned)blocks), dim3(256), 0, st, src, C, dst, nn);
 }
 template <typename T>
 void launch_split_qk(const T* src, int64_t ld, int64_t c0, T* dst, int64_t rows, int64_t n, int64_t np, int heads,
