@@ -601,7 +601,7 @@ int trimul_generic_run(const fjx_trimul_args* a, hipStream_t st) {
 }
 
 struct GenTriAttnWs {
-  size_t xn, proj, bias_pm, q, k, vt, bias, mb, o, y, flags, total;
+  size_t xn, proj, bias_pm, q, k, vt, bias, mb, o, wcat, flags, total;
 };
 GenTriAttnWs gen_triattn_ws(int64_t batch, int64_t n, int64_t c_z, int64_t heads, int32_t dtype) {
   const int64_t np = round64(n), hd = 32 * heads;
@@ -622,7 +622,7 @@ GenTriAttnWs gen_triattn_ws(int64_t batch, int64_t n, int64_t c_z, int64_t heads
   w.bias = take((size_t)batch * heads * np * np * es);
   w.mb = take((size_t)batch * n * np * sizeof(float));
   w.o = take(pos * hd);
-  w.y = take(pos * c_z);
+  w.wcat = take((size_t)4 * hd * c_z * es);  // w_q | w_k | w_v | w_g back to back (one projection GEMM)
   w.flags = take(flash_flags_bytes(batch, n, heads, np));
   w.total = off;
   return w;
@@ -642,12 +642,34 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
   int rc = timed(K_TRIATTN_PROLOGUE, st, "triattn_prologue", [&] {
     launch_ln_grid<T>(static_cast<const T*>(a->x), static_cast<const T*>(a->norm_weight),
                       static_cast<const T*>(a->norm_bias), xn, B, n, (int)cz, a->eps, t, st);
+    // q | k | v | sigmoid(g) as one GEMM over the weights back to back (the
+    // caller's, when they already are; else a copy in the workspace)
     const void* wq[4] = {a->q_weight, a->k_weight, a->v_weight, a->g_weight};
-    for (int j = 0; j < 4; ++j) {
-      if (!wq[j]) continue;
-      GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, wq[j], hd, proj + j * hd, 4 * hd);
-      g.act = j == 3 ? 1 : 0;
+    const int nw = a->g_weight ? 4 : 3;
+    const size_t wbytes = (size_t)hd * cz * sizeof(T);
+    bool contiguous = true;
+    for (int j = 1; j < nw; ++j)
+      contiguous = contiguous && static_cast<const char*>(wq[j]) == static_cast<const char*>(wq[0]) + j * wbytes;
+    const T* wcat = static_cast<const T*>(a->q_weight);
+    bool ok = true;
+    if (!contiguous) {
+      T* dst = at<T>(W, ws.wcat);
+      for (int j = 0; j < nw && ok; ++j)
+        ok = hipMemcpyAsync(reinterpret_cast<char*>(dst) + j * wbytes, wq[j], wbytes, hipMemcpyDeviceToDevice, st) ==
+             hipSuccess;
+      wcat = dst;
+    }
+    if (ok) {
+      GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, wcat, nw * hd, proj, 4 * hd);
+      g.act = 1;  // sigmoid on the gate columns only
+      g.act_col0 = 3 * hd;
       launch_gemm<T, T>(g, st);
+    } else {
+      for (int j = 0; j < nw; ++j) {
+        GemmParams<T, T> g = rows_gemm<T>(xn, rows, cz, wq[j], hd, proj + j * hd, 4 * hd);
+        g.act = j == 3 ? 1 : 0;
+        launch_gemm<T, T>(g, st);
+      }
     }
     launch_gemm<T, T>(rows_gemm<T>(xn, rows, cz, a->bias_weight, H, bpm, H), st);
     launch_split_qk<T>(proj, 4 * hd, 0, at<T>(W, ws.q), B * n, n, np, (int)H,
@@ -681,10 +703,15 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
 
   return timed(K_TRIATTN_EPILOGUE, st, "triattn_epilogue", [&] {
     if (a->g_weight) launch_gate_rows<T>(fp.out, proj, 4 * hd, 3 * hd, rows, (int)hd, st);
-    T* y = at<T>(W, ws.y);
-    launch_gemm<T, T>(rows_gemm<T>(fp.out, rows, hd, a->o_weight, cz, y, cz), st);
-    launch_scatter_add<T>(y, nullptr, static_cast<const T*>(a->residual), static_cast<const T*>(a->out_mask),
-                          static_cast<T*>(a->out), rows, n, (int)cz, t, st);
+    // the output projection stores straight into the original grid (the
+    // ending node's rows transposed) with the residual and the output mask
+    GemmParams<T, T> g = rows_gemm<T>(fp.out, rows, hd, a->o_weight, cz, static_cast<T*>(a->out), cz);
+    g.proj_round = 1;
+    g.residual = static_cast<const T*>(a->residual);
+    g.row_gate = static_cast<const T*>(a->out_mask);
+    g.map_t = t;
+    g.map_n = n;
+    launch_gemm<T, T>(g, st);
   });
 }
 

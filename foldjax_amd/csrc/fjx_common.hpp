@@ -116,6 +116,16 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
 
+// pair-grid row r = b n^2 + i n + j -> b n^2 + j n + i when t is set
+__device__ __forceinline__ int64_t grid_row(int64_t r, int64_t n, int t) {
+  if (!t) return r;
+  const int64_t nn = n * n;
+  const int64_t b = r / nn;
+  const int64_t v = r - b * nn;
+  const int64_t i = v / n;
+  return b * nn + (v - i * n) * n + i;
+}
+
 // wave-wide xor shuffle of a float (64 lanes)
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 

@@ -156,8 +156,9 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
       const int act = col >= P.act_col0 ? P.act : 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int64_t row = m0 + wm + 16 * i + 4 * lg + q;
-        if (row >= M) continue;
+        const int64_t row0 = m0 + wm + 16 * i + 4 * lg + q;
+        if (row0 >= M) continue;
+        const int64_t row = grid_row(row0, P.map_n, P.map_t);
         float v = acc[i][j][q] + bias;
         if (act == 1) v = fast_sigmoid(v);
         else if (act == 2) v *= fast_sigmoid(v);  // silu

@@ -243,8 +243,9 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
         bias[q] = P.bias && (P.bias_n == 0 || col + q < P.bias_n) ? to_f32(P.bias[col + q]) : 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int64_t row = cur.m0 + wm + 16 * i + li;
-        if (row >= M) continue;
+        const int64_t row0 = cur.m0 + wm + 16 * i + li;
+        if (row0 >= M) continue;
+        const int64_t row = grid_row(row0, P.map_n, P.map_t);
         const bool zero_row = P.row_gate && to_f32(P.row_gate[row]) == 0.f;
         const int64_t off = row * P.ldc + col;
         float v[4];
@@ -301,7 +302,10 @@ bool gemm_dma_ok(const GemmParams<bf16, bf16>& p) {
                   p.lda * 2 * (int64_t)kGT < (int64_t)kGOob && p.ldb * 2 * (int64_t)kGT < (int64_t)kGOob &&
                   p.ldc * 2 * (int64_t)kGT < (int64_t)kGOob;
   const int64_t total = p.batches * ((p.m + kGT - 1) / kGT) * ((p.n + kGT - 1) / kGT);
-  return ok && total >= kMinTiles && (!p.swiglu || (p.n % kGT == 0 && !p.gate && !p.residual && !p.proj_round));
+  // at least half a tile of columns: narrower products (a triangle bias of a
+  // few heads) would waste most of every tile
+  return ok && total >= kMinTiles && p.n >= kGT / 2 &&
+         (!p.swiglu || (p.n % kGT == 0 && !p.gate && !p.residual && !p.proj_round && !p.map_t));
 }
 
 bool launch_gemm_dma(const GemmParams<bf16, bf16>& p, hipStream_t st) {

@@ -107,6 +107,11 @@ struct GemmParams {
   // (the order of a transition's row mask and residual)
   int proj_round;
   const TO* row_scale;  // [m] or null (with proj_round)
+  // map_t: row r of the product is stored at, and reads its residual and
+  // row gate from, the transposed pair-grid position: with N = map_n,
+  // r = b N^2 + i N + j goes to b N^2 + j N + i (the ending node's grid)
+  int map_t;
+  int64_t map_n;
   // pair mode (launch_gemm_dma only): B holds two weights interleaved in
   // blocks of 128 rows (a block of the first, then the block of the second
   // for the same 128 output units), n = 2 units, and C[i][u] combines a and b
@@ -255,8 +260,5 @@ void launch_grid_mask_bias(const T* mask, float* mb, int64_t batch, int64_t n, i
                            hipStream_t st);
 template <typename T>
 void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, int width, hipStream_t st);
-template <typename T>
-void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
-                        int64_t n, int c, int t, hipStream_t st);
 
 }  // namespace fjx

@@ -10,6 +10,8 @@ same values (fp32: max-abs <= 1e-4; bf16: relative <= 2e-2):
 
 from __future__ import annotations
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -230,3 +232,49 @@ def test_triattn_wide_dma_gemm_bf16(starting):
     rows = mv.max(axis=1) > 0
     g, w_ = (to_np(got)[rows], want[rows]) if starting else (to_np(got)[:, rows], want[:, rows])
     assert_parity(g, w_, dtype, f"triattn c={c} n={n} starting={starting}")
+
+
+@pytest.mark.parametrize("c_z,heads,n", [(128, 4, 40), (64, 4, 33), (384, 8, 20), (384, 8, 96)])
+@pytest.mark.parametrize("starting", [True, False])
+def test_ungated_triattn_is_twice_the_zero_gate(c_z, heads, n, starting):
+    """An ungated module (g_weight None) on the fused, narrow and general
+    paths, pinned to the oracle: with W_g = 0 the gate is sigmoid(0) = 1/2 at
+    every position, so the ungated update is exactly twice the oracle's update
+    with a zero gate weight (bf16; the halving is exact)."""
+    dtype = DTYPES["bf16"]
+    say(f"ungated triattn c_z={c_z} heads={heads} n={n} starting={starting}")
+    z = syn.pair_input(n, c_z, seed=51)
+    m = mask_case("tail", n)
+    w = syn.triattn_weights(c_z, heads, 32, seed=52)
+    w["attention"]["linear_g"]["weight"] = np.zeros_like(w["attention"]["linear_g"]["weight"])
+    packed = dataclasses.replace(P.pack_triattn_protenix(P.triattn_to_protenix(w), dtype, "cuda"), g_weight=None)
+    got = kernels.triattn(device_tensor(z, dtype), device_tensor(m, dtype), packed, starting=starting)
+    torch.cuda.synchronize()
+    want = 2.0 * O.protenix_triangle_attention(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), num_heads=heads,
+                                               starting=starting)
+    mv = m if starting else m.T
+    rows = mv.max(axis=1) > 0
+    g, w_ = (to_np(got)[rows], want[rows]) if starting else (to_np(got)[:, rows], want[:, rows])
+    assert_parity(g, w_, dtype, f"ungated triattn c_z={c_z} starting={starting}")
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_general_triattn_weights_back_to_back_match_separate(starting):
+    """The general tri-attn path projects q|k|v|g in one GEMM: over the
+    caller's weights when they sit back to back in one buffer, else over a
+    copy in the workspace. Both give the same bits (c_z = 384, 8 heads,
+    n = 96, bf16)."""
+    dtype = DTYPES["bf16"]
+    n, c, heads = 96, 384, 8
+    say(f"triattn back-to-back weights n={n} starting={starting}")
+    z = device_tensor(syn.pair_input(n, c, seed=53), dtype)
+    m = device_tensor(mask_case("random", n), dtype)
+    sep = P.pack_triattn_protenix(P.triattn_to_protenix(syn.triattn_weights(c, heads, 32, seed=54)), dtype, "cuda")
+    cat = torch.cat([sep.q_weight, sep.k_weight, sep.v_weight, sep.g_weight], dim=0)
+    hd = sep.q_weight.shape[0]
+    b2b = dataclasses.replace(sep, q_weight=cat[:hd], k_weight=cat[hd:2 * hd], v_weight=cat[2 * hd:3 * hd],
+                              g_weight=cat[3 * hd:])
+    a = kernels.triattn(z, m, sep, starting=starting, residual=z)
+    b = kernels.triattn(z, m, b2b, starting=starting, residual=z)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
