@@ -55,9 +55,11 @@ namespace {
 //   operands with the contracted axis contiguous), each
 //   mask * sigmoid(x_ln g_in^T) * (x_ln p_in^T).
 // kNarrow: x has P.cw < 128 channels (a multiple of 32); the tile's channels
-// past cw are held at zero (zero LayerNorm affine, zero weight columns).
+// past cw are held at zero (zero LayerNorm affine, zero weight columns). NB:
+// the 32-channel blocks of x worked on (cw / 32 when it is known at compile
+// time, else all 4, the ones past cw being zero).
 // ---------------------------------------------------------------------------
-template <typename T, bool kNarrow>
+template <typename T, bool kNarrow, int NB = 4>
 __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulPrologueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
   __shared__ __attribute__((aligned(16))) float mrow[kTP];
@@ -78,8 +80,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
 
   WSlab<T> wp, wg;
   if constexpr (kNarrow) {
-    load_wslab_w<T>(P.w_p + (int64_t)half * kC * cw, cw, col0, wp, kC, cw);
-    load_wslab_w<T>(P.w_g + (int64_t)half * kC * cw, cw, col0, wg, kC, cw);
+    load_wslab_w<T, NB>(P.w_p + (int64_t)half * kC * cw, cw, col0, wp, kC, cw);
+    load_wslab_w<T, NB>(P.w_g + (int64_t)half * kC * cw, cw, col0, wg, kC, cw);
     stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
   } else {
     load_wslab<T>(P.w_p + (int64_t)half * kC * kC, col0, wp);
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     auto pos_of = [&](int ss) {
       return (int64_t)tl.b * nn + (P.transpose ? (int64_t)ss * n + tl.r : (int64_t)tl.r * n + ss);
     };
-    if constexpr (kNarrow) load_row_part_w<T>(valid ? P.x + pos_of(s) * cw : nullptr, xr, cw);
+    if constexpr (kNarrow) load_row_part_w<T, NB>(valid ? P.x + pos_of(s) * cw : nullptr, xr, cw);
     else load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
     mvalid = valid;
     if (P.mask) mraw = P.mask[pos_of(valid ? s : tl.s0)];
@@ -112,7 +114,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
   for (; tile < ntiles; tile += gridDim.x) {
     const TileRS tl = tile_at(tile, ntx, n);
     const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
-    ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
+    ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
     if ((t & 3) == 0) mrow[p] = mvalid ? (P.mask ? to_f32(mraw) : 1.0f) : 0.f;
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
@@ -124,7 +126,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     for (int j = 0; j < kTP / 32; ++j) {
       f32x4 ap[2][2], ag[2][2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) tile_mma2_row<T, false>(xs, paired_row(j, h, lane & 15), wp, wg, ap[h], ag[h]);
+      for (int h = 0; h < 2; ++h) tile_mma2_row<T, false, NB>(xs, paired_row(j, h, lane & 15), wp, wg, ap[h], ag[h]);
       const int p0 = 32 * j + 8 * (lane >> 4);
       const f32x4 m0 = *reinterpret_cast<const f32x4*>(&mrow[p0]);
       const f32x4 m1 = *reinterpret_cast<const f32x4*>(&mrow[p0 + 4]);
@@ -153,9 +155,9 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
 //   bias [B][H][Np][Np]  x_ln w_bias^T times log2 e (in T)
 //   mb [B][N][Np] fp32   inf*(mask-1)*log2 e, -inf for keys >= N
 // Np = N rounded up to 64; key slots in [N, Np) are written as zeros.
-// kNarrow: x has P.cw < 128 channels, as for the tri-mul prologue.
+// kNarrow and NB: x has P.cw < 128 channels, as for the tri-mul prologue.
 // ---------------------------------------------------------------------------
-template <typename T, bool kNarrow>
+template <typename T, bool kNarrow, int NB = 4>
 __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnPrologueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
   __shared__ __attribute__((aligned(16))) LnAffine ln;
@@ -181,14 +183,14 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   if (role == 0) {
     // paired: lane group g holds head dims 8g .. +7, a quarter of a q/k row
     if constexpr (kNarrow) {
-      load_wslab_paired_w<T>(P.w_q, cw, col0, w1, kC, cw);
-      load_wslab_paired_w<T>(P.w_k, cw, col0, w2, kC, cw);
+      load_wslab_paired_w<T, NB>(P.w_q, cw, col0, w1, kC, cw);
+      load_wslab_paired_w<T, NB>(P.w_k, cw, col0, w2, kC, cw);
     } else {
       load_wslab_paired<T>(P.w_q, col0, w1);
       load_wslab_paired<T>(P.w_k, col0, w2);
     }
   } else {
-    if constexpr (kNarrow) load_wslab_w<T>(P.w_v, cw, col0, w1, kC, cw);
+    if constexpr (kNarrow) load_wslab_w<T, NB>(P.w_v, cw, col0, w1, kC, cw);
     else load_wslab<T>(P.w_v, col0, w1);
     const int li = lane & 15;
     const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -213,7 +215,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
     auto pos_of = [&](int ss) {
       return (int64_t)tl.b * nn + (P.transpose ? (int64_t)ss * n + tl.r : (int64_t)tl.r * n + ss);
     };
-    if constexpr (kNarrow) load_row_part_w<T>(valid ? P.x + pos_of(s) * cw : nullptr, xr, cw);
+    if constexpr (kNarrow) load_row_part_w<T, NB>(valid ? P.x + pos_of(s) * cw : nullptr, xr, cw);
     else load_row_part<T>(valid ? P.x + pos_of(s) * kC : nullptr, xr);
     mvalid = valid;
     if (P.mask) mraw = P.mask[pos_of(valid ? s : tl.s0)];
@@ -226,7 +228,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
     const TileRS tl = tile_at(tile, ntx, n);
     const int nstore = (int)min<int64_t>(kTP, np - tl.s0);  // incl. zero padding; a multiple of 64
     const int nreal = (int)max<int64_t>(0, min<int64_t>(kTP, n - tl.s0));
-    ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
+    ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
     if ((t & 3) == 0 && p < nstore) {
       const float mv = P.mask ? to_f32(mraw) : 1.0f;
       P.mb[((int64_t)tl.b * n + tl.r) * np + tl.s0 + p] = mvalid ? P.inf * (mv - 1.0f) * kLog2e : -INFINITY;
@@ -245,7 +247,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
       for (int rt = 0; rt < 8; ++rt) {
         const int pp = 16 * rt + (lane & 15);
         f32x4 aq[2], ak[2];
-        tile_mma2<T, true>(xs, rt, w1, w2, aq, ak);
+        tile_mma2<T, true, NB>(xs, rt, w1, w2, aq, ak);
         if (pp < nstore) {
           const bool real = pp < nreal;
           float vq[8], vk[8];
@@ -270,7 +272,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
         const int p0 = 32 * j + 8 * (lane >> 4);
         f32x4 av[2][2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) tile_mma_row<T, false>(xs, paired_row(j, h, lane & 15), w1, av[h]);
+        for (int h = 0; h < 2; ++h) tile_mma_row<T, false, NB>(xs, paired_row(j, h, lane & 15), w1, av[h]);
         if (p0 < nstore) {  // nstore is a multiple of 64: all 8 positions are stored
 #pragma unroll
           for (int ct = 0; ct < 2; ++ct) {
@@ -288,7 +290,7 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
         const int p0 = 32 * j + 8 * (lane >> 4);
         f32x4 ab[2][2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) tile_mma_row<T, false>(xs, paired_row(j, h, lane & 15), w2, ab[h]);
+        for (int h = 0; h < 2; ++h) tile_mma_row<T, false, NB>(xs, paired_row(j, h, lane & 15), w2, ab[h]);
         const int hd = lane & 15;
         if (hd < H && p0 < nstore) {
           float v[8];
@@ -328,9 +330,10 @@ constexpr int kTE = 64;
 // flight -- the previous row tile's store and the next tile's prefetch.
 // kNarrow: x, the residual and out have P.cw < 128 channels (a multiple of
 // 32); o keeps 128. The waves whose output channels start at or past cw
-// only help fill the LDS tiles.
+// only help fill the LDS tiles. NB as for the prologues (the x side only: o
+// and its LayerNorm keep 128 channels).
 // ---------------------------------------------------------------------------
-template <typename T, bool kResX, bool kNarrow>
+template <typename T, bool kResX, bool kNarrow, int NB = 4>
 __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpilogueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xg[kTE][kLd];    // LN_in(x)
   __shared__ __attribute__((aligned(16))) T xp[kTE][kLd];    // LN_out(o)
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 
   WSlab<T> wg, wp;
   if constexpr (kNarrow) {
-    load_wslab_paired_w<T>(P.w_gout, cw, col0, wg, cw, cw);
+    load_wslab_paired_w<T, NB>(P.w_gout, cw, col0, wg, cw, cw);
     load_wslab_paired_w<T>(P.w_pout, kC, col0, wp, cw, kC);
     stage_ln_w<T>(P.ln_in_w, P.ln_in_b, ln_in, cw);
   } else {
@@ -378,7 +381,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
-    if constexpr (kNarrow) load_row_part_w<T>(p < nvalid ? P.x + (pos0 + p) * cw : nullptr, xr, cw);
+    if constexpr (kNarrow) load_row_part_w<T, NB>(p < nvalid ? P.x + (pos0 + p) * cw : nullptr, xr, cw);
     else load_row_part<T>(p < nvalid ? P.x + (pos0 + p) * kC : nullptr, xr);
     // channel-major: channel ch of the tile at src + ch * nn; tile-blocked:
     // the whole tile is one contiguous [128][64] block
@@ -411,7 +414,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     const int64_t pos0 = (int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0;
 
-    if (res_x) store_row_part<T>(xr, &xraw[p][0]);
+    if (res_x) store_row_part<T, NB>(xr, &xraw[p][0]);
     // the output gate of this tile (bit rt: row tile rt is kept), taken
     // before the next fetch replaces om
     uint32_t keep = (1u << (kTE / 16)) - 1;
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 #pragma unroll
       for (int rt = 0; rt < kTE / 16; ++rt) keep |= to_f32(om[rt]) != 0.f ? 1u << rt : 0u;
     }
-    ln_quad<T>(xr, ln_in, P.eps, &xg[p][0], cw);
+    ln_quad<T, T, NB>(xr, ln_in, P.eps, &xg[p][0], cw);
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       int ch, p0;
@@ -441,7 +444,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 #pragma unroll 2
     for (int rt = 0; rt < (active ? kTE / 16 : 0); ++rt) {
       f32x4 ag[2], ap[2];
-      tile_mma<T, true>(xg, rt, wg, ag);
+      tile_mma<T, true, NB>(xg, rt, wg, ag);
       tile_mma<T, true>(xp, rt, wp, ap);
       // paired slabs: this lane holds channels col0 + 8g .. +7 of position pp
       const int pp = 16 * rt + (lane & 15);
@@ -477,10 +480,10 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 //   out[orig] = T(o[r,s] * sigmoid(LN(x[orig]) w_g^T)) w_o^T (+ residual[orig])
 // with o position-major [B][N*N][128] and orig = (r, s) or (s, r). 256
 // threads: wave w owns output channels 32w .. 32w+31 of both products for the
-// 64 positions, holding the w_g and w_o slabs. kResX and kNarrow as for the
-// tri-mul epilogue (o and the gate keep 128 channels).
+// 64 positions, holding the w_g and w_o slabs. kResX, kNarrow and NB as for
+// the tri-mul epilogue (o and the gate keep 128 channels).
 // ---------------------------------------------------------------------------
-template <typename T, bool kResX, bool kNarrow>
+template <typename T, bool kResX, bool kNarrow, int NB = 4>
 __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpilogueParams<T> P, int64_t ntiles) {
   __shared__ __attribute__((aligned(16))) T xs[kTE][kLd];    // LN(x)
   __shared__ __attribute__((aligned(16))) T xo[kTE][kLd];    // gated o
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
   // col0 + 8g .. +7, so o, the residual and the output move 16 bytes a lane
   WSlab<T> wg, wo;
   if constexpr (kNarrow) {
-    if (gated) load_wslab_paired_w<T>(P.w_g, cw, col0, wg, kC, cw);
+    if (gated) load_wslab_paired_w<T, NB>(P.w_g, cw, col0, wg, kC, cw);
     load_wslab_paired_w<T>(P.w_o, kC, col0, wo, cw, kC);
     if (gated) stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
   } else {
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
     if constexpr (kNarrow) {
-      if (need_x) load_row_part_w<T>(p < nvalid ? P.x + orig_of(tl, p) * cw : nullptr, xr, cw);
+      if (need_x) load_row_part_w<T, NB>(p < nvalid ? P.x + orig_of(tl, p) * cw : nullptr, xr, cw);
     } else {
       if (need_x) load_row_part<T>(p < nvalid ? P.x + orig_of(tl, p) * kC : nullptr, xr);
     }
@@ -557,7 +560,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     const TileRS tl = tile_at(tile, ntx, n, kTE);
     const int nvalid = (int)min<int64_t>(kTE, n - tl.s0);
 
-    if (res_x) store_row_part<T>(xr, &xraw[p][0]);
+    if (res_x) store_row_part<T, NB>(xr, &xraw[p][0]);
     // the output gate of this tile (bit rt: row tile rt is kept), taken
     // before the next fetch replaces om
     uint32_t keep = (1u << (kTE / 16)) - 1;
@@ -567,12 +570,12 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
       for (int rt = 0; rt < kTE / 16; ++rt) keep |= to_f32(om[rt]) != 0.f ? 1u << rt : 0u;
     }
     if (gated) {
-      ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
+      ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
       __syncthreads();
 #pragma unroll
       for (int rt = 0; rt < kTE / 16; ++rt) {
         f32x4 ag[2];
-        tile_mma<T, true>(xs, rt, wg, ag);
+        tile_mma<T, true, NB>(xs, rt, wg, ag);
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
@@ -631,27 +634,33 @@ void launch_persistent(void (*kern)(P, int64_t), const P& p, int threads, int64_
 template <typename T>
 void launch_trimul_prologue(const TriMulPrologueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTP - 1) / kTP * p.n * batch;
-  launch_persistent(p.cw ? trimul_prologue_kernel<T, true> : trimul_prologue_kernel<T, false>, p, 512, ntiles, st);
+  launch_persistent(p.cw == 64 ? trimul_prologue_kernel<T, true, 2>
+                    : p.cw ? trimul_prologue_kernel<T, true> : trimul_prologue_kernel<T, false>,
+                    p, 512, ntiles, st);
 }
 template <typename T>
 void launch_triattn_prologue(const TriAttnPrologueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.np + kTP - 1) / kTP * p.n * batch;
-  launch_persistent(p.cw ? triattn_prologue_kernel<T, true> : triattn_prologue_kernel<T, false>, p, 512, ntiles, st);
+  launch_persistent(p.cw == 64 ? triattn_prologue_kernel<T, true, 2>
+                    : p.cw ? triattn_prologue_kernel<T, true> : triattn_prologue_kernel<T, false>,
+                    p, 512, ntiles, st);
 }
 template <typename T>
 void launch_trimul_epilogue(const TriMulEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
   const bool res_x = p.residual && p.residual == p.x;
-  auto kern = res_x ? (p.cw ? trimul_epilogue_kernel<T, true, true> : trimul_epilogue_kernel<T, true, false>)
-                    : (p.cw ? trimul_epilogue_kernel<T, false, true> : trimul_epilogue_kernel<T, false, false>);
+  auto kern = p.cw == 64 ? (res_x ? trimul_epilogue_kernel<T, true, true, 2> : trimul_epilogue_kernel<T, false, true, 2>)
+              : res_x ? (p.cw ? trimul_epilogue_kernel<T, true, true> : trimul_epilogue_kernel<T, true, false>)
+                      : (p.cw ? trimul_epilogue_kernel<T, false, true> : trimul_epilogue_kernel<T, false, false>);
   launch_persistent(kern, p, 256, ntiles, st);
 }
 template <typename T>
 void launch_triattn_epilogue(const TriAttnEpilogueParams<T>& p, int64_t batch, hipStream_t st) {
   const int64_t ntiles = (p.n + kTE - 1) / kTE * p.n * batch;
   const bool res_x = p.residual && p.residual == p.x;
-  auto kern = res_x ? (p.cw ? triattn_epilogue_kernel<T, true, true> : triattn_epilogue_kernel<T, true, false>)
-                    : (p.cw ? triattn_epilogue_kernel<T, false, true> : triattn_epilogue_kernel<T, false, false>);
+  auto kern = p.cw == 64 ? (res_x ? triattn_epilogue_kernel<T, true, true, 2> : triattn_epilogue_kernel<T, false, true, 2>)
+              : res_x ? (p.cw ? triattn_epilogue_kernel<T, true, true> : triattn_epilogue_kernel<T, true, false>)
+                      : (p.cw ? triattn_epilogue_kernel<T, false, true> : triattn_epilogue_kernel<T, false, false>);
   launch_persistent(kern, p, 256, ntiles, st);
 }
 

@@ -65,37 +65,39 @@ __device__ __forceinline__ void load_row_part(const T* __restrict__ src, RowPart
 }
 // the same for a row of cw channels (a multiple of 32): the chunks past cw
 // are zero
-template <typename T>
+// NB (the compile-time number of 32-channel blocks, cw / 32 when known):
+// only the first NB chunks of a row part are loaded, normalised or stored
+template <typename T, int NB = 4>
 __device__ __forceinline__ void load_row_part_w(const T* __restrict__ src, RowPart<T>& r, int cw) {
   const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int q = 0; q < 4; ++q) r.f[q] = src && 32 * q < cw ? load8(src + row_chunk(q)) : pack8<T>(z);
+  for (int q = 0; q < NB; ++q) r.f[q] = src && 32 * q < cw ? load8(src + row_chunk(q)) : pack8<T>(z);
 }
-template <typename T>
+template <typename T, int NB = 4>
 __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restrict__ dst_row) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) store8(dst_row + row_chunk(q), r.f[q]);
+  for (int q = 0; q < NB; ++q) store8(dst_row + row_chunk(q), r.f[q]);
 }
 
 // LayerNorm of 128 channels held by 4 consecutive threads (the chunks of
 // load_row_part); put(c, o) receives the 8 outputs of channels c .. c+7.
 // cw < 128: the statistics are those of the first cw channels (the chunks
 // past cw hold zeros and are left out of the variance)
-template <typename T, typename Put>
+template <typename T, typename Put, int NB = 4>
 __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine& l, float eps, Put put, int cw = kC) {
-  float v[32];
+  float v[8 * NB];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) to_f32x8(r.f[q], v + 8 * q);
+  for (int q = 0; q < NB; ++q) to_f32x8(r.f[q], v + 8 * q);
   float s = 0.f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) s += v[e];
+  for (int e = 0; e < 8 * NB; ++e) s += v[e];
   s += shfl_xor(s, 1);
   s += shfl_xor(s, 2);
   const float inv_c = cw == kC ? 1.0f / kC : 1.0f / (float)cw;
   const float mean = s * inv_c;
   float q2 = 0.f;
 #pragma unroll
-  for (int e = 0; e < 32; ++e) {
+  for (int e = 0; e < 8 * NB; ++e) {
     const float d = v[e] - mean;
     if (cw == kC || 32 * (e / 8) < cw) q2 += d * d;
   }
@@ -104,7 +106,7 @@ __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine&
   const float rstd = __builtin_amdgcn_rsqf(q2 * inv_c + eps);
   const float shift = -mean * rstd;
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
+  for (int q = 0; q < NB; ++q) {
     // one 8-channel chunk at a time: keeps the scheduler from hoisting all 16
     // affine reads (64 VGPRs) ahead of the arithmetic
     __builtin_amdgcn_sched_barrier(0);
@@ -124,10 +126,11 @@ __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine&
 }
 
 // ... written to the same channels of dst_row as TO
-template <typename T, typename TO>
+template <typename T, typename TO, int NB = 4>
 __device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row,
                                         int cw = kC) {
-  ln_quad_put(r, l, eps, [&](int c, const float* o) { store8(dst_row + c, pack8<TO>(o)); }, cw);
+  auto put = [&](int c, const float* o) { store8(dst_row + c, pack8<TO>(o)); };
+  ln_quad_put<T, decltype(put), NB>(r, l, eps, put, cw);
 }
 
 // One wave's 32 output channels col0..col0+31 of a [128][128] weight as MFMA
@@ -162,27 +165,27 @@ __device__ __forceinline__ void load_wslab_paired(const T* __restrict__ w, int c
 
 // the same two loaders for a weight with rows ld elements apart, rows >=
 // nrows and columns >= kmax read as zero (a narrow width's padding)
-template <typename T>
+template <typename T, int NB = 4>
 __device__ __forceinline__ void load_wslab_w(const T* __restrict__ w, int64_t ld, int col0, WSlab<T>& wf, int nrows,
                                              int kmax) {
   const int lane = threadIdx.x & 63;
   const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < NB; ++ks)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const int row = col0 + 16 * ct + (lane & 15), k = 32 * ks + 8 * (lane >> 4);
       wf[ks][ct] = row < nrows && k < kmax ? load8(w + (int64_t)row * ld + k) : pack8<T>(z);
     }
 }
-template <typename T>
+template <typename T, int NB = 4>
 __device__ __forceinline__ void load_wslab_paired_w(const T* __restrict__ w, int64_t ld, int col0, WSlab<T>& wf,
                                                     int nrows, int kmax) {
   const int lane = threadIdx.x & 63;
   const int li = lane & 15;
   const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < NB; ++ks)
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
       const int row = col0 + 8 * (li >> 2) + 4 * ct + (li & 3), k = 32 * ks + 8 * (lane >> 4);
@@ -194,12 +197,12 @@ __device__ __forceinline__ void load_wslab_paired_w(const T* __restrict__ w, int
 // feeds (16rt + l%16 for row tile rt):
 //   kTrans = false: acc[ct][q] = D[row of lane 4g + q][ch col0 + 16ct + l%16]
 //   kTrans = true:  acc[ct][q] = D[row of lane l%16][ch col0 + 16ct + 4g + q]
-template <typename T, bool kTrans>
+template <typename T, bool kTrans, int NB = 4>
 __device__ __forceinline__ void tile_mma_row(const T (*xs)[kLd], int row, const WSlab<T>& wf, f32x4 (&acc)[2]) {
   const int lane = threadIdx.x & 63;
   acc[0] = acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < NB; ++ks) {
     const typename Frag<T>::type xf = load8(&xs[row][32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -208,9 +211,9 @@ __device__ __forceinline__ void tile_mma_row(const T (*xs)[kLd], int row, const 
     }
   }
 }
-template <typename T, bool kTrans>
+template <typename T, bool kTrans, int NB = 4>
 __device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab<T>& wf, f32x4 (&acc)[2]) {
-  tile_mma_row<T, kTrans>(xs, 16 * rt + (threadIdx.x & 15), wf, acc);
+  tile_mma_row<T, kTrans, NB>(xs, 16 * rt + (threadIdx.x & 15), wf, acc);
 }
 
 // Rows of the tile pair j (rows 32j .. 32j+31) in paired order: half h of
@@ -220,13 +223,13 @@ __device__ __forceinline__ void tile_mma(const T (*xs)[kLd], int rt, const WSlab
 __device__ __forceinline__ int paired_row(int j, int h, int li) { return 32 * j + 8 * (li >> 2) + 4 * h + (li & 3); }
 
 // the same for two slabs sharing the row fragments
-template <typename T, bool kTrans>
+template <typename T, bool kTrans, int NB = 4>
 __device__ __forceinline__ void tile_mma2_row(const T (*xs)[kLd], int row, const WSlab<T>& w1, const WSlab<T>& w2,
                                               f32x4 (&a1)[2], f32x4 (&a2)[2]) {
   const int lane = threadIdx.x & 63;
   a1[0] = a1[1] = a2[0] = a2[1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < NB; ++ks) {
     const typename Frag<T>::type xf = load8(&xs[row][32 * ks + 8 * (lane >> 4)]);
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
@@ -240,10 +243,10 @@ __device__ __forceinline__ void tile_mma2_row(const T (*xs)[kLd], int row, const
     }
   }
 }
-template <typename T, bool kTrans>
+template <typename T, bool kTrans, int NB = 4>
 __device__ __forceinline__ void tile_mma2(const T (*xs)[kLd], int rt, const WSlab<T>& w1, const WSlab<T>& w2,
                                           f32x4 (&a1)[2], f32x4 (&a2)[2]) {
-  tile_mma2_row<T, kTrans>(xs, 16 * rt + (threadIdx.x & 15), w1, w2, a1, a2);
+  tile_mma2_row<T, kTrans, NB>(xs, 16 * rt + (threadIdx.x & 15), w1, w2, a1, a2);
 }
 
 // 4 elements of T packed in registers (two VGPRs for bf16)
@@ -300,14 +303,14 @@ __device__ __forceinline__ void load_wcol(const T* __restrict__ w, int64_t ldw, 
 }
 
 // the same with rows >= nrows and columns k >= kmax (multiples of 8) read as zero
-template <typename T>
+template <typename T, int NB = 4>
 __device__ __forceinline__ void load_wcol_w(const T* __restrict__ w, int64_t ldw, int row0, int64_t k0, WCol<T>& wf,
                                             int nrows, int64_t kmax) {
   const int lane = threadIdx.x & 63;
   const float z[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const int row = row0 + (lane & 15);
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < NB; ++ks) {
     const int64_t k = k0 + 32 * ks + 8 * (lane >> 4);
     wf[ks] = row < nrows && k < kmax ? load8(w + (int64_t)row * ldw + k) : pack8<T>(z);
   }
@@ -315,11 +318,11 @@ __device__ __forceinline__ void load_wcol_w(const T* __restrict__ w, int64_t ldw
 
 // acc += rows 16rt.. of the tile against one 16-column tile, transposed form:
 // acc[q] = D[pos 16rt + l%16][col 4g + q]
-template <typename T>
+template <typename T, int NB = 4>
 __device__ __forceinline__ void tile_mma1_acc(const T (*xs)[kLd], int rt, const WCol<T>& wf, f32x4& acc) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks)
+  for (int ks = 0; ks < NB; ++ks)
     mma(acc, wf[ks], load8(&xs[16 * rt + (lane & 15)][32 * ks + 8 * (lane >> 4)]));
 }
 

@@ -181,7 +181,7 @@ __device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, 
 // the hidden width is 4 cw; the tile works at 128 channels with the ones past
 // cw at zero (zero affine, zero weight rows and columns), in cw / 32 hidden
 // chunks, and stores only the first cw channels
-template <typename T, bool kPbF32, bool kNarrow = false>
+template <typename T, bool kPbF32, bool kNarrow = false, int NB = 4>
 __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P) {
   using namespace tile;
   __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];  // LN(x)
@@ -204,7 +204,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   {
     RowPart<T> xr;
     if constexpr (kNarrow) {
-      load_row_part_w<T>(p < nvalid ? P.x + (m0 + p) * cw : nullptr, xr, cw);
+      load_row_part_w<T, NB>(p < nvalid ? P.x + (m0 + p) * cw : nullptr, xr, cw);
       stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
     } else {
       load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
@@ -216,7 +216,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
       stage_wz_split(P, wz);
     }
     __syncthreads();
-    ln_quad<T>(xr, ln, P.eps, &xs[p][0], cw);
+    ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
   }
   __syncthreads();
 
@@ -228,8 +228,8 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   for (int ch = 0; ch < nch; ++ch) {
     WCol<T> wa, wb, wo;
     if constexpr (kNarrow) {
-      load_wcol_w<T>(P.w_a, cw, ch * kC + col, 0, wa, 4 * cw, cw);
-      load_wcol_w<T>(P.w_b, cw, ch * kC + col, 0, wb, 4 * cw, cw);
+      load_wcol_w<T, NB>(P.w_a, cw, ch * kC + col, 0, wa, 4 * cw, cw);
+      load_wcol_w<T, NB>(P.w_b, cw, ch * kC + col, 0, wb, 4 * cw, cw);
       load_wcol_w<T>(P.w_o, 4 * cw, col, ch * kC, wo, cw, 4 * cw);
     } else {
       load_wcol<T>(P.w_a, kC, ch * kC + col, 0, wa);
@@ -239,8 +239,8 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
 #pragma unroll 2
     for (int rt = 0; rt < 8; ++rt) {
       f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f}, b = f32x4{0.f, 0.f, 0.f, 0.f};
-      tile_mma1_acc<T>(xs, rt, wa, a);
-      tile_mma1_acc<T>(xs, rt, wb, b);
+      tile_mma1_acc<T, NB>(xs, rt, wa, a);
+      tile_mma1_acc<T, NB>(xs, rt, wb, b);
       float h[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) h[q] = silu(a[q]) * b[q];
@@ -327,9 +327,9 @@ template <typename T>
 __global__ __launch_bounds__(512) void transition128_kernel(TransitionParams<T> P) {
   transition128_body<T, false>(P);
 }
-template <typename T>
+template <typename T, int NB>
 __global__ __launch_bounds__(512) void transition_narrow_kernel(TransitionParams<T> P) {
-  transition128_body<T, false, true>(P);
+  transition128_body<T, false, true, NB>(P);
 }
 // two 512-thread workgroups (70 KB of LDS each) share a CU only at 4 waves
 // per SIMD, so this variant is held to 128 VGPRs as the plain one fits
@@ -346,7 +346,9 @@ template <typename T>
 void launch_transition(const TransitionParams<T>& p, int c, hipStream_t st) {
   const dim3 grid((unsigned)((p.rows + tile::kTP - 1) / tile::kTP));
   if (c < tile::kC) {
-    hipLaunchKernelGGL(transition_narrow_kernel<T>, grid, dim3(512), 0, st, p);
+    // c = 64 (the template stack): the x side compiled for its 2 blocks of 32
+    if (c == 64) hipLaunchKernelGGL((transition_narrow_kernel<T, 2>), grid, dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((transition_narrow_kernel<T, 4>), grid, dim3(512), 0, st, p);
     return;
   }
   if constexpr (std::is_same<T, bf16>::value) {
