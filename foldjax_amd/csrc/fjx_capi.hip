@@ -332,10 +332,13 @@ int triattn_run(const fjx_triattn_args* a, hipStream_t st) {
   fp.np = np;
   fp.heads = a->heads;
   fp.rows = n;
+  // o head-major, [B][N rows][4 heads][N][32]: a workgroup's 128 queries of
+  // one head are 8 KB in one piece, and the epilogue's wave for head h reads
+  // one 4 KB block per 64-position tile
   fp.o_stride_b = n * n * 128;
   fp.o_stride_row = n * 128;
-  fp.o_stride_head = 32;
-  fp.o_stride_q = 128;
+  fp.o_stride_head = n * 32;
+  fp.o_stride_q = 32;
   fp.bias_stride_b = a->heads * np * np;
   fp.fallback = at<unsigned>(W, ws.flags);
   rc = timed(K_TRIATTN_FLASH, st, "triattn_flash", [&] { launch_flash<T>(fp, a->batch, st); });

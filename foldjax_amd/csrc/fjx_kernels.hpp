@@ -71,7 +71,7 @@ struct TriMulEpilogueParams {
 
 template <typename T>
 struct TriAttnEpilogueParams {
-  const T* o;         // attention output, position-major [B][N*N][128] in the virtual grid
+  const T* o;         // attention output, head-major [B][N rows][4 heads][N][32] in the virtual grid
   const T* x;         // the op's input [B][N][N][128] (for the gate)
   const T* ln_w;
   const T* ln_b;

@@ -536,12 +536,14 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     } else {
       if (need_x) load_row_part<T>(p < nvalid ? P.x + orig_of(tl, p) * kC : nullptr, xr);
     }
-    const T* osrc = P.o + ((int64_t)tl.b * nn + (int64_t)tl.r * n + tl.s0) * kC;
+    // head-major o: this wave's head (channels col0 .. col0+31) of the tile's
+    // 64 positions is one contiguous 4 KB block
+    const T* osrc = P.o + ((((int64_t)tl.b * n + tl.r) * 4 + wave) * n + tl.s0) * 32;
 #pragma unroll
     for (int rt = 0; rt < kTE / 16; ++rt) {
       const int pp = 16 * rt + (lane & 15);
       if (pp < nvalid) {
-        ov[rt] = load8(osrc + (int64_t)pp * kC + col0 + 8 * (lane >> 4));
+        ov[rt] = load8(osrc + (int64_t)pp * 32 + 8 * (lane >> 4));
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) ov[rt][e] = from_f32<T>(0.f);
