@@ -599,7 +599,20 @@ int trimul_generic_run(const fjx_trimul_args* a, hipStream_t st) {
     g.gate = g2;
     g.residual = static_cast<const T*>(a->residual);
     g.row_gate = static_cast<const T*>(a->out_mask);
-    launch_gemm<T, T>(g, st);
+    bool direct = false;
+    if constexpr (std::is_same<T, bf16>::value) direct = gemm_dma_ok(g);
+    if (direct) {
+      launch_gemm<T, T>(g, st);
+    } else {
+      // the gated product into xn (no longer read), then a vectorized pass
+      // adds the residual and applies the output mask
+      g.c = xn;
+      g.residual = nullptr;
+      g.row_gate = nullptr;
+      launch_gemm<T, T>(g, st);
+      launch_scatter_add<T>(xn, nullptr, static_cast<const T*>(a->residual), static_cast<const T*>(a->out_mask),
+                            static_cast<T*>(a->out), rows, n, (int)cz, 0, st);
+    }
   });
 }
 
@@ -714,12 +727,22 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
     g.row_gate = static_cast<const T*>(a->out_mask);
     g.map_t = t;
     g.map_n = n;
-    launch_gemm<T, T>(g, st);
+    bool direct = false;
+    if constexpr (std::is_same<T, bf16>::value) direct = gemm_dma_ok(g);
+    if (direct) {
+      launch_gemm<T, T>(g, st);
+    } else {
+      // the product into xn (read only by the prologue), then a vectorized
+      // pass scatters it to the original grid with the residual and mask
+      launch_gemm<T, T>(rows_gemm<T>(fp.out, rows, hd, a->o_weight, cz, xn, cz), st);
+      launch_scatter_add<T>(xn, nullptr, static_cast<const T*>(a->residual), static_cast<const T*>(a->out_mask),
+                            static_cast<T*>(a->out), rows, n, (int)cz, t, st);
+    }
   });
 }
 
 struct GenTransitionWs {
-  size_t xn, h, wcat, total;
+  size_t xn, h, wcat, y, total;
 };
 GenTransitionWs gen_transition_ws(int64_t rows, int64_t c, int64_t hidden, int32_t dtype) {
   const size_t es = esize(dtype);
@@ -733,6 +756,7 @@ GenTransitionWs gen_transition_ws(int64_t rows, int64_t c, int64_t hidden, int32
   w.xn = take((size_t)rows * c * es);
   w.h = take((size_t)rows * hidden * es);
   w.wcat = take((size_t)2 * hidden * c * es);  // W_a and W_b interleaved by 128 rows (the fused SwiGLU GEMM)
+  w.y = take((size_t)rows * c * es);           // the output projection, when its GEMM cannot apply the epilogue
   w.total = off;
   return w;
 }
@@ -773,13 +797,23 @@ int transition_generic_run(const fjx_transition_args* a, hipStream_t st) {
       launch_gemm<T, T>(g, st);
     }
     // the output projection with the row mask, the residual and the output
-    // mask in its epilogue (rows map to themselves)
+    // mask in the DMA GEMM's epilogue (rows map to themselves); a product it
+    // does not take goes to a buffer and a vectorized pass adds them
     GemmParams<T, T> g = rows_gemm<T>(h, rows, hid, a->w_o, c, static_cast<T*>(a->out), c);
     g.proj_round = 1;
     g.row_scale = static_cast<const T*>(a->row_mask);
     g.residual = static_cast<const T*>(a->residual);
     g.row_gate = static_cast<const T*>(a->out_mask);
-    launch_gemm<T, T>(g, st);
+    bool direct = false;
+    if constexpr (std::is_same<T, bf16>::value) direct = gemm_dma_ok(g);
+    if (direct) {
+      launch_gemm<T, T>(g, st);
+    } else {
+      T* y = at<T>(W, ws.y);
+      launch_gemm<T, T>(rows_gemm<T>(h, rows, hid, a->w_o, c, y, c), st);
+      launch_scatter_add<T>(y, static_cast<const T*>(a->row_mask), static_cast<const T*>(a->residual),
+                            static_cast<const T*>(a->out_mask), static_cast<T*>(a->out), rows, 1, (int)c, 0, st);
+    }
   });
 }
 

@@ -372,6 +372,55 @@ __global__ __launch_bounds__(256) void to_position_major8_kernel(const T* __rest
   }
 }
 
+// out[b][orig(v)][c] = (T(y[b][v][c] * m) + residual[b][orig(v)][c]) * (g != 0),
+// with m the row mask and g the output mask at the output position (1 without)
+template <typename T>
+__global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
+                                   const T* __restrict__ residual, const T* __restrict__ out_mask,
+                                   T* __restrict__ out, int64_t rows, int64_t n, int c, int t) {
+  const int64_t total = rows * c;
+  const int64_t nn = n * n;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = idx / c;
+    const int ch = (int)(idx - row * c);
+    const int64_t bb = row / nn;
+    const int64_t o = bb * nn + orig_pos(row - bb * nn, n, t);
+    float v = to_f32(y[idx]);
+    if (row_mask) v *= to_f32(row_mask[o]);
+    v = round_to<T>(v);
+    if (residual) v += to_f32(residual[o * c + ch]);
+    if (out_mask && to_f32(out_mask[o]) == 0.f) v *= 0.f;
+    out[o * c + ch] = from_f32<T>(v);
+  }
+}
+
+// scatter_add_kernel, 8 channels per thread
+template <typename T>
+__global__ void scatter_add8_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
+                                    const T* __restrict__ residual, const T* __restrict__ out_mask,
+                                    T* __restrict__ out, int64_t rows, int64_t n, int c, int t) {
+  const int c8 = c / 8;
+  const int64_t total = rows * c8;
+  const int64_t nn = n * n;
+  for (int64_t i8 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i8 < total;
+       i8 += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i8 / c8;
+    const int ch = (int)(i8 - row * c8) * 8;
+    const int64_t bb = row / nn;
+    const int64_t o = bb * nn + orig_pos(row - bb * nn, n, t);
+    float v[8];
+    to_f32x8(load8(y + row * c + ch), v);
+    const float m = row_mask ? to_f32(row_mask[o]) : 1.f;
+    const float g = out_mask && to_f32(out_mask[o]) == 0.f ? 0.f : 1.f;
+    float r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (residual) to_f32x8(load8(residual + o * c + ch), r);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (round_to<T>(v[e] * m) + r[e]) * g;
+    store8(out + o * c + ch, pack8<T>(v));
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -443,6 +492,17 @@ void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, i
   else
     hipLaunchKernelGGL(gate_rows_kernel<T>, stride_grid(rows * width), dim3(256), 0, st, o, g, ldg, c0, rows, width);
 }
+template <typename T>
+void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
+                        int64_t n, int c, int t, hipStream_t st) {
+  if (c % 8 == 0 && al16(y) && al16(out) && (!residual || al16(residual)))
+    hipLaunchKernelGGL(scatter_add8_kernel<T>, stride_grid(rows * c / 8), dim3(256), 0, st, y, row_mask, residual,
+                       out_mask, out, rows, n, c, t);
+  else
+    hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out_mask,
+                       out, rows, n, c, t);
+}
+
 #define FJX_INST(T)                                                                                                \
   template void launch_ln_grid<T>(const T*, const T*, const T*, T*, int64_t, int64_t, int, float, int, hipStream_t); \
   template void launch_to_channel_major<T>(const T*, int64_t, int, int, const T*, T*, int64_t, int64_t, int,        \
@@ -453,7 +513,9 @@ void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, i
   template void launch_split_vt<T>(const T*, int64_t, int64_t, T*, int64_t, int64_t, int64_t, int, hipStream_t);   \
   template void launch_bias_planes<T>(const T*, int64_t, int64_t, T*, int64_t, int64_t, int64_t, int, hipStream_t); \
   template void launch_grid_mask_bias<T>(const T*, float*, int64_t, int64_t, int64_t, float, int, hipStream_t);     \
-  template void launch_gate_rows<T>(T*, const T*, int64_t, int64_t, int64_t, int, hipStream_t);
+  template void launch_gate_rows<T>(T*, const T*, int64_t, int64_t, int64_t, int, hipStream_t);                      \
+  template void launch_scatter_add<T>(const T*, const T*, const T*, const T*, T*, int64_t, int64_t, int, int,     \
+                                      hipStream_t);
 FJX_INST(float)
 FJX_INST(bf16)
 #undef FJX_INST
