@@ -300,20 +300,43 @@ __global__ __launch_bounds__(512) void contract_kernel(const bf16* __restrict__ 
 // through registers or LDS write instructions. DS stages of DK k each; the
 // configuration used (2 x 64, 128 KB) measured faster than deeper pipelines
 // of 32-wide stages (3 or 4 x 32), which pay a barrier per 32 k. Stage layout
-// per operand: 256 rows of CH = DK/8 16-byte chunks, chunk c of row r in
-// slot CH*r + (c ^ ((r / (16/CH)) % CH)) -- each wave's DMA instruction
-// writes whole rows (1 KB, lane-ordered), and the swizzle, applied through
-// the lanes' source addresses, keeps the 16-byte fragment reads of 16
-// consecutive rows on 16 distinct bank groups. Synchronisation: each wave
-// waits for its own DMA with an explicit vmcnt, then a bare s_barrier (a
-// fenced __syncthreads would wait for every DMA still in flight).
+// per operand: 256 rows of 8 16-byte chunks (DK = 64), chunk c of row r in
+// slot 8r + (c ^ swz(r)) -- each wave's DMA instruction writes whole rows
+// (1 KB, lane-ordered), and the swizzle, applied through the lanes' source
+// addresses, keeps the 16-byte fragment reads on 16 distinct bank groups:
+// with 128-byte rows the bank group of a chunk is 8 (r % 2) + (c ^ swz(r)).
+//
+// Output columns: the B fragment of column tile j holds B rows in the
+// permuted order pcol(j, r) (the same permutation the flash attention uses
+// for its keys), so that a lane's accumulators of tiles 2s and 2s+1 are 8
+// consecutive columns: one 16-byte store per lane, each row's four lanes
+// writing 64 contiguous bytes, half the store instructions of 4-column
+// pieces. An A fragment covers 16 consecutive rows, so A keeps the swizzle
+// of row bits 1-3; a B fragment covers rows {0..3, 8..11, 16..19, 24..27}
+// + 4 (j % 2) + 32 (j / 2), so B's swizzle takes row bits 1, 3 and 4. Each
+// is a bijection on its rows and ignores the bits that differ between its
+// fragments, so every fragment of a k-step is a constant offset from the
+// first (no address registers per fragment). B's DMA offsets are A's XOR
+// 16 (swz_a ^ swz_b)(r), which for the rows of DMA instruction j is
+// 32 (lane bit 5) XOR a constant.
+//
+// Synchronisation: each wave waits for its own DMA with an explicit vmcnt,
+// then a bare s_barrier (a fenced __syncthreads would wait for every DMA
+// still in flight).
 // ---------------------------------------------------------------------------
-// chunk c (16 bytes) of row r of a stage with CH chunks per row sits in
-// slot CH*r + (c ^ dma_swz<CH>(r))
-template <int CH>
-__device__ __forceinline__ int dma_swz(int r) { return (r / (16 / CH)) % CH; }
-template <int CH>
-__device__ __forceinline__ int dma_slot(int r, int c) { return CH * r + (c ^ dma_swz<CH>(r)); }
+__device__ __forceinline__ int swz_a(int r) { return (r >> 1) & 7; }
+__device__ __forceinline__ int swz_b(int r) { return ((r >> 1) & 1) | (((r >> 3) & 3) << 1); }
+__device__ __forceinline__ int slot_a(int r, int c) { return 8 * r + (c ^ swz_a(r)); }
+__device__ __forceinline__ int slot_b(int r, int c) { return 8 * r + (c ^ swz_b(r)); }
+// B row (within the wave's 64) behind accumulator row r of column tile j
+__device__ __forceinline__ int pcol(int j, int r) { return 32 * (j >> 1) + 8 * (r >> 2) + 4 * (j & 1) + (r & 3); }
+// a lane's 8 consecutive output columns 32s + 8 (lane / 16) .. +7 of row tile
+// i: accumulator rows 4 (lane / 16) .. +3 of column tiles 2s and 2s + 1
+__device__ __forceinline__ bf16x8 cols8(const f32x4 (&acc)[4][8], int i, int s) {
+  const float v[8] = {acc[2 * s][i][0],     acc[2 * s][i][1],     acc[2 * s][i][2],     acc[2 * s][i][3],
+                      acc[2 * s + 1][i][0], acc[2 * s + 1][i][1], acc[2 * s + 1][i][2], acc[2 * s + 1][i][3]};
+  return pack8<bf16>(v);
+}
 
 // Persistent: one workgroup per CU walks its XCD's contiguous share of the
 // tiles (workgroup w runs on XCD w % 8), so all tiles of a channel stay on
@@ -328,10 +351,11 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
                                                            bf16* __restrict__ O, int64_t n, int64_t batches,
                                                            bool blocked) {
   static_assert(DS == 2, "the persistent hand-over assumes two stages");
+  static_assert(DK == 64, "the swizzle is built for 8 chunks per row");
   constexpr int CH = DK / 8;       // 16-byte chunks per row
   constexpr int RPI = 64 / CH;     // rows per DMA instruction (1 KB)
   constexpr int NI = CH / 2;       // DMA instructions per wave per operand per stage
-  constexpr int kStores = 32;      // output stores per lane per tile (8 x 4 of 4 elements)
+  constexpr int kStores = 16;      // output stores per lane per tile (8 rows x 2 of 8 elements)
   __shared__ __attribute__((aligned(16))) bf16 S[DS][2][kCT * DK];  // [stage][A, B][256 rows x DK]
 
   const int64_t tpd = n / kCT;
@@ -341,7 +365,7 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
   const int64_t hi = (xcd + 1) * total / kNumXcd;  // this XCD's tiles: [xcd * total / 8, hi)
 
   const int t = threadIdx.x;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: wave offsets in SGPRs
   const int lane = t & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
@@ -356,23 +380,34 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int r = 32 * wave + RPI * j + lane / CH;
-    const int c = (lane % CH) ^ dma_swz<CH>(r);
+    const int c = (lane % CH) ^ swz_a(r);
     voff[j] = (uint32_t)(r * n * 2 + 16 * c);
   }
+  // B's offsets: voff[j] ^ xb ^ kBx[j] (r * n * 2 is a multiple of 512, so
+  // the XOR touches only the chunk bits)
+  static_assert(NI == 4, "kBx lists the four DMA instructions of a stage");
+  constexpr uint32_t kBx[4] = {0u, 32u | 64u, 64u, 32u};  // 16 (2 (j % 2) + 4 ((j ^ (j >> 1)) % 2))
+  const uint32_t xb = (uint32_t)(32 * ((lane >> 5) & 1));
   struct Tile {
     int64_t bat, m0, n0;
     const char* base[2];
   };
-  auto tile_of = [&](int64_t lid) {
+  // tile (bat, ti, tj) = lid as bat * tpd^2 + ti * tpd + tj; a workgroup's
+  // tiles are lid, lid + per_xcd, ..., so the next one's coordinates come
+  // from fixed carries instead of 64-bit divisions in the tile loop (whose
+  // reciprocal estimates the compiler keeps in spilled registers, with a
+  // vmcnt(0) reload that would wait for the previous tile's stores)
+  auto tile_at = [&](int64_t bat, int64_t ti, int64_t tj) {
     Tile tl;
-    tl.bat = lid / (tpd * tpd);
-    const int64_t r = lid % (tpd * tpd);
-    tl.m0 = (r / tpd) * kCT;
-    tl.n0 = (r % tpd) * kCT;
+    tl.bat = bat;
+    tl.m0 = ti * kCT;
+    tl.n0 = tj * kCT;
     tl.base[0] = reinterpret_cast<const char*>(A + (tl.bat * n + tl.m0) * n);
     tl.base[1] = reinterpret_cast<const char*>(B + (tl.bat * n + tl.n0) * n);
     return tl;
   };
+  const int64_t tt = tpd * tpd;
+  const int64_t step_b = per_xcd / tt, step_i = (per_xcd % tt) / tpd, step_j = per_xcd % tpd;
   // k-tile kt goes to stage kt % DS; the stage is always a compile-time
   // constant (a run-time stage index makes the compiler wait for every DMA in
   // flight before each LDS read)
@@ -382,20 +417,31 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
     for (int op = 0; op < 2; ++op)
 #pragma unroll
       for (int j = 0; j < NI; ++j)
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(tl.base[op] + 2 * k0 + voff[j]),
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(tl.base[op] + 2 * k0 +
+                                                                       (op ? voff[j] ^ (xb ^ kBx[j]) : voff[j])),
                                          reinterpret_cast<void*>(&S[st][op][(32 * wave + RPI * j) * DK]), 16, 0, 0);
   };
 
   const int64_t ktiles = n / DK;  // a multiple of DS (checked by the launcher)
   int64_t lid = xcd * total / kNumXcd + blockIdx.x / kNumXcd;
   if (lid >= hi) return;
-  Tile cur = tile_of(lid);
+  int64_t cb = lid / tt, ci = (lid % tt) / tpd, cj = lid % tpd;
+  Tile cur = tile_at(cb, ci, cj);
   issue(cur, 0, 0);
   bool first = true;
   for (;;) {
     const int64_t next_lid = lid + per_xcd;
     const bool has_next = next_lid < hi;
-    const Tile nxt = tile_of(has_next ? next_lid : lid);
+    int64_t nb = cb + step_b, ni = ci + step_i, nj = cj + step_j;
+    if (nj >= tpd) {
+      nj -= tpd;
+      ++ni;
+    }
+    if (ni >= tpd) {
+      ni -= tpd;
+      ++nb;
+    }
+    const Tile nxt = has_next ? tile_at(nb, ni, nj) : cur;
 
     f32x4 acc[4][8];
 #pragma unroll
@@ -425,10 +471,10 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
           bf16x8 af[8], bfr[4];
 #pragma unroll
           for (int i = 0; i < 8; ++i)
-            af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * dma_slot<CH>(wm + 16 * i + li, 4 * ks + lg));
+            af[i] = *reinterpret_cast<const bf16x8*>(As_ + 8 * slot_a(wm + 16 * i + li, 4 * ks + lg));
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * dma_slot<CH>(wn + 16 * j + li, 4 * ks + lg));
+            bfr[j] = *reinterpret_cast<const bf16x8*>(Bs_ + 8 * slot_b(wn + pcol(j, li), 4 * ks + lg));
 #pragma unroll
           for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -437,37 +483,39 @@ __global__ __launch_bounds__(512) void contract_dma_kernel(const bf16* __restric
       }
     }
 
+    // the lane's row and column offsets, opaque here: the store addresses are
+    // then formed after the k-loop instead of being hoisted above it (eight
+    // 64-bit addresses the accumulators leave no room for: spilled, and the
+    // reload's vmcnt(0) would wait for the next tile's DMA)
+    int lrow = li, lcol = 8 * lg;
+    asm volatile("" : "+v"(lrow), "+v"(lcol));
     if (blocked) {
       // [item][position / 64][channel][position % 64]; cur.bat = item * 128 + channel
       // the tile's 256 columns are one 256-position block of each row (n and
       // n0 are multiples of 256): block row * n/256 + n0/256
       bf16* Ob = O + ((cur.bat >> 7) * (n * n) * tile::kC) + (cur.bat & 127) * kOBlk +
-                 (cur.n0 / kOBlk) * (tile::kC * kOBlk) + wn + 4 * lg;
+                 (cur.n0 / kOBlk) * (tile::kC * kOBlk) + wn + lcol;
       const int64_t bpr = (n / kOBlk) * (tile::kC * kOBlk);  // elements per row of blocks
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        bf16* dst = Ob + (cur.m0 + wm + 16 * i + li) * bpr;
+        bf16* dst = Ob + (cur.m0 + wm + 16 * i + lrow) * bpr;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
-          store4f(dst + 16 * j, v);
-        }
+        for (int s = 0; s < 2; ++s) store8(dst + 32 * s, cols8(acc, i, s));
       }
     } else {
-      bf16* Ob = O + cur.bat * n * n;
+      bf16* Ob = O + cur.bat * n * n + cur.n0 + wn + lcol;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int64_t row = cur.m0 + wm + 16 * i + li;
+        bf16* dst = Ob + (cur.m0 + wm + 16 * i + lrow) * n;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t col = cur.n0 + wn + 16 * j + 4 * lg;
-          float v[4] = {acc[j][i][0], acc[j][i][1], acc[j][i][2], acc[j][i][3]};
-          store4f(Ob + row * n + col, v);
-        }
+        for (int s = 0; s < 2; ++s) store8(dst + 32 * s, cols8(acc, i, s));
       }
     }
     if (!has_next) break;
     lid = next_lid;
+    cb = nb;
+    ci = ni;
+    cj = nj;
     cur = nxt;
     first = false;
   }
