@@ -62,7 +62,7 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
   const int64_t hi = (xcd + 1) * total / kGXcd;
 
   const int t = threadIdx.x;
-  const int wave = t >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: wave offsets in SGPRs
   const int lane = t & 63;
   const int li = lane & 15;
   const int lg = lane >> 4;
