@@ -201,6 +201,22 @@ def test_trimul_multi_tile_sampled(n, n_real, direction):
     check_trimul(z, pm, wt, prep_tree(w, BF16), direction, pos, f"n={n} {direction}")
 
 
+@pytest.mark.parametrize("c_z,c_h", [(48, 128), (64, 64)])
+@pytest.mark.parametrize("direction", ["outgoing", "incoming"])
+def test_trimul_general_width_multi_tile_sampled(c_z, c_h, direction):
+    """The general-width tri-mul at N=512: its contraction is the LDS-DMA
+    kernel with row-major (not tile-blocked) output over 2x2 tiles of 256,
+    the store addressing the fused widths never reach."""
+    n, n_real = 512, 500
+    say(f"trimul general width c_z={c_z} c_h={c_h} n={n} {direction}")
+    w = syn.trimul_weights(c_z, c_h, seed=13)
+    wt = P.pack_trimul_torch(P.trimul_to_protenix(w), BF16, "cuda")
+    pm = syn.pair_mask(n, n_real)
+    z = device_normal((n, n, c_z), seed=14)
+    pos = [(i, j) for i in (0, 255, 256, n - 1) for j in (0, 127, 255, 256, n_real, n - 1)]
+    check_trimul(z, pm, wt, prep_tree(w, BF16), direction, pos, f"general c_z={c_z} c_h={c_h} n={n} {direction}")
+
+
 def test_trimul_persistent_batch_n768():
     """The persistent LDS-DMA contraction walks each XCD's share of the
     (batch, channel, tile) space; at N=768 (3x3 tiles of 256 per channel) and
