@@ -19,8 +19,13 @@
 // Persistent: one workgroup per CU walks its XCD's contiguous share of the
 // tiles, n-tiles fastest, so an A row block is reused from that XCD's L2 by
 // its consecutive n-tiles; the next tile's first stage goes out during the
-// last k-step. Accumulators are transposed (A operand = B rows), so a lane
-// holds 4 consecutive output columns of one row: 8-byte epilogue accesses.
+// last k-step. Accumulators are transposed (A operand = B rows), and the
+// B rows of a wave's 64 columns sit in LDS in a permuted order (the DMA of B
+// writes LDS row 16 j + r of a 64-row block from B row pcol(j, r) =
+// 32 (j / 2) + 8 (r / 4) + 4 (j % 2) + r % 4), so that a lane's accumulators
+// of column tiles 2s and 2s+1 are 8 consecutive output columns: 16-byte
+// epilogue accesses, half the store instructions of 4-column pieces. The
+// fragment reads and their swizzle are those of consecutive LDS rows.
 #include <algorithm>
 
 #include "fjx_common.hpp"
@@ -69,10 +74,12 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
   const int wm = (wave >> 2) * 128;
   const int wn = (wave & 3) * 64;
 
-  // this lane's DMA rows and chunks: instruction j copies tile row
-  // r = 32 wave + 8 j + lane / 8, chunk c (k = 8 c). The swizzle of r depends
-  // on j only through j % 2, so two per-lane offsets per operand serve all
-  // four instructions, the rest (16 rows per two instructions) is uniform
+  // this lane's DMA rows and chunks: instruction j writes LDS row
+  // r = 32 wave + 8 j + lane / 8, chunk c (k = 8 c), from A row r and from B
+  // row 32 wave + 16 (j % 2) + 4 (j / 2) + 8 (lane bit 5) + (lane / 8) % 4
+  // (the permuted order above). The swizzle of r depends on j only through
+  // j % 2, so two per-lane offsets per operand serve all four instructions,
+  // the rest (16 A rows or 4 B rows per two instructions) is uniform
   uint32_t aoff[2], boff[2];
   int kc[2];
 #pragma unroll
@@ -81,9 +88,10 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
     const int c = (lane % kGCH) ^ gswz(r);
     kc[j] = 8 * c;
     aoff[j] = (uint32_t)(r * P.lda * 2 + 16 * c);
-    boff[j] = (uint32_t)(r * P.ldb * 2 + 16 * c);
+    const int rb = 32 * wave + 16 * j + 8 * ((lane >> 5) & 1) + ((lane >> 3) & 3);
+    boff[j] = (uint32_t)(rb * P.ldb * 2 + 16 * c);
   }
-  const uint32_t astep = (uint32_t)(2 * kGRPI * P.lda * 2), bstep = (uint32_t)(2 * kGRPI * P.ldb * 2);
+  const uint32_t astep = (uint32_t)(2 * kGRPI * P.lda * 2), bstep = (uint32_t)(4 * P.ldb * 2);
 
   struct Tile {
     int64_t bat, m0, n0;
@@ -204,21 +212,22 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
         bf16* O = P.c + cur.bat * P.sc;
         const int64_t hid = N / 2;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t col = cur.n0 / 2 + wn + 16 * j + 4 * lg;
+        for (int s = 0; s < 2; ++s) {
+          const int64_t col = cur.n0 / 2 + wn + 32 * s + 8 * lg;
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            const bf16x4 b = *reinterpret_cast<const bf16x4*>(X + 4 * ((pair * 32 + j * 8 + i) * 64 + lane));
+            const bf16x4 b0 = *reinterpret_cast<const bf16x4*>(X + 4 * ((pair * 32 + 2 * s * 8 + i) * 64 + lane));
+            const bf16x4 b1 = *reinterpret_cast<const bf16x4*>(X + 4 * ((pair * 32 + (2 * s + 1) * 8 + i) * 64 + lane));
             const int64_t row = cur.m0 + wm + 16 * i + li;
             if (row >= M || col >= hid) continue;
-            float v[4];
+            float v[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float a = round_to<bf16>(acc[j][i][q]);
-              const float bb = static_cast<float>(b[q]);
-              v[q] = P.swiglu == 1 ? a * fast_sigmoid(a) * bb : a * round_to<bf16>(fast_sigmoid(bb));
+            for (int e = 0; e < 8; ++e) {
+              const float a = round_to<bf16>(e < 4 ? acc[2 * s][i][e] : acc[2 * s + 1][i][e - 4]);
+              const float bb = static_cast<float>(e < 4 ? b0[e] : b1[e - 4]);
+              v[e] = P.swiglu == 1 ? a * fast_sigmoid(a) * bb : a * round_to<bf16>(fast_sigmoid(bb));
             }
-            store4f(O + row * P.ldc + col, v);
+            store8(O + row * P.ldc + col, pack8<bf16>(v));
           }
         }
       }
@@ -229,18 +238,18 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
     }
 
     // epilogue: this lane holds row m0 + wm + 16 i + li, columns
-    // n0 + wn + 16 j + 4 lg .. +3 of acc[j][i]
+    // n0 + wn + 32 s + 8 lg .. +7 in acc[2s][i] (the first 4) and acc[2s+1][i]
     bf16* O = P.c + cur.bat * P.sc;
     const bf16* G = P.gate ? P.gate + cur.bat * P.sc : nullptr;
     const bf16* R = P.residual ? P.residual + cur.bat * P.sc : nullptr;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = cur.n0 + wn + 16 * j + 4 * lg;
-      if (col >= N) continue;  // N is a multiple of 4 (checked by the launcher)
-      float bias[4];
+    for (int s = 0; s < 2; ++s) {
+      const int64_t col = cur.n0 + wn + 32 * s + 8 * lg;
+      if (col >= N) continue;  // N is a multiple of 8 (checked by the launcher)
+      float bias[8];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        bias[q] = P.bias && (P.bias_n == 0 || col + q < P.bias_n) ? to_f32(P.bias[col + q]) : 0.f;
+      for (int e = 0; e < 8; ++e)
+        bias[e] = P.bias && (P.bias_n == 0 || col + e < P.bias_n) ? to_f32(P.bias[col + e]) : 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int64_t row0 = cur.m0 + wm + 16 * i + li;
@@ -248,37 +257,37 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
         const int64_t row = grid_row(row0, P.map_n, P.map_t);
         const bool zero_row = P.row_gate && to_f32(P.row_gate[row]) == 0.f;
         const int64_t off = row * P.ldc + col;
-        float v[4];
+        float v[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float x = acc[j][i][q] + bias[q];
-          const int act = col + q >= P.act_col0 ? P.act : 0;
+        for (int e = 0; e < 8; ++e) {
+          float x = (e < 4 ? acc[2 * s][i][e] : acc[2 * s + 1][i][e - 4]) + bias[e];
+          const int act = col + e >= P.act_col0 ? P.act : 0;
           if (act == 1) x = fast_sigmoid(x);
           else if (act == 2) x *= fast_sigmoid(x);  // silu
-          v[q] = x;
+          v[e] = x;
         }
         if (G) {
-          float g[4];
-          load4f(G + off, g);
+          float g[8];
+          to_f32x8(load8(G + off), g);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] *= g[q];
+          for (int e = 0; e < 8; ++e) v[e] *= g[e];
         }
         if (P.proj_round) {
           const float rs = P.row_scale ? to_f32(P.row_scale[row]) : 1.f;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = round_to<bf16>(round_to<bf16>(v[q]) * rs);
+          for (int e = 0; e < 8; ++e) v[e] = round_to<bf16>(round_to<bf16>(v[e]) * rs);
         }
         if (R) {
-          float r[4];
-          load4f(R + off, r);
+          float r[8];
+          to_f32x8(load8(R + off), r);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] += r[q];
+          for (int e = 0; e < 8; ++e) v[e] += r[e];
         }
         if (zero_row) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] *= 0.f;
+          for (int e = 0; e < 8; ++e) v[e] *= 0.f;
         }
-        store4f(O + off, v);
+        store8(O + off, pack8<bf16>(v));
       }
     }
     if (!has_next) break;
@@ -292,13 +301,13 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
 }  // namespace
 
 bool gemm_dma_ok(const GemmParams<bf16, bf16>& p) {
-  // 16-byte rows for the DMA, 8-byte output groups, and enough rows to fill
+  // 16-byte rows for the DMA, 16-byte output groups, and enough rows to fill
   // the device with 256 x 256 tiles
-  const bool ok = p.k % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.n % 4 == 0 && p.ldc % 4 == 0 &&
+  const bool ok = p.k % 8 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.n % 8 == 0 && p.ldc % 8 == 0 &&
                   (reinterpret_cast<uintptr_t>(p.a) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.b) & 15) == 0 &&
-                  (reinterpret_cast<uintptr_t>(p.c) & 7) == 0 && (!p.gate || (reinterpret_cast<uintptr_t>(p.gate) & 7) == 0) &&
-                  (!p.residual || (reinterpret_cast<uintptr_t>(p.residual) & 7) == 0) &&
-                  (p.batches == 1 || (p.sa % 8 == 0 && p.sb % 8 == 0 && p.sc % 4 == 0)) &&
+                  (reinterpret_cast<uintptr_t>(p.c) & 15) == 0 && (!p.gate || (reinterpret_cast<uintptr_t>(p.gate) & 15) == 0) &&
+                  (!p.residual || (reinterpret_cast<uintptr_t>(p.residual) & 15) == 0) &&
+                  (p.batches == 1 || (p.sa % 8 == 0 && p.sb % 8 == 0 && p.sc % 8 == 0)) &&
                   p.lda * 2 * (int64_t)kGT < (int64_t)kGOob && p.ldb * 2 * (int64_t)kGT < (int64_t)kGOob &&
                   p.ldc * 2 * (int64_t)kGT < (int64_t)kGOob;
   const int64_t total = p.batches * ((p.m + kGT - 1) / kGT) * ((p.n + kGT - 1) / kGT);
