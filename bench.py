@@ -59,6 +59,9 @@ def _args():
                         "paths, e.g. 64 for the template stack, 384 for OpenDDE's structural pair track)")
     p.add_argument("--c-h", type=int, default=128, help="with --op trimul: the hidden width")
     p.add_argument("--heads", type=int, default=4, help="with --op triattn: heads of 32 channels")
+    p.add_argument("--cpu-whole", action="store_true",
+                   help="no GPU work: time the whole block at --n on the CPU once, beside the sampled estimate "
+                        "the bench line reports (checks the sample model)")
     return p.parse_args()
 
 
@@ -128,7 +131,7 @@ def _trimul_sample_s(O, z, pm, p, n: int, pos_div: int = 16, ch: int = 16) -> fl
     return t_pos * pos_div + t_con * (128 / ch)
 
 
-def cpu_baseline(n: int, n_real: int) -> dict:
+def cpu_baseline(n: int, n_real: int, with_configs: bool = True) -> dict:
     """The float32 numpy restatement (``oracle/``, the reference's XLA path in
     fp32) timed on this host's cores at the headline size, on a bounded
     sample whose work scales exactly to the whole block:
@@ -181,17 +184,8 @@ def cpu_baseline(n: int, n_real: int) -> dict:
             return s2 + O.transition(s2, w["transition_s"])
 
         parts["single_track"], _ = _median_time(single, 0.0, 1)
-        # configs 1 and 2, whole
-        z1 = syn.pair_input(256, 128, seed=0, batch=1).astype(np.float32)
-        t_c1, _ = _median_time(lambda: [O.protenix_triangle_multiplication(z1, None, w[k], d) for k, d in
-                                        (("tri_mul_out", "outgoing"), ("tri_mul_in", "incoming"))], 0.0, 1)
-        z2 = syn.pair_input(384, 128, seed=0, batch=1)
-        pm2 = syn.pair_mask(384, 346)[None]
-        t_c2 = sum(_rows_model(lambda r, k=k, st=st: O.protenix_triangle_attention(
-            z2, pm2, w[k], num_heads=4, starting=st, rows=np.arange(r)), 16, 48, 384)
-            for k, st in (("tri_att_start", True), ("tri_att_end", False)))
     total = 2 * parts["trimul_out"] + 2 * parts["triattn_start"] + parts["transition_z"] + parts["single_track"]
-    return {
+    out = {
         "value": round(total * 1e3, 1),
         "unit": "ms",
         "cores": cores,
@@ -205,10 +199,62 @@ def cpu_baseline(n: int, n_real: int) -> dict:
             f"transition on 1/32 of the positions x32 ({parts['transition_z']:.1f} s); single track whole "
             f"({parts['single_track']:.2f} s)"
         ),
-        "configs": {
-            "config1_trimul_out_in_n256_fp32_ms": round(t_c1 * 1e3, 1),
-            "config2_triattn_start_end_n384_ms": round(t_c2 * 1e3, 1),
-        },
+    }
+    if not with_configs:
+        return out
+    with O.compute_dtype(np.float32):
+        # configs 1 and 2, whole
+        z1 = syn.pair_input(256, 128, seed=0, batch=1).astype(np.float32)
+        def config1():
+            z = z1 + O.protenix_triangle_multiplication(z1, None, w["tri_mul_out"], "outgoing")
+            return z + O.protenix_triangle_multiplication(z, None, w["tri_mul_in"], "incoming")
+
+        def config2():
+            z = z2 + O.protenix_triangle_attention(z2, pm2, w["tri_att_start"], num_heads=4, starting=True)
+            return z + O.protenix_triangle_attention(z, pm2, w["tri_att_end"], num_heads=4, starting=False)
+
+        t_c1, _ = _median_time(config1, 0.0, 1)
+        z2 = syn.pair_input(384, 128, seed=0, batch=1).astype(np.float32)
+        pm2 = syn.pair_mask(384, 346)[None]
+        t_c2, _ = _median_time(config2, 0.0, 1)
+    out["configs"] = {
+        "config1_trimul_out_in_n256_fp32_ms": round(t_c1 * 1e3, 1),
+        "config2_triattn_start_end_n384_ms": round(t_c2 * 1e3, 1),
+        "note": "configs 1 and 2 timed whole, each second sublayer on the first one's output",
+    }
+    return out
+
+
+def cpu_whole_block(n: int, n_real: int) -> dict:
+    """The whole block on the CPU once, against the sampled estimate of
+    ``cpu_baseline`` at the same size: the float32 restatement of the Boltz-2
+    layer (``oracle.boltz2_pairformer_layer``: tri-mul out and in, tri-attn
+    start and end over the whole grid, 16 rows at a time, the pair transition,
+    the single attention with pair bias and the single transition) on the
+    same inputs. This checks the sample model; the default bench line keeps
+    the bounded sample."""
+    import numpy as np
+
+    from foldjax_amd import synthetic as syn
+    from oracle import triangle as O
+
+    w = syn.pairformer_layer_weights(seed=2)
+    z = syn.pair_input(n, 128, seed=0, batch=1)
+    s = syn.single_input(n, 384, seed=1, batch=1)
+    tm = syn.token_mask(n, n_real)[None]
+    pm = syn.pair_mask(n, n_real)[None]
+    with O.compute_dtype(np.float32):
+        t0 = time.perf_counter()
+        s_out, z_out = O.boltz2_pairformer_layer(w, s, z, tm, pm)
+        whole = time.perf_counter() - t0
+    if not (np.all(np.isfinite(z_out)) and np.all(np.isfinite(s_out))):
+        raise RuntimeError("non-finite CPU block output")
+    sampled = cpu_baseline(n, n_real, with_configs=False)
+    return {
+        "n": n, "n_real": n_real, "cores": len(os.sched_getaffinity(0)),
+        "whole_ms": round(whole * 1e3, 1), "sampled_ms": sampled["value"],
+        "sampled_over_whole": round(sampled["value"] / (whole * 1e3), 3),
+        "sample": sampled["sample"],
     }
 
 
@@ -245,17 +291,25 @@ def other_configs(single_dtype) -> dict:
     layer32 = PairformerLayerWeights.random(torch.float32, dev, seed=2)
     z1 = t(syn.pair_input(256, 128, seed=0, batch=1), torch.float32)
     tri = layer32.triangle
-    out["config1_trimul_out_in_n256_fp32_ms"] = round(_timed(lambda: kernels.trimul(
-        kernels.trimul(z1, None, tri.tri_mul_out, "outgoing", residual=z1), None, tri.tri_mul_in, "incoming",
-        residual=z1), 20, 3, dev), 4)
+
+    def config1():
+        # z += tri-mul outgoing, then z += tri-mul incoming of that z
+        z = kernels.trimul(z1, None, tri.tri_mul_out, "outgoing", residual=z1)
+        return kernels.trimul(z, None, tri.tri_mul_in, "incoming", residual=z, out=z)
+
+    out["config1_trimul_out_in_n256_fp32_ms"] = round(_timed(config1, 20, 3, dev), 4)
     del layer32, z1
     layer = PairformerLayerWeights.random(bf, dev, seed=2, single_dtype=single_dtype)
     tri = layer.triangle
     z2 = t(syn.pair_input(384, 128, seed=0, batch=1), bf)
     m2 = t(syn.pair_mask(384, 346)[None], bf)
-    out["config2_triattn_start_end_n384_bf16_ms"] = round(_timed(lambda: kernels.triattn(
-        kernels.triattn(z2, m2, tri.tri_att_start, starting=True, residual=z2), m2, tri.tri_att_end, starting=False,
-        residual=z2), 20, 3, dev), 4)
+
+    def config2():
+        # z += tri-attn starting node, then z += tri-attn ending node of that z
+        z = kernels.triattn(z2, m2, tri.tri_att_start, starting=True, residual=z2)
+        return kernels.triattn(z, m2, tri.tri_att_end, starting=False, residual=z, out=z)
+
+    out["config2_triattn_start_end_n384_bf16_ms"] = round(_timed(config2, 20, 3, dev), 4)
     del z2, m2
     for key, n, n_real, layers, steps in (("config5_block_n3072_ms", 3072, 3012, 1, 3),
                                           ("config4_trunk48_n2048_ms", 2048, 2048, 48, 2)):
@@ -293,6 +347,10 @@ def main() -> int:
             file=sys.stderr,
         )
         return 2
+    if a.cpu_whole:
+        n_real = a.n - int(round(a.pad_frac * a.n))
+        print(json.dumps({"cpu_whole_block": cpu_whole_block(a.n, n_real)}))
+        return 0
     import torch
 
     from foldjax_amd import _lib

@@ -181,17 +181,25 @@ def pairformer_layer_forward(
     """Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:100-206``):
     every residual is fused into the producing kernel. ``params`` is the
     Boltz-2 layer dict, or a ``foldjax_amd.pairformer.PairformerLayerWeights``."""
+    w = _packed_layer(params, s, z)
+    _check_layer_selectors(matmul_precision, triangle_backend)
+    return w.forward(s, z, mask, pair_mask, eps=eps)
+
+
+def _packed_layer(params, s: torch.Tensor, z: torch.Tensor):
     from foldjax_amd.pairformer import PairformerLayerWeights
 
-    w = params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_boltz2(
+    return params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_boltz2(
         params, z.dtype, z.device, single_dtype=s.dtype)
-    # selector validation as the reference's entry points do it
+
+
+def _check_layer_selectors(matmul_precision: str, triangle_backend: str) -> None:
+    """Selector validation as the reference's layer entry point does it."""
     resolve_matmul_precision(matmul_precision)
     if triangle_backend not in ("xla", "pallas", "tokamax", "cueq", "hip"):
         raise ValueError(f"Unsupported triangle_backend: {triangle_backend!r}")
     if triangle_backend != "hip":
         raise RuntimeError(_REFERENCE_ONLY.format(kind="triangle attention", name=triangle_backend))
-    return w.forward(s, z, mask, pair_mask, eps=eps)
 
 
 def pairformer_no_seq_layer_forward(
@@ -228,8 +236,9 @@ def pairformer_no_seq_layer_forward(
         pack_triattn_boltz2(params["tri_att_start"], dt, dev),
         pack_triattn_boltz2(params["tri_att_end"], dt, dev),
     )
-    z = tri.forward(z, pair_mask)
-    return kernels.transition(z, pack_transition_boltz2(params["transition_z"], dt, dev), residual=z, eps=eps)
+    z = tri.forward(z, pair_mask)  # a new tensor, updated in place from here on
+    return kernels.transition(z, pack_transition_boltz2(params["transition_z"], dt, dev), residual=z, eps=eps,
+                              out=z)
 
 
 def stack_layer_params(layer_list, dtype: torch.dtype | None = None, device=None, single_dtype=None):
@@ -277,25 +286,13 @@ def pairformer_module_forward(
     without it each layer is used as given. The chunk arguments are accepted
     for signature parity: the reference uses them to bound XLA's memory,
     while every layer here streams through fused kernels with a fixed
-    workspace."""
+    workspace. As the reference's scan donates its carry
+    (``B2K/pairformer.py:74-96``), the first layer writes new s and z and
+    every later layer updates those in place."""
     layers = params["layers"]
     if use_scan:
         layers = stack_layer_params(layers, z.dtype, z.device, single_dtype=s.dtype)
-    for layer in layers:
-        s, z = pairformer_layer_forward(
-            layer,
-            s,
-            z,
-            mask,
-            pair_mask,
-            eps=eps,
-            chunk_size=chunk_size,
-            triangle_attention_chunk=triangle_attention_chunk,
-            triangle_attention_q_chunk=triangle_attention_q_chunk,
-            transition_hidden_chunk=transition_hidden_chunk,
-            matmul_precision=matmul_precision,
-            attention_backend=attention_backend,
-            triangle_backend=triangle_backend,
-            glu_backend=glu_backend,
-        )
+    _check_layer_selectors(matmul_precision, triangle_backend)
+    for idx, layer in enumerate(layers):
+        s, z = _packed_layer(layer, s, z).forward(s, z, mask, pair_mask, eps=eps, donate=idx > 0)
     return s, z

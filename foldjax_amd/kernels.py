@@ -210,6 +210,7 @@ def transition(
     pair_bias_for: SingleAttentionWeights | None = None,
     pair_bias_eps: float = 1e-5,
     out_mask: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ):
     """``((silu(LN(x) w_a^T) * (LN(x) w_b^T)) w_o^T [* row_mask] [+ residual])
     [* (out_mask != 0)]`` over the last axis (``fjx_transition_fwd``);
@@ -224,7 +225,11 @@ def transition(
     heads it is computed in the transition's epilogue, so the pair tensor is
     not read again. The bias takes the attention's dtype: a float32
     attention over a bfloat16 pair track gets a float32 bias computed to
-    float32 accuracy."""
+    float32 accuracy.
+
+    ``out``: write the result into this tensor (x's shape, dtype and device,
+    contiguous) instead of a new one; it may be ``x`` and/or ``residual``
+    (in place)."""
     c = int(x.shape[-1])
     w.check(c)
     _same_device(x, row_mask=row_mask, residual=residual, out_mask=out_mask)
@@ -239,7 +244,7 @@ def transition(
     rows = x.numel() // max(c, 1)
     xf = x.contiguous()
     lib = _lib.load()
-    out = torch.empty_like(xf)
+    out = _out_buffer(out, x, xf)
     pb = None
     pb_n = pb_heads = 0
     pb_f32 = False
@@ -291,6 +296,7 @@ def single_attention(
     pair_bias: torch.Tensor | None = None,
     out_mask: torch.Tensor | None = None,
     extra_bias: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Single-track attention with pair bias (``fjx_single_attention_fwd``).
     ``s`` ``[B, N, c_s]`` (or ``[N, c_s]``), ``z`` ``[B, N, N, c_z]``, ``mask``
@@ -302,7 +308,9 @@ def single_attention(
     prepared from this ``z`` in ``s``'s dtype; ``z`` is then not read (and may
     be None). ``extra_bias``: an additive bias broadcasting to ``[B, H, N, N]``
     from a 4-D tensor whose last two axes are ``[N, N]`` (Protenix's
-    ``extra_attn_bias``)."""
+    ``extra_attn_bias``). ``out``: write the result into this tensor (s's
+    shape, dtype and device, contiguous); it may be ``s`` when ``residual`` is
+    ``s`` (in place)."""
     _same_device(s, z=z, mask=mask, residual=residual, pair_bias=pair_bias, out_mask=out_mask,
                  extra_bias=extra_bias)
     if residual is not None:
@@ -350,7 +358,9 @@ def single_attention(
         res = (residual.unsqueeze(0) if squeeze else residual).to(dtype=s.dtype).contiguous()
     lib = _lib.load()
     code = _code(s.dtype)
-    out = torch.empty_like(sb)
+    if out is not None and out.data_ptr() == s.data_ptr() and (residual is None or residual.data_ptr() != s.data_ptr()):
+        raise ValueError("out may be s only when residual is s")
+    out = _out_buffer(out, s, sb)
     ws_bytes = lib.fjx_single_attention_workspace_size(batch, n, c_s, w.heads, code)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=s.device)
     a = _lib.SingleAttentionArgs(
@@ -367,6 +377,22 @@ def single_attention(
     _check_weights(s, w)
     _lib.check(lib.fjx_single_attention_fwd(ctypes.byref(a), _stream(s)))
     return out[0] if squeeze else out
+
+
+def _out_buffer(out: torch.Tensor | None, x: torch.Tensor, flat: torch.Tensor) -> torch.Tensor:
+    """The output buffer of a call on ``x`` (flattened as ``flat``): a new
+    tensor, or the caller's ``out``, which must be a contiguous tensor of x's
+    shape, dtype and device and may be x itself and/or the residual (every
+    kernel reads an output position's inputs before it writes it, and only
+    the workgroup that writes a position reads it)."""
+    if out is None:
+        return torch.empty_like(flat)
+    if tuple(out.shape) != tuple(x.shape) or out.dtype != x.dtype or out.device != x.device:
+        raise ValueError(f"out must be a {x.dtype} tensor of shape {tuple(x.shape)} on {x.device}, "
+                         f"got {out.dtype} {tuple(out.shape)} on {out.device}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
+    return out.reshape(flat.shape)
 
 
 def _flatten_pair(x: torch.Tensor, mask: torch.Tensor | None):
@@ -399,6 +425,7 @@ def trimul(
     *,
     no_alloc: bool = False,
     out_mask: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Triangle multiplicative update (``fjx_trimul_fwd``); returns the update,
     or ``residual + update`` when ``residual`` is given, times
@@ -407,7 +434,9 @@ def trimul(
     ``no_alloc``: run ``fjx_trimul_fwd_noalloc`` instead, whose workspace is
     the library's static per-GPU scratch (shapes up to
     ``_lib.NOALLOC_SCRATCH_BYTES`` of workspace; calls on one GPU must not
-    overlap). Only the output is allocated here."""
+    overlap). Only the output is allocated here, unless ``out`` is given:
+    the result then goes into that tensor (x's shape, dtype and device,
+    contiguous), which may be ``x`` and/or ``residual`` (in place)."""
     if direction not in ("outgoing", "incoming"):
         raise ValueError(f"Unsupported triangle multiplication direction: {direction!r}")
     _same_device(x, residual=residual, out_mask=out_mask)
@@ -419,7 +448,7 @@ def trimul(
     _dev(x)
     lib = _lib.load()
     code = _code(x.dtype)
-    out = torch.empty_like(xf)
+    out = _out_buffer(out, x, xf)
     res = None if residual is None else residual.to(dtype=x.dtype).contiguous().reshape(batch, n, n, c)
     ws_bytes = 0 if no_alloc else lib.fjx_trimul_workspace_size(batch, n, c, c_h, code)
     ws = None if no_alloc else torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
@@ -450,9 +479,11 @@ def triattn(
     eps: float = 1e-5,
     residual: torch.Tensor | None = None,
     out_mask: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Triangle attention, starting or ending node (``fjx_triattn_fwd``);
-    ``out_mask`` (``[..., N, N]``, indexed like the output) as for ``trimul``."""
+    ``out_mask`` (``[..., N, N]``, indexed like the output) and ``out`` (may
+    be ``x`` and/or ``residual``: in place) as for ``trimul``."""
     _same_device(x, residual=residual, out_mask=out_mask)
     if residual is not None:
         _need_shape("residual", residual, x.shape)
@@ -463,7 +494,7 @@ def triattn(
     _dev(x)
     lib = _lib.load()
     code = _code(x.dtype)
-    out = torch.empty_like(xf)
+    out = _out_buffer(out, x, xf)
     res = None if residual is None else residual.to(dtype=x.dtype).contiguous().reshape(batch, n, n, c)
     ws_bytes = lib.fjx_triattn_workspace_size(batch, n, c, heads, hd // heads, code)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)

@@ -187,10 +187,17 @@ def pairformer_block(
     pair bias comes out of the pair transition's epilogue."""
     if chunk_size is not None and chunk_size <= 0:
         raise ValueError(f"chunk_size must be positive, got {chunk_size}")
+    return _block_forward(s, z, params, single_mask, pair_mask, no_heads_pair, no_heads_pair_bias, inf,
+                          mask_transition, eps, donate=False)
+
+
+def _block_forward(s, z, params, single_mask, pair_mask, no_heads_pair, no_heads_pair_bias, inf, mask_transition,
+                   eps, *, donate):
     block = params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_openfold3(
         params, z.dtype, z.device, single_dtype=s.dtype)
     _check_block_heads(block, no_heads_pair, no_heads_pair_bias)
-    return block.forward_openfold3(s, z, single_mask, pair_mask, inf=inf, mask_transition=mask_transition, eps=eps)
+    return block.forward_openfold3(s, z, single_mask, pair_mask, inf=inf, mask_transition=mask_transition, eps=eps,
+                                   donate=donate)
 
 
 def can_scan(blocks) -> bool:
@@ -227,8 +234,11 @@ def pairformer_stack(
                   for b in blocks]
         if scan_blocks and can_scan(blocks):
             blocks = stacked_or_stack(blocks)
-    for block in blocks:
-        s, z = pairformer_block(s, z, block, single_mask=single_mask, pair_mask=pair_mask,
-                                no_heads_pair=no_heads_pair, no_heads_pair_bias=no_heads_pair_bias, inf=inf,
-                                mask_transition=mask_transition, eps=eps, chunk_size=chunk_size)
+    if chunk_size is not None and chunk_size <= 0:
+        raise ValueError(f"chunk_size must be positive, got {chunk_size}")
+    # the first block writes new s and z, every later one updates them in
+    # place (the reference's scan donates its carry)
+    for idx, block in enumerate(blocks):
+        s, z = _block_forward(s, z, block, single_mask, pair_mask, no_heads_pair, no_heads_pair_bias, inf,
+                              mask_transition, eps, donate=idx > 0)
     return s, z

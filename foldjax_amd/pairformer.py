@@ -27,22 +27,42 @@ class TriangleSublayers:
     tri_att_end: kernels.TriAttnWeights
 
     def forward(self, z: torch.Tensor, mask: torch.Tensor | None, *, inf: float = 1e9, eps: float = 1e-5,
-                out_mask: torch.Tensor | None = None, tri_mul_first: bool = True) -> torch.Tensor:
+                out_mask: torch.Tensor | None = None, tri_mul_first: bool = True,
+                donate: bool = False) -> torch.Tensor:
         """z += each sublayer in turn (the residual fused into its epilogue);
         with ``out_mask`` every sublayer's output is multiplied by
         ``out_mask != 0`` (Protenix's ``z * pair_gate``). ``tri_mul_first``
         orders the multiplication pair before the attention pair (OpenFold3's
-        ``pair_block`` option)."""
+        ``pair_block`` option).
+
+        The sublayers update one pair tensor in place: the first writes a new
+        tensor and the others overwrite it (the kernels read each position's
+        inputs before writing it), so the four sublayers allocate one pair
+        tensor. ``donate``: the caller gives up ``z`` (a contiguous tensor it
+        no longer reads, as the reference's scan donates its carry,
+        ``B2K/pairformer.py:74-96``), and the first sublayer overwrites it as
+        well."""
+        first = [True]
+
+        def dest(z):
+            # the output buffer of the next sublayer: z itself, except for the
+            # first sublayer of a call that does not donate z
+            if first[0]:
+                first[0] = False
+                return z if donate and z.is_contiguous() else None
+            return z
 
         def mul_pair(z):
-            z = kernels.trimul(z, mask, self.tri_mul_out, "outgoing", eps=eps, residual=z, out_mask=out_mask)
-            return kernels.trimul(z, mask, self.tri_mul_in, "incoming", eps=eps, residual=z, out_mask=out_mask)
+            z = kernels.trimul(z, mask, self.tri_mul_out, "outgoing", eps=eps, residual=z, out_mask=out_mask,
+                               out=dest(z))
+            return kernels.trimul(z, mask, self.tri_mul_in, "incoming", eps=eps, residual=z, out_mask=out_mask,
+                                  out=dest(z))
 
         def att_pair(z):
             z = kernels.triattn(z, mask, self.tri_att_start, starting=True, inf=inf, eps=eps, residual=z,
-                                out_mask=out_mask)
+                                out_mask=out_mask, out=dest(z))
             return kernels.triattn(z, mask, self.tri_att_end, starting=False, inf=inf, eps=eps, residual=z,
-                                   out_mask=out_mask)
+                                   out_mask=out_mask, out=dest(z))
 
         return att_pair(mul_pair(z)) if tri_mul_first else mul_pair(att_pair(z))
 
@@ -84,30 +104,39 @@ class PairformerLayerWeights:
         return None
 
     def _pair_transition(self, z, s, *, row_mask=None, out_mask=None, eps=1e-5):
+        """z += transition(z) in place (z is the triangle sublayers' own
+        output), with the single attention's pair bias when it applies."""
         att = self._pair_bias_prep(s, z)
         if att is None:
             return kernels.transition(z, self.transition_z, row_mask=row_mask, residual=z, eps=eps,
-                                      out_mask=out_mask), None
+                                      out_mask=out_mask, out=z), None
         return kernels.transition(z, self.transition_z, row_mask=row_mask, residual=z, eps=eps, out_mask=out_mask,
-                                  pair_bias_for=att, pair_bias_eps=eps)
+                                  pair_bias_for=att, pair_bias_eps=eps, out=z)
+
+    @staticmethod
+    def _s_dest(s, donate):
+        return s if donate and s is not None and s.is_contiguous() else None
 
     def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor | None, pair_mask: torch.Tensor | None,
-                eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
+                eps: float = 1e-5, *, donate: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """Boltz-2 ``pairformer_layer_forward`` (``B2K/pairformer.py:133-205``):
         z += tri-mul out, in, tri-attn start, end, transition; s +=
         attention(LN(s), z, mask); s += transition_s. The attention's pair
         bias LN_z(z) w_z^T comes out of the pair transition's epilogue (in
         float32 when s is float32 over a bfloat16 z), so z is not read a
-        further time."""
-        z = self.triangle.forward(z, pair_mask, eps=eps)
+        further time. The block allocates one pair tensor and one single
+        tensor for its outputs and updates them in place; with ``donate`` it
+        allocates neither and overwrites s and z (``TriangleSublayers.forward``)."""
+        z = self.triangle.forward(z, pair_mask, eps=eps, donate=donate)
         z, bias = self._pair_transition(z, s, eps=eps)
         s = kernels.single_attention(s, None if bias is not None else z, mask, self.attention, residual=s, eps=eps,
-                                     pair_bias=bias)
-        s = kernels.transition(s, self.transition_s, residual=s, eps=eps)
+                                     pair_bias=bias, out=self._s_dest(s, donate))
+        s = kernels.transition(s, self.transition_s, residual=s, eps=eps, out=s)
         return s, z
 
     def forward_protenix(self, s: torch.Tensor | None, z: torch.Tensor,
-                         pair_mask: torch.Tensor | None) -> tuple[torch.Tensor | None, torch.Tensor]:
+                         pair_mask: torch.Tensor | None, *, donate: bool = False
+                         ) -> tuple[torch.Tensor | None, torch.Tensor]:
         """Protenix ``pairformer_block`` (``PXK/pairformer.py:49-180``). Every
         sublayer's output is multiplied by ``pair_gate = bool(pair_mask)``
         inside its epilogue. Gating z (and s) on entry as well is not needed
@@ -117,11 +146,11 @@ class PairformerLayerWeights:
         pair mask) is the single attention's key mask with ``inf = 1e10`` and
         gates its output and the single transition's; the reference's extra
         bias ``-1e10`` on invalid query rows changes only rows that the gate
-        then zeroes."""
+        then zeroes. ``donate`` as for ``forward``."""
         valid = None
         if pair_mask is not None:
             valid = torch.diagonal(pair_mask, dim1=-2, dim2=-1).ne(0)
-        z = self.triangle.forward(z, pair_mask, out_mask=pair_mask)
+        z = self.triangle.forward(z, pair_mask, out_mask=pair_mask, donate=donate)
         z, bias = self._pair_transition(z, s, out_mask=pair_mask)
         if self.attention is None:
             if s is not None and valid is not None:
@@ -132,24 +161,24 @@ class PairformerLayerWeights:
         if self.transition_s is None:
             raise ValueError("missing single_transition for single path")
         s = kernels.single_attention(s, None if bias is not None else z, valid, self.attention, inf=1e10,
-                                     residual=s, pair_bias=bias, out_mask=valid)
-        s = kernels.transition(s, self.transition_s, residual=s, out_mask=valid)
+                                     residual=s, pair_bias=bias, out_mask=valid, out=self._s_dest(s, donate))
+        s = kernels.transition(s, self.transition_s, residual=s, out_mask=valid, out=s)
         return s, z
 
     def forward_openfold3(self, s: torch.Tensor, z: torch.Tensor, single_mask: torch.Tensor | None,
                           pair_mask: torch.Tensor | None, *, inf: float = 1e9, mask_transition: bool = True,
-                          eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
+                          eps: float = 1e-5, donate: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
         """OpenFold3 ``pairformer_block`` (``OF3/pairformer.py:42-102``): the
         pair block (``OF3/pair_block.py:106-190``), then s += attention with
         pair bias (key mask ``single_mask``, ``inf``) and the SwiGLU single
         transition, whose update is multiplied by ``single_mask`` when
-        ``mask_transition``."""
-        z = self.triangle.forward(z, pair_mask, inf=inf, eps=eps)
+        ``mask_transition``. ``donate`` as for ``forward``."""
+        z = self.triangle.forward(z, pair_mask, inf=inf, eps=eps, donate=donate)
         z, bias = self._pair_transition(z, s, row_mask=pair_mask if mask_transition else None, eps=eps)
         s = kernels.single_attention(s, None if bias is not None else z, single_mask, self.attention, inf=inf,
-                                     eps=eps, residual=s, pair_bias=bias)
+                                     eps=eps, residual=s, pair_bias=bias, out=self._s_dest(s, donate))
         s = kernels.transition(s, self.transition_s, row_mask=single_mask if mask_transition else None, residual=s,
-                               eps=eps)
+                               eps=eps, out=s)
         return s, z
 
     @classmethod

@@ -186,6 +186,11 @@ def pairformer_block(
     ``PairformerBlockParams`` (fields the reference's containers or packed
     weights) or a packed ``PairformerLayerWeights``. Chunk sizes are accepted
     and unused; the backend selectors are validated as upstream."""
+    _check_block_selectors(single_attention_backend, triangle_attention_backend)
+    return _packed_block(params, s, z).forward_protenix(s, z, pair_mask)
+
+
+def _check_block_selectors(single_attention_backend: str, triangle_attention_backend: str | None) -> None:
     _single_backend(single_attention_backend)
     backend = _triangle_attention_backend() if triangle_attention_backend is None else triangle_attention_backend
     if backend not in {"xla", "xla_jit", "tokamax", "cueq", "cueq_jit", "hip", "hip_jit"}:
@@ -197,10 +202,12 @@ def pairformer_block(
         raise ValueError(f"unsupported triangle multiplication backend: {mul!r}")
     if mul != "hip":
         raise RuntimeError(_REFERENCE_ONLY.format(kind="triangle multiplication", name=mul))
+
+
+def _packed_block(params, s: torch.Tensor | None, z: torch.Tensor) -> PairformerLayerWeights:
     sd = s.dtype if s is not None else z.dtype
-    block = params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_protenix(
+    return params if isinstance(params, PairformerLayerWeights) else PairformerLayerWeights.from_protenix(
         params, z.dtype, z.device, single_dtype=sd)
-    return block.forward_protenix(s, z, pair_mask)
 
 
 def stack_pairformer_block_params(blocks, dtype: torch.dtype | None = None, device=None) -> StackedLayers:
@@ -242,13 +249,9 @@ def pairformer_stack(
         blocks = stacked_or_stack([b if isinstance(b, PairformerLayerWeights)
                                    else PairformerLayerWeights.from_protenix(b, z.dtype, z.device, single_dtype=sd)
                                    for b in blocks])
-    for block in blocks:
-        s, z = pairformer_block(
-            s, z, pair_mask, block,
-            triangle_mul_chunk_size=triangle_mul_chunk_size,
-            triangle_att_q_chunk_size=triangle_att_q_chunk_size,
-            single_att_q_chunk_size=single_att_q_chunk_size,
-            single_attention_backend=single_attention_backend,
-            triangle_attention_backend=triangle_attention_backend,
-        )
+    _check_block_selectors(single_attention_backend, triangle_attention_backend)
+    # the first block writes new s and z, every later one updates them in
+    # place (the reference's scan donates its carry)
+    for idx, block in enumerate(blocks):
+        s, z = _packed_block(block, s, z).forward_protenix(s, z, pair_mask, donate=idx > 0)
     return s, z

@@ -104,7 +104,9 @@ typedef struct fjx_trimul_args {
   const void* norm_out_bias;   /* [c_h] */
   const void* p_out_weight;    /* [c_z, c_h] */
   const void* g_out_weight;    /* [c_z, c_z] */
-  const void* residual;        /* NULL, or [batch, n, n, c_z] added to the update; may equal out */
+  const void* residual;        /* NULL, or [batch, n, n, c_z] added to the update; x, residual and out
+                                  may be one buffer (in place: every position's inputs are read before
+                                  it is written, by the workgroup that writes it) */
   void* out;                   /* [batch, n, n, c_z] */
   void* workspace;
   size_t workspace_bytes;
@@ -176,7 +178,7 @@ typedef struct fjx_triattn_args {
   const void* v_weight;     /* [heads*head_dim, c_z] */
   const void* g_weight;     /* [heads*head_dim, c_z], or NULL for an ungated module */
   const void* o_weight;     /* [c_z, heads*head_dim] */
-  const void* residual;     /* NULL, or [batch, n, n, c_z]; may equal out */
+  const void* residual;     /* NULL, or [batch, n, n, c_z]; x, residual and out may be one buffer */
   void* out;                /* [batch, n, n, c_z] */
   void* workspace;
   size_t workspace_bytes;
@@ -256,7 +258,7 @@ typedef struct fjx_transition_args {
   const void* w_b;
   const void* w_o;
   const void* row_mask;  /* [rows] or NULL */
-  const void* residual;  /* [rows, c] or NULL; may equal out */
+  const void* residual;  /* [rows, c] or NULL; x, residual and out may be one buffer */
   void* out;             /* [rows, c] */
   int64_t hidden;        /* 0 for 4c */
   void* workspace;       /* general path only; may be NULL when the size is 0 */

@@ -176,6 +176,85 @@ def test_config3_block_sublayers_n1024():
     run_layer_checked(1024, 1024 - 51, seed=2, tag="config3")
 
 
+def test_config3_block_fp32_single_track_n1024():
+    """The precision split that ``bench.py`` times at config 3: the pair track
+    in bf16, s and the single-track weights in fp32, as Boltz-2 runs it
+    (``B2K/pairformer.py:182-199``). The pair transition then writes the
+    attention's bias in fp32 from its epilogue (``transition128_pbf32_kernel``,
+    its persistent multi-tile walk at N=1024):
+
+    * its z equals the plain bf16 transition's, bit for bit, and matches the
+      oracle at sampled positions (bf16 bar);
+    * its fp32 bias matches ``LN_z(z) W_z^T`` of the GPU's bf16 z at sampled
+      positions to the fp32 bar (max-abs 1e-4), and the whole bias equals the
+      standalone fp32 pair-bias pass within that bar;
+    * the fp32 single attention fed that bias matches the oracle's rows (given
+      the GPU's z) to the fp32 bar, and so does the fp32 single transition;
+    * ``PairformerLayerWeights.forward`` -- the bench's step -- gives the same
+      s and z, bit for bit, as the sublayer-by-sublayer run checked here."""
+    n, n_real, seed = 1024, 1024 - 51, 2
+    f32 = torch.float32
+    w = syn.pairformer_layer_weights(seed=seed)
+    wq = prep_tree(w, BF16)
+    att = w["attention"]  # the single track keeps its float32 weights
+    layer = PairformerLayerWeights.from_fields(w, BF16, "cuda", single_dtype=f32)
+    assert layer.attention.z_weight.dtype == f32
+    pm_np = syn.pair_mask(n, n_real)
+    tm_np = syn.token_mask(n, n_real)
+    pm = torch.from_numpy(pm_np[None]).to("cuda", BF16)
+    tm = torch.from_numpy(tm_np[None]).to("cuda", f32)
+    z0 = device_normal((1, n, n, 128), seed=seed + 200)
+    s0 = torch.from_numpy(syn.single_input(n, 384, seed=1, batch=1)).to("cuda", f32)
+    pos = positions(n, n_real, seed + 1)
+
+    say("config3 fp32 single track: triangle sublayers (bf16 pair track)")
+    z_tri = layer.triangle.forward(z0, pm)
+    say("config3 fp32 single track: pair transition with the fp32 pair bias")
+    plain = kernels.transition(z_tri, layer.transition_z, residual=z_tri)
+    z1, pb = kernels.transition(z_tri, layer.transition_z, residual=z_tri, pair_bias_for=layer.attention)
+    torch.cuda.synchronize()
+    assert pb.dtype == f32 and tuple(pb.shape) == (1, 16, n, n)
+    assert torch.equal(z1, plain), "pbf32 transition z differs from the plain transition"
+    rows_in = gather(z_tri[0], pos)
+    check_rows(gather(z1[0], pos), rows_in + O.transition(rows_in, wq["transition_z"]), "config3 pair transition")
+
+    zl = Lines(z1[0])
+    want_pb = O.pair_bias_at(att, zl, pos)  # [P, H] from the GPU's bf16 z, fp32 weights
+    idx = torch.tensor(pos, device="cuda", dtype=torch.long)
+    got_pb = pb[0][:, idx[:, 0], idx[:, 1]].double().cpu().numpy().T / LOG2E
+    err_pb = float(np.max(np.abs(got_pb - want_pb)))
+    say(f"  fp32 pair bias at {len(pos)} positions: max-abs {err_pb:.2e}")
+    assert err_pb <= 1e-4, f"fused fp32 pair bias max-abs {err_pb:.2e} > 1e-4"
+
+    say("config3 fp32 single track: single attention from the fused bias and from z itself")
+    s1 = kernels.single_attention(s0, None, tm, layer.attention, residual=s0, pair_bias=pb)
+    s1_z = kernels.single_attention(s0, z1, tm, layer.attention, residual=s0)
+    torch.cuda.synchronize()
+    assert s1.dtype == f32
+    err_paths = float((s1 - s1_z).abs().max())
+    assert err_paths <= 1e-4, f"fused-bias vs standalone-bias attention max-abs {err_paths:.2e}"
+    s_np = s0[0].double().cpu().numpy()
+    s_ln = O.layer_norm(s_np, att["pre_norm_s"]["weight"], att["pre_norm_s"]["bias"])
+    queries = sorted(q for q in {0, 1, 255, 256, n // 3, n_real - 1, n_real, n - 1} if q < n)
+    want_s = s_np[queries] + O.boltz2_attention_pair_bias_at(att, s_ln, zl, tm_np, queries)
+    err_s = float(np.max(np.abs(s1[0].double().cpu().numpy()[queries] - want_s)))
+    say(f"  fp32 single attention rows {queries}: max-abs {err_s:.2e}")
+    assert err_s <= 1e-4, f"fp32 single attention max-abs {err_s:.2e} > 1e-4"
+
+    say("config3 fp32 single track: single transition")
+    s2 = kernels.transition(s1, layer.transition_s, residual=s1)
+    s1_np = s1[0].double().cpu().numpy()
+    want_s2 = s1_np + O.transition(s1_np, w["transition_s"])
+    err_t = float(np.max(np.abs(s2[0].double().cpu().numpy() - want_s2)))
+    say(f"  fp32 single transition: max-abs {err_t:.2e}")
+    assert err_t <= 1e-4, f"fp32 single transition max-abs {err_t:.2e} > 1e-4"
+
+    say("config3 fp32 single track: the bench's layer forward")
+    fs, fz = layer.forward(s0, z0, tm, pm)
+    torch.cuda.synchronize()
+    assert torch.equal(fz, z1) and torch.equal(fs, s2), "layer.forward differs from the checked sublayer run"
+
+
 def test_config4_layer_n2048():
     """BASELINE config 4's layer at N=2048 (all-ones mask), sublayer by sublayer."""
     run_layer_checked(2048, 2048, seed=5, tag="config4")
