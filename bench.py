@@ -105,51 +105,24 @@ def _rows_model(fn, r1: int, r2: int, n: int) -> float:
     return t1 + (n - r1) * per_row
 
 
-def _trimul_sample_s(O, z, pm, p, n: int, pos_div: int = 16, ch: int = 16) -> float:
-    """Seconds of one float32 tri-mul (``oracle.protenix_triangle_multiplication``)
-    at size n from two exact samples: its per-position steps (LN_in, the four
-    gated input projections, LN_out, the output projection and gate) on
-    1/pos_div of the positions, and the contraction on ``ch`` of its 128
-    channels; each part scales linearly to the whole."""
-    import numpy as np
-
-    x, m = z[:, : n // pos_div], pm[:, : n // pos_div]
-
-    def per_position():
-        zn = O.layer_norm(x, *O._ln_params(p["layer_norm_in"]))
-        mm = m[..., None]
-        a = mm * O.sigmoid(O.linear_torch(zn, p["linear_a_g"])) * O.linear_torch(zn, p["linear_a_p"])
-        b = mm * O.sigmoid(O.linear_torch(zn, p["linear_b_g"])) * O.linear_torch(zn, p["linear_b_p"])
-        o = O.layer_norm(a + b, *O._ln_params(p["layer_norm_out"]))  # stands in for the contraction output
-        return O.linear_torch(o, p["linear_z"]) * O.sigmoid(O.linear_torch(zn, p["linear_g"]))
-
-    rng = np.random.default_rng(0)
-    a = rng.standard_normal((1, n, n, ch), dtype=np.float32)
-    b = rng.standard_normal((1, n, n, ch), dtype=np.float32)
-    t_pos, _ = _median_time(per_position, 0.0, 1)
-    t_con, _ = _median_time(lambda: O.triangle_contract(a, b, "outgoing"), 0.0, 1)
-    return t_pos * pos_div + t_con * (128 / ch)
-
-
 def cpu_baseline(n: int, n_real: int, with_configs: bool = True) -> dict:
     """The float32 numpy restatement (``oracle/``, the reference's XLA path in
-    fp32) timed on this host's cores at the headline size, on a bounded
-    sample whose work scales exactly to the whole block:
+    fp32) timed on this host's cores at the headline size. Every part runs
+    whole on the block's own inputs except the two triangle attentions,
+    which dominate and are sampled by rows:
 
-    * tri-mul outgoing at N: its per-position steps on 1/16 of the positions
-      and its contraction on 16 of the 128 channels, each scaled linearly;
-      incoming is the same work transposed and is counted as a second
-      outgoing;
-    * tri-attn starting node at N, on r1 and r2 of the N rows, extrapolated
-      linearly in rows (rows are independent; the LayerNorm and bias of the
-      whole grid are in both samples); the ending node counted as a second
-      starting node;
-    * the pair transition on 1/32 of the positions, times 32;
-    * the single attention with pair bias and the single transition, whole.
+    * tri-mul outgoing and incoming, whole;
+    * tri-attn starting and ending node, each on r1 and r2 of its N rows,
+      extrapolated linearly in rows (rows are independent; the LayerNorm and
+      bias of the whole grid are in both samples, and the ending node samples
+      its own transposed grid);
+    * the pair transition, the single attention with pair bias and the
+      single transition, whole.
 
-    Also times config 1 of the baseline table whole (tri-mul out+in at N=256
-    in fp32) and config 2 (tri-attn start+end at N=384, 346 real tokens) by
-    the same row extrapolation."""
+    ``--cpu-whole`` checks this sample model against the whole block.
+    Also times config 1 of the baseline table (tri-mul out+in at N=256 in
+    fp32) and config 2 (tri-attn start+end at N=384, 346 real tokens),
+    whole."""
     import numpy as np
 
     from foldjax_amd import synthetic as syn
@@ -170,12 +143,14 @@ def cpu_baseline(n: int, n_real: int, with_configs: bool = True) -> dict:
     r1, r2 = 8, 56
     parts = {}
     with O.compute_dtype(np.float32):
-        parts["trimul_out"] = _trimul_sample_s(O, z, pm, w["tri_mul_out"], n)
-        parts["triattn_start"] = _rows_model(
-            lambda r: O.protenix_triangle_attention(z, pm, w["tri_att_start"], num_heads=4, rows=np.arange(r)),
-            r1, r2, n)
-        zs = z[:, : n // 32]
-        parts["transition_z"] = 32 * _median_time(lambda: O.transition(zs, w["transition_z"]), 0.0, 1)[0]
+        z = z.astype(np.float32)
+        for key, d in (("tri_mul_out", "outgoing"), ("tri_mul_in", "incoming")):
+            parts[key], _ = _median_time(lambda key=key, d=d: O.protenix_triangle_multiplication(z, pm, w[key], d),
+                                         0.0, 1)
+        for key, st in (("tri_att_start", True), ("tri_att_end", False)):
+            parts[key] = _rows_model(lambda r, key=key, st=st: O.protenix_triangle_attention(
+                z, pm, w[key], num_heads=4, starting=st, rows=np.arange(r)), r1, r2, n)
+        parts["transition_z"], _ = _median_time(lambda: O.transition(z, w["transition_z"]), 0.0, 1)
         a = w["attention"]
 
         def single():
@@ -184,7 +159,7 @@ def cpu_baseline(n: int, n_real: int, with_configs: bool = True) -> dict:
             return s2 + O.transition(s2, w["transition_s"])
 
         parts["single_track"], _ = _median_time(single, 0.0, 1)
-    total = 2 * parts["trimul_out"] + 2 * parts["triattn_start"] + parts["transition_z"] + parts["single_track"]
+    total = sum(parts.values())
     out = {
         "value": round(total * 1e3, 1),
         "unit": "ms",
@@ -192,13 +167,13 @@ def cpu_baseline(n: int, n_real: int, with_configs: bool = True) -> dict:
         "kind": "port",
         "sample": (
             f"float32 numpy restatement of the reference's XLA path (oracle/triangle.py) at N={n} ({n_real} real "
-            f"tokens), BLAS on {blas} threads, elementwise numpy on one: tri-mul outgoing from its per-position "
-            f"steps on 1/16 of the positions and its contraction on 16 of 128 channels, each scaled linearly "
-            f"({parts['trimul_out']:.1f} s, counted for both directions); tri-attn starting node on {r1} and {r2} "
-            f"rows extrapolated linearly to {n} ({parts['triattn_start']:.1f} s, counted for both nodes); pair "
-            f"transition on 1/32 of the positions x32 ({parts['transition_z']:.1f} s); single track whole "
-            f"({parts['single_track']:.2f} s)"
+            f"tokens), BLAS on {blas} threads, elementwise numpy on one: tri-mul outgoing and incoming whole "
+            f"({parts['tri_mul_out']:.1f} + {parts['tri_mul_in']:.1f} s); tri-attn starting and ending node each "
+            f"on {r1} and {r2} of its rows, extrapolated linearly to {n} ({parts['tri_att_start']:.1f} + "
+            f"{parts['tri_att_end']:.1f} s); pair transition whole ({parts['transition_z']:.1f} s); single track "
+            f"whole ({parts['single_track']:.2f} s)"
         ),
+        "parts_s": {k: round(v, 3) for k, v in parts.items()},
     }
     if not with_configs:
         return out

@@ -393,20 +393,37 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
     if (lane == 0) P.fallback[blockIdx.x] = 1u;
     return;
   }
+  // Output: lane (li, g) holds dims 4g .. 4g+3 and 16 + 4g .. +3 of query
+  // li. Two lane swaps (lanes 32 apart, then 16 apart; the query stays) give
+  // it dims 8g .. 8g+7 instead, so each query's 64 bytes leave as four
+  // 16-byte stores of one instruction: whole cache lines, not 8-byte pieces
+  // written by two instructions.
   bf16* OUT = P.out + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head;
+  auto pack2 = [](float x, float y) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(x)) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(y)) << 16);
+  };
 #pragma unroll
   for (int qt = 0; qt < NQT; ++qt) {
     const float ls = __shfl(lsum[qt >> 2][0], 16 * (qt & 3) + li, 64);
     const float inv = 1.0f / ls;
     const int64_t q = q0 + qw + 16 * qt + li;
-    if (q >= n) continue;
+    uint32_t a[2], c[2];  // a: dims 4g .., c: dims 16 + 4g ..
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
-      float v[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = o[qt][dt][r] * inv;
-      store4f(OUT + q * P.o_stride_q + 16 * dt + 4 * lg, v);
+    for (int e = 0; e < 2; ++e) {
+      a[e] = pack2(o[qt][0][2 * e] * inv, o[qt][0][2 * e + 1] * inv);
+      c[e] = pack2(o[qt][1][2 * e] * inv, o[qt][1][2 * e + 1] * inv);
     }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      // lanes 0-31 keep a and take c of lanes 0-31; lanes 32-63 the a and c of lanes 32-63
+      const auto s32 = __builtin_amdgcn_permlane32_swap(a[e], c[e], false, false);
+      // then rows of 16: row 0 keeps its own and takes row 1's, and so on
+      const auto s16 = __builtin_amdgcn_permlane16_swap(s32[0], s32[1], false, false);
+      a[e] = s16[0];  // dims 8g .. 8g+3
+      c[e] = s16[1];  // dims 8g+4 .. 8g+7
+    }
+    if (q < n) *reinterpret_cast<u32x4*>(OUT + q * P.o_stride_q + 8 * lg) = u32x4{a[0], a[1], c[0], c[1]};
   }
 }
 

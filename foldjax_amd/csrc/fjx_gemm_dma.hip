@@ -14,7 +14,10 @@
 // so the fragment reads of 16 consecutive rows hit 16 bank groups. The DMA
 // goes through buffer resources sized to the operands, and a lane whose chunk
 // lies past K gets an offset past the resource's end: rows past M or N and
-// the k tail read as zero, so any M, N and K (K a multiple of 8) work.
+// the k tail read as zero, so any M, N and K (K a multiple of 8) work. A
+// lane's whole row offset is in its vector offset: the raw-buffer range check
+// covers the vector and instruction offsets, not the scalar one, which
+// carries only the k offset.
 //
 // Persistent: one workgroup per CU walks its XCD's contiguous share of the
 // tiles, n-tiles fastest, so an A row block is reused from that XCD's L2 by
@@ -79,7 +82,8 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
   // row 32 wave + 16 (j % 2) + 4 (j / 2) + 8 (lane bit 5) + (lane / 8) % 4
   // (the permuted order above). The swizzle of r depends on j only through
   // j % 2, so two per-lane offsets per operand serve all four instructions,
-  // the rest (16 A rows or 4 B rows per two instructions) is uniform
+  // plus a uniform step (16 A rows or 4 B rows per two instructions) added
+  // to the lane's offset
   uint32_t aoff[2], boff[2];
   int kc[2];
 #pragma unroll
@@ -113,16 +117,19 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
     // the k offset and the uniform row offset go in the scalar offset; a
     // lane whose chunk lies past K reads from past the resource's end
     const bool in0 = k0 + kc[0] < K, in1 = k0 + kc[1] < K;
-    const uint32_t ao[2] = {in0 ? aoff[0] : kGOob, in1 ? aoff[1] : kGOob};
-    const uint32_t bo[2] = {in0 ? boff[0] : kGOob, in1 ? boff[1] : kGOob};
+    // opaque here, so the sums below are formed per call rather than hoisted
+    // into loop-invariant registers (which would spill)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(aoff[j]), "+v"(boff[j]));
 #pragma unroll
     for (int j = 0; j < kGNI; ++j) {
+      const bool kin = (j & 1) ? in1 : in0;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           tl.ra, (__attribute__((address_space(3))) void*)(&S[st][0][(32 * wave + kGRPI * j) * kGDK]), 16,
-          ao[j & 1], (uint32_t)(2 * k0) + (uint32_t)(j >> 1) * astep, 0, 0);
+          kin ? aoff[j & 1] + (uint32_t)(j >> 1) * astep : kGOob, (uint32_t)(2 * k0), 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           tl.rb, (__attribute__((address_space(3))) void*)(&S[st][1][(32 * wave + kGRPI * j) * kGDK]), 16,
-          bo[j & 1], (uint32_t)(2 * k0) + (uint32_t)(j >> 1) * bstep, 0, 0);
+          kin ? boff[j & 1] + (uint32_t)(j >> 1) * bstep : kGOob, (uint32_t)(2 * k0), 0, 0);
     }
   };
 

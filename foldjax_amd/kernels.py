@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass, fields
+from typing import ClassVar
 
 import torch
 
@@ -160,6 +161,10 @@ class TransitionWeights:
 class SingleAttentionWeights:
     """Boltz-2 ``AttentionPairBias`` weights (PyTorch ``[out, in]``) plus the
     layer's ``pre_norm_s`` (None when the caller passes a normalised s)."""
+
+    # fields a packed layer keeps back to back in one buffer (one projection
+    # GEMM); stacking layers keeps them so (foldjax_amd.stacking)
+    STACK_GROUPS: ClassVar[tuple[tuple[str, ...], ...]] = (("q_weight", "k_weight", "v_weight", "g_weight"),)
 
     pre_norm_weight: torch.Tensor | None
     pre_norm_bias: torch.Tensor | None

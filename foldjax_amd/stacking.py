@@ -41,7 +41,25 @@ def _stack_leaf(leaves: Sequence[Any]):
         if any(type(leaf) is not type(first) for leaf in leaves):
             raise ValueError("cannot stack layers of differing structure")
         bufs, views = {}, [dict() for _ in leaves]
+        grouped = set()
+        # field groups a packed layer keeps back to back in one buffer (e.g.
+        # the single attention's q|k|v|g, run as one projection GEMM) stay
+        # back to back: one [L, len(group) * rows, ...] buffer, each layer's
+        # fields consecutive slices of its row
+        for group in getattr(type(first), "STACK_GROUPS", ()):
+            parts = [[getattr(leaf, name) for name in group] for leaf in leaves]
+            flat = [t for p in parts for t in p]
+            if any(t is None for t in flat) or len({(tuple(t.shape), t.dtype, t.device) for t in flat}) != 1:
+                continue
+            buf = torch.stack([torch.cat(p, 0) for p in parts], 0).contiguous()
+            bufs["|".join(group)] = buf
+            for i in range(len(leaves)):
+                for name, x in zip(group, buf[i].chunk(len(group), 0)):
+                    views[i][name] = x
+            grouped.update(group)
         for f in dataclasses.fields(first):
+            if f.name in grouped:
+                continue
             b, v = _stack_leaf([getattr(leaf, f.name) for leaf in leaves])
             bufs[f.name] = b
             for i, x in enumerate(v):

@@ -390,8 +390,10 @@ def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, in
         mask = np.ones(x.shape[:-1])
     mask = _f(mask)
     if not starting:
-        x = np.swapaxes(x, -2, -3)
-        mask = np.swapaxes(mask, -1, -2)
+        # the transposed grid as its own array: numpy runs every later op of
+        # the whole-grid computation on it at the speed of a contiguous one
+        x = np.ascontiguousarray(np.swapaxes(x, -2, -3))
+        mask = np.ascontiguousarray(np.swapaxes(mask, -1, -2))
     x = layer_norm(x, *_ln_params(_get(params, "layer_norm")))
     mask_bias = (inf * (mask - 1.0))[..., :, None, None, :]
     tri_bias = linear_torch(x, _get(params, "linear"))
@@ -411,7 +413,7 @@ def protenix_triangle_attention(x, mask, params, *, num_heads, starting=True, in
     o = o.reshape(o.shape[:-2] + (-1,))
     out = linear_torch(o, _get(att, "linear_o"))
     if not starting and rows is None:
-        out = np.swapaxes(out, -2, -3)
+        out = np.ascontiguousarray(np.swapaxes(out, -2, -3))
     return out
 
 

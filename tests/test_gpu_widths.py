@@ -175,7 +175,45 @@ def test_narrow_separate_residual_and_out_mask(dt, c_z):
         assert_parity(g, w_, dtype, f"narrow triattn starting={starting} residual")
 
 
-@pytest.mark.parametrize("c,rows,masked", [(384, 8300, True), (264, 8300, False)])
+def test_single_projection_dma_gemm_row_tail_caller_operand_bf16():
+    """The q|k|v|g projection of a single attention without a pre-norm reads
+    the caller's s as the LDS-DMA GEMM's A operand (72 tiles of 256 x 256 at
+    n = 2839). n % 256 = 23, so in the last row tile 9 of the first 32-row
+    group's rows and every row of the other groups lie past s: each DMA
+    instruction's row is tested against M through the buffer range check,
+    and such rows read zero instead of the memory that follows s. Here s is a
+    tensor of exactly n rows; the attention rows, the last ones included,
+    match the oracle (a row read from past s would only reach output rows that
+    are not stored, so the test pins the tail's results, not the absence of
+    the read, which the range check guarantees)."""
+    n, n_real, dtype = 2839, 2830, torch.bfloat16
+    say(f"single attention no pre-norm, dma gemm row tail n={n}")
+    w = syn.single_attention_weights(heads=16, seed=71)
+    att, _ = P.single_attention_to_boltz2(w)
+    aw = P.pack_single_attention_boltz2(att, dtype, "cuda", pre_norm=None)
+    s_np = syn.single_input(n, 384, seed=72)
+    s = torch.empty((n, 384), device="cuda", dtype=dtype)
+    s.copy_(torch.from_numpy(s_np))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(73)
+    z = torch.randn((1, n, n, 128), generator=g, device="cuda", dtype=torch.float32).to(dtype)
+    tm = syn.token_mask(n, n_real)
+    got = kernels.single_attention(s[None], z, device_tensor(tm[None], dtype), aw)
+    torch.cuda.synchronize()
+    queries = [0, 1, 2560, 2815, 2816, n - 9, n - 1]
+    zl = lambda i: z[0, i].float().cpu().numpy().astype(np.float64)  # noqa: E731
+
+    class Rows:
+        def __getitem__(self, i):
+            return zl(int(i))
+
+    wq = prep_tree(w, dtype)
+    want = O.boltz2_attention_pair_bias_at({k: wq[k] for k in wq if k != "pre_norm_s"}, prep(s_np, dtype), Rows(),
+                                            tm, queries)
+    assert_parity(to_np(got[0])[queries], want, dtype, "single attention rows past the last full tile")
+
+
+@pytest.mark.parametrize("c,rows,masked", [(384, 8300, True), (264, 8300, False), (384, 8215, False)])
 def test_transition_wide_rows_dma_gemm_bf16(c, rows, masked):
     """Wide transitions over enough rows that their GEMMs run on the LDS-DMA
     kernel (64 or more 256 x 256 tiles): c = 384 (K = 384 and 1536, even

@@ -236,6 +236,33 @@ def test_stacked_layers_share_one_buffer_per_weight_kind():
         stacked_or_stack([])
 
 
+def test_stacking_keeps_single_attention_projections_back_to_back():
+    """A packed single attention keeps q|k|v|g in one buffer, so the library
+    runs one projection GEMM (``fjx_single_attention_fwd``); the stacked
+    layers' views keep that layout: each layer's four weights are consecutive
+    slices of one [4 c_s, c_s] row of a [L, 4 c_s, c_s] buffer."""
+    from foldjax_amd.pairformer import PairformerLayerWeights
+    from foldjax_amd.stacking import stacked_or_stack
+
+    ls = [PairformerLayerWeights.random(torch.float32, "cpu", seed=i) for i in (3, 4, 5)]
+    c = int(ls[0].attention.q_weight.shape[0])
+    step = c * c * ls[0].attention.q_weight.element_size()
+
+    def back_to_back(a):
+        ptrs = [getattr(a, k).data_ptr() for k in ("q_weight", "k_weight", "v_weight", "g_weight")]
+        return all(p1 - p0 == step for p0, p1 in zip(ptrs, ptrs[1:]))
+
+    assert all(back_to_back(layer.attention) for layer in ls)
+    st = stacked_or_stack(ls)
+    buf = st.stacked["attention"]["q_weight|k_weight|v_weight|g_weight"]
+    assert tuple(buf.shape) == (3, 4 * c, c)
+    for i, layer in enumerate(st):
+        a = layer.attention
+        assert back_to_back(a) and a.q_weight.data_ptr() == buf[i].data_ptr()
+        for k in ("q_weight", "k_weight", "v_weight", "g_weight", "o_weight"):
+            assert torch.equal(getattr(a, k), getattr(ls[i].attention, k))
+
+
 def test_neutral_triangle_kernel_knob():
     """``triangle_kernel`` (``src/foldjax/execution.py:43``) gains "hip";
     "auto" maps to it explicitly on every port, the reference's values keep

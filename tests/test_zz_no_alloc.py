@@ -51,6 +51,14 @@ def test_noalloc_refuses_shapes_beyond_scratch():
     w = P.pack_trimul_torch(P.trimul_to_protenix(syn.trimul_weights(seed=1)), torch.bfloat16, "cuda")
     with pytest.raises(_lib.FjxError, match="static scratch holds"):
         kernels.trimul(z, None, w, "outgoing", no_alloc=True)
-    # the largest bf16 shape that fits still runs
+    # the largest bf16 shape that fits runs, close to the scratch's end, and
+    # matches the workspace entry bit for bit
     n_fit = 591
     assert lib.fjx_trimul_workspace_size(1, n_fit, 128, 128, _lib.FJX_DTYPE_BF16) <= _lib.NOALLOC_SCRATCH_BYTES
+    assert lib.fjx_trimul_workspace_size(1, n_fit + 1, 128, 128, _lib.FJX_DTYPE_BF16) > _lib.NOALLOC_SCRATCH_BYTES
+    say(f"noalloc trimul at the scratch limit n={n_fit}")
+    z, m, w = _case(n_fit, torch.bfloat16, 7)
+    want = kernels.trimul(z, m, w, "incoming", residual=z)
+    got = kernels.trimul(z, m, w, "incoming", residual=z, no_alloc=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want), f"n={n_fit}: noalloc output differs from fjx_trimul_fwd"
