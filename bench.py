@@ -20,6 +20,9 @@ headline workload and on configs 1 and 2.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--n N] [--no-cpu] [--no-configs]
     python bench.py --op trimul|triattn|transition|transition_pb|copy   (one sublayer kind, a profiling aid)
+    python bench.py --n 2048 --pad-frac 0 --layers 48 --no-cpu --no-configs   (config 4's trunk, per kernel)
+    python bench.py --n 3072 --pad-frac 0.01953125 --no-cpu --no-configs      (config 5's block, per kernel)
+    python bench.py --cpu-whole [--n N]   (the whole block on the CPU beside the sampled estimate)
 """
 
 from __future__ import annotations
@@ -52,13 +55,18 @@ def _args():
     p.add_argument("--single-dtype", default="fp32", choices=["fp32", "bf16"],
                    help="the single track's dtype: fp32 as the reference runs it over the bf16 pair track "
                         "(B2K/pairformer.py:182-199), or bf16")
-    p.add_argument("--op", default="block", choices=["block", "trimul", "triattn", "transition", "transition_pb", "copy"],
-                   help="profiling aid: run only one sublayer kind per step instead of the whole block")
+    p.add_argument("--op", default="block",
+                   choices=["block", "trimul", "triattn", "transition", "transition_pb", "copy", "mixprobe"],
+                   help="profiling aid: run only one sublayer kind per step instead of the whole block; mixprobe: "
+                        "the issue rate of the flash attention's per-tile instruction mix alone")
     p.add_argument("--c-z", type=int, default=128,
                    help="with --op trimul|triattn|transition: the pair width (other than 128 runs the general-width "
                         "paths, e.g. 64 for the template stack, 384 for OpenDDE's structural pair track)")
     p.add_argument("--c-h", type=int, default=128, help="with --op trimul: the hidden width")
     p.add_argument("--heads", type=int, default=4, help="with --op triattn: heads of 32 channels")
+    p.add_argument("--layers", type=int, default=1,
+                   help="with --op block: layers per step, each with its own weights (48 at --n 2048 --pad-frac 0 is "
+                        "BASELINE config 4's trunk; the per-kernel averages then cover the whole trunk)")
     p.add_argument("--cpu-whole", action="store_true",
                    help="no GPU work: time the whole block at --n on the CPU once, beside the sampled estimate "
                         "the bench line reports (checks the sample model)")
@@ -233,6 +241,60 @@ def cpu_whole_block(n: int, n_real: int) -> dict:
     }
 
 
+def hbm_bytes_per_launch(n: int, single_dtype) -> dict:
+    """Algorithmic HBM bytes of one launch of the block's memory-bound
+    kernels at size n (bf16 pair tensor, c = 128): each input and output
+    element once. Pair row = 128 x 2 B.
+
+    * tri-mul prologue: x and the mask in, a and b out (channel-major);
+    * tri-mul epilogue: o and x in (x for the output gate and the residual),
+      z out;
+    * tri-attn prologue: x and the mask in; q, k, v, the [4, N, N] bias and
+      the [N, N] fp32 mask bias out;
+    * tri-attn epilogue: o and x in, z out;
+    * pair transition: x in, z out, plus the single attention's [16, N, N]
+      pair bias (fp32 for an fp32 single track)."""
+    row = 128 * 2
+    pos = n * n
+    mask = pos * 2
+    pb = 16 * pos * (4 if str(single_dtype).endswith("float32") else 2)
+    return {
+        "trimul_prologue": 3 * pos * row + mask,
+        "trimul_epilogue": 3 * pos * row,
+        "triattn_prologue": 4 * pos * row + mask + 4 * pos * 2 + pos * 4,
+        "triattn_epilogue": 3 * pos * row,
+        "transition": 2 * pos * row + pb,
+    }
+
+
+MIXES = {0: "flash tile: 10 MFMA + 16 exp + 24 VALU", 1: "without the bias widenings: 10 MFMA + 16 exp + 8 VALU",
+         2: "10 MFMA alone", 3: "16 exp alone", 4: "24 VALU alone"}
+
+
+def mix_probe(n: int) -> dict:
+    """``fjx_probe_issue_mix``: each mix at 1-4 waves per SIMD; ns for one
+    SIMD to issue one tile's instructions, and that rate times the tiles one
+    SIMD runs in a flash launch at size n (4 heads, 16 x 64 tiles over 256 CUs
+    x 4 SIMDs) -- the issue floor of the launch."""
+    import torch
+
+    from foldjax_amd import _lib
+
+    torch.zeros(1, device="cuda")  # the device context
+    iters = 2000
+    simds = torch.cuda.get_device_properties(0).multi_processor_count * 4
+    tiles_per_simd = n * 4 * (n // 16) * (n // 64) / simds
+    out = {"op": "mixprobe", "n": n, "iters": iters, "simds": simds, "tiles_per_simd": tiles_per_simd, "mixes": {}}
+    for mix, what in MIXES.items():
+        row = {"mix": what}
+        for w in (1, 2, 3, 4):
+            ms = _lib.probe_issue_mix(mix, w, iters)
+            ns = ms * 1e6 / (iters * w)
+            row[f"waves{w}"] = {"ns_per_tile": round(ns, 2), "floor_ms": round(ns * tiles_per_simd / 1e6, 4)}
+        out["mixes"][str(mix)] = row
+    return out
+
+
 def _timed(fn, steps: int, warmup: int, dev) -> float:
     import torch
 
@@ -332,6 +394,10 @@ def main() -> int:
     from foldjax_amd import synthetic as syn
     from foldjax_amd.pairformer import PairformerLayerWeights, flops_block, flops_triangle
 
+    if a.op == "mixprobe":
+        print(json.dumps(mix_probe(a.n)))
+        return 0
+
     dev = torch.device("cuda:0")
     dtype = torch.bfloat16
     sdt = torch.float32 if a.single_dtype == "fp32" else torch.bfloat16
@@ -342,8 +408,19 @@ def main() -> int:
     tmask = torch.from_numpy(syn.token_mask(n, n_real)[None]).to(dev, sdt)
     pmask = torch.from_numpy(syn.pair_mask(n, n_real)[None]).to(dev, dtype)
     layer = PairformerLayerWeights.random(dtype, dev, seed=2, single_dtype=sdt)
+    # further layers of a trunk (--layers), each with its own weights
+    more = [PairformerLayerWeights.random(dtype, dev, seed=2 + i, single_dtype=sdt) for i in range(1, a.layers)]
 
     from foldjax_amd import kernels
+
+    def block_step():
+        # the first layer writes new s and z (the inputs stay as they are for
+        # the next step), every further one updates them in place, as the
+        # stacks do
+        s, z = layer.forward(s0, z0, tmask, pmask)
+        for lay in more:
+            s, z = lay.forward(s, z, tmask, pmask, donate=True)
+        return s, z
 
     tri = layer.triangle
     if a.op in ("trimul", "triattn", "transition") and (a.c_z, a.c_h, a.heads) != (128, 128, 4):
@@ -355,7 +432,7 @@ def main() -> int:
             PP.triattn_to_protenix(syn.triattn_weights(a.c_z, a.heads, 32, seed=4)), dtype, dev)
         layer.transition_z = PP.pack_transition_torch(syn.transition_weights(a.c_z, seed=5), dtype, dev)
     steps_fn = {
-        "block": lambda: layer.forward(s0, z0, tmask, pmask),
+        "block": block_step,
         "trimul": lambda: (s0, kernels.trimul(z0, pmask, tri.tri_mul_out, "outgoing", residual=z0)),
         "triattn": lambda: (s0, kernels.triattn(z0, pmask, tri.tri_att_start, starting=True, residual=z0)),
         "transition": lambda: (s0, kernels.transition(z0, layer.transition_z, residual=z0)),
@@ -407,7 +484,9 @@ def main() -> int:
     per_launch = {
         "trimul_contract": fl["contraction"],
         "triattn_flash": fl["attn_core"],
+        "transition": flops_block(n)["transition_z"],
     }
+    hbm = hbm_bytes_per_launch(n, sdt)
     kern = {}
     for name, (tot_ms, cnt) in stats.items():
         if cnt == 0:
@@ -417,6 +496,9 @@ def main() -> int:
         if name in per_launch:
             tf = per_launch[name] / (avg * 1e-3) / 1e12
             entry.update(tflops=round(tf, 1), mfma_frac=round(tf / PEAK_BF16_TFLOPS, 4))
+        if name in hbm:
+            gbs = hbm[name] / (avg * 1e-3) / 1e9
+            entry.update(alg_bytes=hbm[name], hbm_gbs=round(gbs, 1), hbm_frac=round(gbs / PEAK_HBM_GBS, 4))
         kern[name] = entry
     dominant = max(kern, key=lambda k: kern[k]["avg_ms"] * kern[k]["launches"])
     t_contract = kern["trimul_contract"]["avg_ms"] * 2
@@ -425,8 +507,8 @@ def main() -> int:
     tri_kernels = ("trimul_prologue", "trimul_contract", "trimul_epilogue", "triattn_prologue", "triattn_flash",
                    "triattn_epilogue")
     sub_t = sum(kern[k]["avg_ms"] * kern[k]["launches"] for k in tri_kernels if k in kern) / a.steps
-    secondary = (2 * fl["trimul"] + 2 * fl["triattn"]) / (sub_t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
-    block_tflops = sum(flops_block(n).values()) / (ms_step * 1e-3) / 1e12
+    secondary = a.layers * (2 * fl["trimul"] + 2 * fl["triattn"]) / (sub_t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS
+    block_tflops = a.layers * sum(flops_block(n).values()) / (ms_step * 1e-3) / 1e12
     dom_flops = per_launch.get(dominant)
     traffic = measured_traffic(dominant, n)
     if dom_flops is not None:
@@ -444,7 +526,7 @@ def main() -> int:
 
     out = {
         "metric": METRIC,
-        "value": round(ms_step, 4),
+        "value": round(ms_step / a.layers, 4),  # ms per block (a step runs --layers blocks)
         "unit": "ms",
         "n_gpus": 1,
         "steps": a.steps,
@@ -460,7 +542,7 @@ def main() -> int:
             "workload": "one Pairformer block (Boltz-2 layer): tri-mul out+in, tri-attn start+end, pair transition "
                         "4x SwiGLU, single attention with pair bias, single transition; residuals fused",
             "n": n, "n_real": n_real, "c_z": 128, "c_hidden": 128, "c_s": 384, "tri_heads": 4, "tri_head_dim": 32,
-            "single_heads": 16, "pair_dtype": "bf16", "single_dtype": a.single_dtype,
+            "single_heads": 16, "pair_dtype": "bf16", "single_dtype": a.single_dtype, "layers": a.layers,
         },
         "block_tflops": round(block_tflops, 1),
         "roofline": roof,

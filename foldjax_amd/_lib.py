@@ -124,6 +124,8 @@ SYMBOLS = {
     "fjx_prof_num_kernels": (ctypes.c_int, []),
     "fjx_prof_kernel_name": (ctypes.c_char_p, [ctypes.c_int]),
     "fjx_prof_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
+    "fjx_probe_issue_mix": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float),
+                                           _vp]),
 }
 
 _lock = threading.Lock()
@@ -187,3 +189,11 @@ def prof_read() -> dict[str, tuple[float, int]]:
         check(lib.fjx_prof_read(i, ctypes.byref(ms), ctypes.byref(cnt)))
         out[lib.fjx_prof_kernel_name(i).decode()] = (ms.value, cnt.value)
     return out
+
+
+def probe_issue_mix(mix: int, waves_per_simd: int, iters: int, stream: int = 0) -> float:
+    """Kernel milliseconds of ``fjx_probe_issue_mix`` (the flash tile's
+    instruction mix alone; see the header)."""
+    ms = ctypes.c_float()
+    check(load().fjx_probe_issue_mix(mix, waves_per_simd, iters, ctypes.byref(ms), stream))
+    return ms.value

@@ -235,6 +235,8 @@ void launch_flash_single(const FlashParams<T>& p, int64_t batch, hipStream_t st)
 // the pipelined offset-free pass (fjx_flash_pipe.hip); false when the shape
 // or the parameters do not suit it (then nothing is launched)
 bool launch_flash_pipe(const FlashParams<bf16>& p, int64_t batch, hipStream_t st);
+// the flash tile's instruction mix alone (fjx_probe.hip): kernel ms, or -1 on a HIP error
+int probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream_t st);
 
 // general-width paths (fjx_generic.hip); positions v = r*n + s of the virtual
 // grid read the original grid at s*n + r when t = 1

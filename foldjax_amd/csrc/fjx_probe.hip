@@ -1,0 +1,149 @@
+// Issue-rate probe for the flash attention's per-tile instruction mix (a
+// measurement aid, no counterpart in the reference).
+//
+// Per 16-query x 64-key tile a wave of flash_pipe_kernel_bf16 issues 10
+// v_mfma_f32_16x16x32_bf16 (4 scores, 4 probability-value products, 2 row
+// sums), 16 v_exp_f32 and about 24 other VALU instructions (16 bias
+// widenings, 8 bf16 packs). This kernel issues exactly such a mix in a loop,
+// with independent operands (no memory, no LDS, no barriers), on every SIMD
+// of the GPU at a chosen number of waves per SIMD, so its time per iteration
+// is the rate at which one SIMD can issue one tile's instructions: the floor
+// the flash kernel's tile loop is measured against.
+//
+// Mixes: 0 = the kernel's (10 MFMA + 16 exp + 24 VALU), 1 = without the bias
+// widenings (10 MFMA + 16 exp + 8 VALU), 2 = the 10 MFMAs alone, 3 = the 16
+// exponentials alone, 4 = the 24 VALU alone.
+#include <hip/hip_runtime.h>
+
+#include "fjx_common.hpp"
+#include "fjx_kernels.hpp"
+
+namespace fjx {
+namespace {
+
+#define FJX_M(i) "v_mfma_f32_16x16x32_bf16 %" #i ", %34, %35, %" #i "\n"
+#define FJX_E(j) "v_exp_f32 %" #j ", %36\n"
+#define FJX_V(j) "v_fma_f32 %" #j ", %" #j ", 0.5, 1.0\n"
+// operands: %0..%9 accumulators (f32x4), %10..%25 exponential results,
+// %26..%33 VALU chains, %34 / %35 the MFMA's A and B fragments, %36 the
+// exponentials' argument (a fixed normal value: the scores the kernel
+// exponentiates are normal numbers, never infinities)
+#define FJX_OPS                                                                                           \
+  "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]), "+v"(c[6]), "+v"(c[7]),         \
+      "+v"(c[8]), "+v"(c[9]), "+v"(e[0]), "+v"(e[1]), "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]),     \
+      "+v"(e[6]), "+v"(e[7]), "+v"(e[8]), "+v"(e[9]), "+v"(e[10]), "+v"(e[11]), "+v"(e[12]), "+v"(e[13]), \
+      "+v"(e[14]), "+v"(e[15]), "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]),   \
+      "+v"(x[6]), "+v"(x[7])                                                                              \
+  : "v"(fa), "v"(fb), "v"(xe)
+
+template <int MIX>
+__global__ __launch_bounds__(256) void issue_mix_kernel(float* sink, int iters) {
+  f32x4 c[10];
+  float e[16], x[8];
+  bf16x8 fa, fb;
+  const float t = 1e-3f * (float)threadIdx.x;
+  const float xe = -0.75f - t;
+#pragma unroll
+  for (int i = 0; i < 10; ++i) c[i] = f32x4{t, t, t, t};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) e[j] = -0.01f * (float)j;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = t + (float)j;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    fa[k] = static_cast<bf16>(0.001f * (float)k);
+    fb[k] = static_cast<bf16>(t);
+  }
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (MIX == 0) {
+      // 10 MFMA, each followed by its share of 16 exp and 24 VALU (8 VALU
+      // chains, each used three times)
+      asm volatile(FJX_M(0) FJX_E(10) FJX_E(11) FJX_V(26) FJX_V(27) FJX_V(28)
+                   FJX_M(1) FJX_E(12) FJX_E(13) FJX_V(29) FJX_V(30) FJX_V(31)
+                   FJX_M(2) FJX_E(14) FJX_E(15) FJX_V(32) FJX_V(33)
+                   FJX_M(3) FJX_E(16) FJX_E(17) FJX_V(26) FJX_V(27) FJX_V(28)
+                   FJX_M(4) FJX_E(18) FJX_E(19) FJX_V(29) FJX_V(30)
+                   FJX_M(5) FJX_E(20) FJX_E(21) FJX_V(31) FJX_V(32) FJX_V(33)
+                   FJX_M(6) FJX_E(22) FJX_E(23) FJX_V(26) FJX_V(27)
+                   FJX_M(7) FJX_E(24) FJX_E(25) FJX_V(28) FJX_V(29) FJX_V(30)
+                   FJX_M(8) FJX_V(31) FJX_V(32)
+                   FJX_M(9) FJX_V(33)
+                   : FJX_OPS);
+    } else if constexpr (MIX == 1) {
+      asm volatile(FJX_M(0) FJX_E(10) FJX_E(11) FJX_V(26)
+                   FJX_M(1) FJX_E(12) FJX_E(13) FJX_V(27)
+                   FJX_M(2) FJX_E(14) FJX_E(15) FJX_V(28)
+                   FJX_M(3) FJX_E(16) FJX_E(17) FJX_V(29)
+                   FJX_M(4) FJX_E(18) FJX_E(19) FJX_V(30)
+                   FJX_M(5) FJX_E(20) FJX_E(21) FJX_V(31)
+                   FJX_M(6) FJX_E(22) FJX_E(23) FJX_V(32)
+                   FJX_M(7) FJX_E(24) FJX_E(25) FJX_V(33)
+                   FJX_M(8) FJX_M(9)
+                   : FJX_OPS);
+    } else if constexpr (MIX == 2) {
+      asm volatile(FJX_M(0) FJX_M(1) FJX_M(2) FJX_M(3) FJX_M(4) FJX_M(5) FJX_M(6) FJX_M(7) FJX_M(8) FJX_M(9)
+                   : FJX_OPS);
+    } else if constexpr (MIX == 3) {
+      asm volatile(FJX_E(10) FJX_E(11) FJX_E(12) FJX_E(13) FJX_E(14) FJX_E(15) FJX_E(16) FJX_E(17)
+                   FJX_E(18) FJX_E(19) FJX_E(20) FJX_E(21) FJX_E(22) FJX_E(23) FJX_E(24) FJX_E(25)
+                   : FJX_OPS);
+    } else {
+      asm volatile(FJX_V(26) FJX_V(27) FJX_V(28) FJX_V(29) FJX_V(30) FJX_V(31) FJX_V(32) FJX_V(33)
+                   FJX_V(26) FJX_V(27) FJX_V(28) FJX_V(29) FJX_V(30) FJX_V(31) FJX_V(32) FJX_V(33)
+                   FJX_V(26) FJX_V(27) FJX_V(28) FJX_V(29) FJX_V(30) FJX_V(31) FJX_V(32) FJX_V(33)
+                   : FJX_OPS);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 10; ++i) s += c[i][0] + c[i][3];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += e[j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += x[j];
+  sink[(int64_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+#undef FJX_M
+#undef FJX_E
+#undef FJX_V
+#undef FJX_OPS
+
+}  // namespace
+
+// waves_per_simd waves on each SIMD of the device's CUs (256-thread
+// workgroups: one wave per SIMD each), every wave `iters` iterations; the
+// kernel time in ms (HIP events on `st`, synchronised)
+int probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream_t st) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess)
+    return -1;
+  const int blocks = cus * waves_per_simd;
+  float* sink = nullptr;
+  if (hipMallocAsync(reinterpret_cast<void**>(&sink), (size_t)blocks * 256 * sizeof(float), st) != hipSuccess)
+    return -1;
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return -1;
+  if (hipEventCreate(&b) != hipSuccess) return -1;
+  auto launch = [&]() {
+    switch (mix) {
+      case 0: hipLaunchKernelGGL(issue_mix_kernel<0>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      case 1: hipLaunchKernelGGL(issue_mix_kernel<1>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      case 2: hipLaunchKernelGGL(issue_mix_kernel<2>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      case 3: hipLaunchKernelGGL(issue_mix_kernel<3>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      default: hipLaunchKernelGGL(issue_mix_kernel<4>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+    }
+  };
+  launch();  // warm-up: the clock settles under load
+  (void)hipEventRecord(a, st);
+  launch();
+  (void)hipEventRecord(b, st);
+  int rc = hipEventSynchronize(b) == hipSuccess && hipEventElapsedTime(ms, a, b) == hipSuccess ? 0 : -1;
+  (void)hipFreeAsync(sink, st);
+  (void)hipStreamSynchronize(st);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return rc;
+}
+
+}  // namespace fjx

@@ -360,6 +360,19 @@ int fjx_prof_num_kernels(void);
 const char* fjx_prof_kernel_name(int id);
 int fjx_prof_read(int id, double* total_ms, int64_t* launches);
 
+/*
+ * Measurement aid, no counterpart in the reference: the issue rate of the
+ * flash attention's per-tile instruction mix on its own. Runs a kernel that
+ * issues the mix (0: 10 v_mfma_f32_16x16x32_bf16 + 16 v_exp_f32 + 24 other
+ * VALU, the pipelined flash pass's instructions per 16 x 64 tile and wave;
+ * 1: the same without the 16 bias widenings; 2: the MFMAs alone; 3: the
+ * exponentials alone; 4: the 24 VALU alone) `iters` times in every wave,
+ * waves_per_simd (1-4) waves on each SIMD of the device, no memory traffic,
+ * and returns its time in *ms (HIP events on `stream`; the call waits for
+ * them). One SIMD issues one tile's mix in ms / (iters * waves_per_simd).
+ */
+int fjx_probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
