@@ -15,7 +15,13 @@ namespace tile {
 
 constexpr int kTP = 128;     // positions per tile
 constexpr int kC = 128;      // channels
-constexpr int kLd = kC + 8;  // padded LDS row (elements)
+// Padded LDS row (elements): 288-byte rows. An MFMA fragment read (16 rows,
+// four 16-byte chunks a row, one ds_read_b128 per lane) runs at the
+// conflict-free rate on them, where 272-byte rows take twice the LDS cycles
+// (timed on gfx950 for every stride from 256 to 384 bytes: 288 and 352 are
+// the conflict-free ones). The 16 padding elements of a row are free space
+// (the fp32 pair-bias transition keeps its split weight there).
+constexpr int kLd = kC + 16;
 
 // fp32 copy of a LayerNorm affine (gamma, beta) in LDS, staged once per
 // workgroup so the per-element normalisation does no bf16 unpacking

@@ -70,6 +70,16 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P,
   }
 }
 
+// The fp32 pair-bias weight split into bf16 high and low parts (16 heads x
+// 128) lives in the padding columns of the two tiles, which no tile access
+// touches: the high part in xs, the low part in hs, element (h, k) at row
+// 8h + k/16, column 128 + k%16. Without it in a buffer of its own the
+// kernel's LDS stays within two workgroups per CU.
+static_assert(tile::kLd - tile::kC == 16 && 16 * tile::kC == 16 * tile::kTP, "the split weight fills the padding");
+__device__ __forceinline__ bf16* wz_at(bf16 (*tl)[tile::kLd], int h, int k) {
+  return &tl[8 * h + (k >> 4)][tile::kC + (k & 15)];
+}
+
 // The same projection in fp32 for a bf16 transition (the attention runs in
 // fp32 over the bf16 pair tensor): the LayerNormed rows and the fp32 weight
 // are split into bf16 high and low parts, hi = bf16(v), lo = bf16(v - hi),
@@ -77,8 +87,8 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P,
 // dropped lo.lo term is below 2^-16 of the product). The high parts go to
 // xs, the low parts to hs (free after the last chunk).
 __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf16>& P, bf16 (*xs)[tile::kLd],
-                                                       bf16 (*hs)[tile::kLd], const tile::LnAffine& ln,
-                                                       const bf16 (*wz)[16][tile::kC], int64_t m0, int nvalid) {
+                                                       bf16 (*hs)[tile::kLd], const tile::LnAffine& ln, int64_t m0,
+                                                       int nvalid) {
   using namespace tile;
   const int t = threadIdx.x;
   const int wave = t >> 6;
@@ -91,8 +101,8 @@ __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf
   WCol<bf16> whi, wlo;
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    whi[ks] = load8(&wz[0][li][32 * ks + 8 * lg]);
-    wlo[ks] = load8(&wz[1][li][32 * ks + 8 * lg]);
+    whi[ks] = load8(wz_at(xs, li, 32 * ks + 8 * lg));
+    wlo[ks] = load8(wz_at(hs, li, 32 * ks + 8 * lg));
   }
   __syncthreads();
   {
@@ -143,9 +153,11 @@ __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf
 
 // The fp32 pair-bias weight [heads][128], split once per workgroup into
 // bf16 high and low parts (hi = bf16(w), lo = bf16(w - hi)) in LDS, rows past
-// pb_heads zero: the epilogue then reads its fragments from LDS instead of
-// waiting, at the end of the tile, for global loads and the split
-__device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, bf16 (*wz)[16][tile::kC]) {
+// pb_heads zero (wz_at: the padding columns of xs and hs): the epilogue then
+// reads its fragments from LDS instead of waiting, at the end of the tile,
+// for global loads and the split
+__device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, bf16 (*xs)[tile::kLd],
+                                               bf16 (*hs)[tile::kLd]) {
   using namespace tile;
   const int t = threadIdx.x;  // 512 threads x 4 weights = 16 x 128
   const int h = t >> 5;
@@ -162,8 +174,8 @@ __device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, 
 #pragma unroll
     for (int e = 0; e < 4; ++e) hi[e] = lo[e] = 0.f;
   }
-  store4f(&wz[0][h][k0], hi);
-  store4f(&wz[1][h][k0], lo);
+  store4f(wz_at(xs, h, k0), hi);
+  store4f(wz_at(hs, h, k0), lo);
 }
 
 // ---------------------------------------------------------------------------
@@ -188,8 +200,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   __shared__ __attribute__((aligned(16))) T hs[kTP][kLd];  // silu(a) * b, one hidden chunk
   __shared__ __attribute__((aligned(16))) LnAffine ln;
   __shared__ __attribute__((aligned(16))) LnAffine pb_ln;  // the pair-bias epilogue's norm
-  // the fp32 pair-bias weight split into bf16 hi / lo (the fp32-bias form only)
-  __shared__ __attribute__((aligned(16))) bf16 wz[kPbF32 ? 2 : 1][16][kPbF32 ? kC : 8];
+  // (the fp32-bias form's split weight: the padding columns of xs and hs, wz_at)
 
   const int64_t m0 = (int64_t)blockIdx.x * kTP;
   const int nvalid = (int)min<int64_t>(kTP, P.rows - m0);
@@ -213,7 +224,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
     if (!kNarrow && P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
     if constexpr (kPbF32) {
       stage_ln<float>(P.pbf_ln_w, P.pbf_ln_b, pb_ln);
-      stage_wz_split(P, wz);
+      stage_wz_split(P, xs, hs);
     }
     __syncthreads();
     ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
@@ -317,7 +328,7 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
     }
   }
   if constexpr (kPbF32) {
-    pair_bias_epilogue_f32(P, xs, hs, pb_ln, wz, m0, nvalid);
+    pair_bias_epilogue_f32(P, xs, hs, pb_ln, m0, nvalid);
   } else if constexpr (!kNarrow) {
     if (P.pb_out) pair_bias_epilogue<T>(P, xs, pb_ln, pb_wf, m0, nvalid);
   }
