@@ -67,13 +67,20 @@ def device_normal(shape, seed: int) -> torch.Tensor:
 
 def positions(n: int, n_real: int, seed: int, extra: int = 8) -> list[tuple[int, int]]:
     """Pairs over the contraction tile edges (multiples of 256 and their
-    neighbours), the first padded token, the last token, plus random pairs."""
+    neighbours), the first padded token, the last token, random pairs, and
+    one pair inside every 256 x 256 contraction tile: a random row of each
+    tile row crossed with a random column of each tile column, so the
+    (n/256)^2 tiles are each reached while the oracle evaluates only 2n/256
+    lines."""
     edges = sorted({v for v in (0, 1, 255, 256, 511, 512, n // 2 + 3, n_real - 1, n_real, n - 1) if 0 <= v < n})
     rng = np.random.default_rng(seed)
     pick = rng.choice(len(edges), size=(16, 2))
     pairs = {(edges[a], edges[b]) for a, b in pick}
     pairs |= {(0, n - 1), (n - 1, 0), (n_real - 1, n_real - 1)}
     pairs |= {tuple(int(v) for v in rng.integers(0, n, size=2)) for _ in range(extra)}
+    tile_rows = [min(t0 + int(rng.integers(0, 256)), n - 1) for t0 in range(0, n, 256)]
+    tile_cols = [min(t0 + int(rng.integers(0, 256)), n - 1) for t0 in range(0, n, 256)]
+    pairs |= {(i, j) for i in tile_rows for j in tile_cols}
     return sorted(pairs)
 
 
@@ -115,17 +122,22 @@ def check_triattn(z, mask_np, w, wq, starting, pos, what):
     return out
 
 
-def run_layer_checked(n: int, n_real: int, seed: int, tag: str):
-    """One Boltz-2 Pairformer layer at size n on the product kernels,
-    sublayer by sublayer, each checked at sampled positions."""
+def run_layer_checked(n: int, n_real: int, seed: int, tag: str, z: torch.Tensor | None = None,
+                      s: torch.Tensor | None = None):
+    """One Boltz-2 Pairformer layer at size n on the product kernels (the
+    weights of ``syn.pairformer_layer_weights(seed)``), sublayer by sublayer,
+    each checked at sampled positions; from the given ``[n, n, 128]`` z and
+    ``[n, 384]`` s, or from seeded random ones. Returns the layer's s and z."""
     w = syn.pairformer_layer_weights(seed=seed)
     wq = prep_tree(w, BF16)
     layer = PairformerLayerWeights.from_fields(w, BF16, "cuda")
     tri = layer.triangle
     pm = syn.pair_mask(n, n_real)
     tm = syn.token_mask(n, n_real)
-    z = device_normal((n, n, 128), seed=seed + 100)
-    s = torch.from_numpy(syn.single_input(n, 384, seed=1)).to("cuda", BF16)
+    if z is None:
+        z = device_normal((n, n, 128), seed=seed + 100)
+    if s is None:
+        s = torch.from_numpy(syn.single_input(n, 384, seed=1)).to("cuda", BF16)
     pos = positions(n, n_real, seed)
     say(f"{tag}: n={n} n_real={n_real} tri-mul outgoing")
     z = check_trimul(z, pm, tri.tri_mul_out, wq["tri_mul_out"], "outgoing", pos, f"{tag} tri-mul out")
@@ -320,9 +332,12 @@ def test_trimul_persistent_batch_n768():
 
 def test_config4_trunk_48_layers_n2048():
     """the 48-layer trunk at N=2048 (all-ones mask, each
-    layer with its own weights). Layer-level parity is
-    ``test_config4_layer_n2048``; here the whole stack must stay finite and
-    its pair activations keep a bounded, non-degenerate scale."""
+    layer with its own weights). The whole stack must stay finite and its
+    pair activations keep a bounded, non-degenerate scale; the last layer,
+    fed the state 47 layers deep, is checked against the oracle sublayer by
+    sublayer at sampled positions (every contraction tile among them), and
+    the trunk's own forward of that layer must equal the checked run bit for
+    bit."""
     n, layers = 2048, 48
     say(f"config4 trunk {layers} layers n={n}")
     z = device_normal((1, n, n, 128), seed=300)
@@ -332,7 +347,14 @@ def test_config4_trunk_48_layers_n2048():
     rms = []
     for l in range(layers):
         layer = PairformerLayerWeights.random(BF16, "cuda", seed=1000 + 7 * l)
-        s, z = layer.forward(s, z, tm, pm)
+        if l == layers - 1:
+            say(f"  layer {l}: checked against the oracle")
+            s_chk, z_chk = run_layer_checked(n, n, seed=1000 + 7 * l, tag=f"config4 trunk layer {l}", z=z[0], s=s[0])
+            s, z = layer.forward(s, z, tm, pm)
+            torch.cuda.synchronize()
+            assert torch.equal(z[0], z_chk) and torch.equal(s[0], s_chk), "trunk layer differs from the checked run"
+        else:
+            s, z = layer.forward(s, z, tm, pm)
         if l % 8 == 7 or l == layers - 1:
             zf = z.float()
             assert bool(torch.isfinite(zf).all()), f"layer {l}: non-finite z"
