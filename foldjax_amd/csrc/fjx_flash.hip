@@ -39,6 +39,7 @@
 
 #include "fjx_common.hpp"
 #include "fjx_kernels.hpp"
+#include "fjx_tile.hpp"
 
 namespace fjx {
 
@@ -91,8 +92,10 @@ template <> __device__ __forceinline__ f32x8 ones8<float>(bool on) {
 // accumulator whose A operand is 1 only in rows 4(qt%4) .. +3, so lane group
 // g holds the sums of tile 4(qt/4) + g -- padded queries have zero scores,
 // so the zero-weighted rows add nothing)
+// vb: the workgroup's index in the launch grid of `total` workgroups (its
+// fallback flag and, through xcd_remap_f, its tile)
 template <typename T, int ROWS, int NQT, bool FAST = false>
-__device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
+__device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P, int64_t vb, int64_t total) {
   typedef typename Frag<T>::type FragT;
   constexpr int QTL = 16 * NQT;
   constexpr bool kQLds = NQT == 4;
@@ -103,7 +106,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
 
   // the offset path after a FAST launch: only the workgroups it flagged
   if constexpr (!FAST) {
-    if (P.fallback && P.fallback[blockIdx.x] == 0u) return;
+    if (P.fallback && P.fallback[vb] == 0u) return;
   }
 
   const int64_t n = P.n;
@@ -111,8 +114,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
   const int64_t H = P.heads;
   const int64_t QT = np / QTL;
   const int64_t RG = (P.rows + ROWS - 1) / ROWS;
-  const int64_t total = (int64_t)gridDim.x;
-  int64_t lid = xcd_remap_f(blockIdx.x, total);
+  int64_t lid = xcd_remap_f(vb, total);
   const int64_t qtile = lid % QT;
   lid /= QT;
   const int64_t rg = lid % RG;
@@ -350,7 +352,7 @@ __device__ __forceinline__ void flash_tri_body(const FlashParams<T>& P) {
         for (int r = 0; r < 4; ++r) bad |= (__float_as_uint(o[dt][qt][r]) & 0x7F800000u) == 0x7F800000u;
     }
     if (__builtin_amdgcn_ballot_w64(bad) != 0) {
-      if (lane == 0) P.fallback[blockIdx.x] = 1u;
+      if (lane == 0) P.fallback[vb] = 1u;
       return;
     }
   }
@@ -381,7 +383,30 @@ constexpr int kRows = 4;
 // than 64 queries at 3 waves per SIMD, as each K and V load serves twice the
 // queries
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_tri8_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows, 8>(P);
+  flash_tri_body<bf16, kRows, 8>(P, blockIdx.x, gridDim.x);
+}
+
+// The same kernel as the fallback of the pipelined pass, over that pass's
+// grid of `total` workgroups: workgroup w reads the flags of `per`
+// consecutive ones (64 a load) and recomputes the flagged ones. Launched with
+// no more workgroups than the GPU holds at once, it costs few short
+// workgroups when nothing is flagged and, when everything is, as many rounds
+// of resident workgroups as the full grid would.
+__global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void flash_tri8_redo_kernel_bf16(FlashParams<bf16> P, int64_t total, int64_t per) {
+  const int64_t base = (int64_t)blockIdx.x * per;
+  const int lane = threadIdx.x & 63;
+  for (int64_t c0 = 0; c0 < per; c0 += 64) {
+    const int64_t vb = base + c0 + lane;
+    const bool f = c0 + lane < per && vb < total && P.fallback[vb] != 0u;
+    uint64_t m = __builtin_amdgcn_ballot_w64(f);  // the same in every wave
+    while (m != 0) {
+      const int k = __builtin_ctzll(m);
+      m &= m - 1;
+      flash_tri_body<bf16, kRows, 8>(P, base + c0 + k, total);
+      __syncthreads();  // LDS is reused by the next flagged workgroup
+    }
+  }
 }
 
 // The same 128-query kernel without a softmax offset: p = exp2(s) straight
@@ -393,7 +418,7 @@ __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2
 // below 2^-100 or a non-finite value after its last block, and its workgroup
 // is then recomputed by the offset kernel above.
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(2, 2))) void flash_tri8_fast_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows, 8, true>(P);
+  flash_tri_body<bf16, kRows, 8, true>(P, blockIdx.x, gridDim.x);
 }
 
 __global__ void zero_flags_kernel(unsigned* __restrict__ f, int64_t count) {
@@ -405,15 +430,15 @@ __global__ void zero_flags_kernel(unsigned* __restrict__ f, int64_t count) {
 // the fp32 variant would spill heavily under that cap and keeps 2.
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void flash_tri_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows, 4>(P);
+  flash_tri_body<bf16, kRows, 4>(P, blockIdx.x, gridDim.x);
 }
 // its offset-free pass (as flash_tri8_fast_kernel_bf16)
 __global__ __launch_bounds__(64 * kRows) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void flash_tri_fast_kernel_bf16(FlashParams<bf16> P) {
-  flash_tri_body<bf16, kRows, 4, true>(P);
+  flash_tri_body<bf16, kRows, 4, true>(P, blockIdx.x, gridDim.x);
 }
 __global__ __launch_bounds__(64 * kRows) void flash_tri_kernel_f32(FlashParams<float> P) {
-  flash_tri_body<float, kRows, 4>(P);
+  flash_tri_body<float, kRows, 4>(P, blockIdx.x, gridDim.x);
 }
 
 template <typename T>
@@ -435,14 +460,22 @@ void launch_flash(const FlashParams<T>& p_in, int64_t batch, hipStream_t st) {
     const bool q128 = p.np % 128 == 0;
     const dim3 g = q128 ? dim3((unsigned)(batch * p.heads * rg * (p.np / 128))) : grid;
     if (p.fallback) {
+      // the pipelined pass writes every flag in the 128-query grid of the
+      // offset kernel; the offset kernel then redoes the flagged workgroups
+      if (q128 && launch_flash_pipe(p, batch, st)) {
+        const int64_t total = g.x;
+        const int64_t cap = tile::resident_blocks(reinterpret_cast<const void*>(&flash_tri8_redo_kernel_bf16), 64 * kRows);
+        const int64_t per = (total + cap - 1) / cap;
+        hipLaunchKernelGGL(flash_tri8_redo_kernel_bf16, dim3((unsigned)((total + per - 1) / per)), dim3(64 * kRows), 0,
+                           st, p, total, per);
+        return;
+      }
       // offset-free pass, then the offset kernel for the workgroups it flagged
       const int64_t nb = ((int64_t)g.x + 255) / 256;
       hipLaunchKernelGGL(zero_flags_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, p.fallback,
                          (int64_t)g.x);
-      // the pipelined pass flags in the 128-query grid of the offset kernel
-      if (!(q128 && launch_flash_pipe(p, batch, st)))
-        hipLaunchKernelGGL(q128 ? flash_tri8_fast_kernel_bf16 : flash_tri_fast_kernel_bf16, g, dim3(64 * kRows), 0,
-                           st, p);
+      hipLaunchKernelGGL(q128 ? flash_tri8_fast_kernel_bf16 : flash_tri_fast_kernel_bf16, g, dim3(64 * kRows), 0, st,
+                         p);
     }
     hipLaunchKernelGGL(q128 ? flash_tri8_kernel_bf16 : flash_tri_kernel_bf16, g, dim3(64 * kRows), 0, st, p);
   } else

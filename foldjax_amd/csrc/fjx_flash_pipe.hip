@@ -45,6 +45,7 @@ constexpr int kPHalves = 1; // query groups per row (waves per row)
 constexpr int kPNqt = 8;    // query tiles of 16 per wave
 constexpr int kPQwg = 16 * kPNqt * kPHalves;  // queries per workgroup: 128, the fallback kernel's tile
 constexpr int kPWaves = kPRows * kPHalves;
+static_assert(kPWaves <= 4, "one byte of a workgroup's 32-bit fallback flag per wave");
 constexpr int kPXcd = 8;
 
 // blockIdx -> logical workgroup id, all tiles of a row group on one XCD (as
@@ -375,9 +376,10 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   // the clamped prefetches may still be writing LDS: drain before leaving
   __builtin_amdgcn_s_waitcnt(0);
 
-  if (!row_ok) return;
   // every softmax sum in [2^-100, inf) and every output finite, checked on
-  // the bit patterns; otherwise the fallback kernel recomputes the workgroup
+  // the bit patterns; otherwise the fallback kernel recomputes the workgroup.
+  // Each wave writes its own byte of the workgroup's flag word, 1 or 0 (0 for
+  // rows past the end), so the flags need no clearing before this pass.
   bool bad = unusual;
 #pragma unroll
   for (int qt = 0; qt < NQT; ++qt) {
@@ -389,10 +391,9 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) bad |= (__float_as_uint(o[qt][dt][r]) & 0x7F800000u) == 0x7F800000u;
   }
-  if (__builtin_amdgcn_ballot_w64(bad) != 0) {
-    if (lane == 0) P.fallback[blockIdx.x] = 1u;
-    return;
-  }
+  const bool redo = row_ok && __builtin_amdgcn_ballot_w64(bad) != 0;
+  if (lane == 0) reinterpret_cast<unsigned char*>(P.fallback + blockIdx.x)[wave] = redo ? 1 : 0;
+  if (!row_ok || redo) return;
   // Output: lane (li, g) holds dims 4g .. 4g+3 and 16 + 4g .. +3 of query
   // li. Two lane swaps (lanes 32 apart, then 16 apart; the query stays) give
   // it dims 8g .. 8g+7 instead, so each query's 64 bytes leave as four
@@ -429,8 +430,9 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
 
 bool launch_flash_pipe(const FlashParams<bf16>& p, int64_t batch, hipStream_t st) {
   // needs the fallback flags (the offset kernel recomputes what this pass
-  // flags) and a padded length that is a multiple of 128; launches the grid
-  // of the fallback kernel
+  // flags; every flag is written, none needs clearing first) and a padded
+  // length that is a multiple of 128; launches the grid of the fallback
+  // kernel
   if (!p.fallback || p.rows < 2 || p.np % kPQwg != 0) return false;
   const int64_t rg = (p.rows + kPRows - 1) / kPRows;
   const dim3 grid((unsigned)(batch * p.heads * rg * (p.np / kPQwg)));
