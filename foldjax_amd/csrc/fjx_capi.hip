@@ -741,6 +741,19 @@ int triattn_generic_run(const fjx_triattn_args* a, hipStream_t st) {
   });
 }
 
+// K splits of the fp32 output projection of the general transition: its
+// [rows, c] output is a grid of few 64 x 64 tiles (the 384-wide single track:
+// 96 at 1024 rows) whose k loop runs the whole hidden width; split, the
+// partial products go to the workspace and the scatter pass sums them. bf16
+// keeps one product (its projection rounds the whole sum once).
+int transition_out_splits(int64_t rows, int64_t c, int64_t hidden, int32_t dtype) {
+  if (dtype != FJX_DTYPE_F32) return 1;
+  const int64_t tiles = ((rows + 63) / 64) * ((c + 63) / 64);
+  int s = 1;
+  while (s < 8 && tiles * s < 256 && hidden % (16 * s) == 0 && hidden / (2 * s) >= 128) s *= 2;
+  return s;
+}
+
 struct GenTransitionWs {
   size_t xn, h, wcat, y, total;
 };
@@ -756,7 +769,8 @@ GenTransitionWs gen_transition_ws(int64_t rows, int64_t c, int64_t hidden, int32
   w.xn = take((size_t)rows * c * es);
   w.h = take((size_t)rows * hidden * es);
   w.wcat = take((size_t)2 * hidden * c * es);  // W_a and W_b interleaved by 128 rows (the fused SwiGLU GEMM)
-  w.y = take((size_t)rows * c * es);           // the output projection, when its GEMM cannot apply the epilogue
+  // the output projection (each of its K splits), when its GEMM cannot apply the epilogue
+  w.y = take((size_t)transition_out_splits(rows, c, hidden, dtype) * rows * c * es);
   w.total = off;
   return w;
 }
@@ -810,9 +824,17 @@ int transition_generic_run(const fjx_transition_args* a, hipStream_t st) {
       launch_gemm<T, T>(g, st);
     } else {
       T* y = at<T>(W, ws.y);
-      launch_gemm<T, T>(rows_gemm<T>(h, rows, hid, a->w_o, c, y, c), st);
+      const int splits = transition_out_splits(rows, c, hid, a->dtype);
+      // split s: hidden columns s kc .. (s + 1) kc - 1 into y + s rows c
+      GemmParams<T, T> gy = rows_gemm<T>(h, rows, hid / splits, a->w_o, c, y, c);
+      gy.lda = gy.ldb = hid;
+      gy.batches = splits;
+      gy.sa = gy.sb = hid / splits;
+      gy.sc = rows * c;
+      launch_gemm<T, T>(gy, st);
       launch_scatter_add<T>(y, static_cast<const T*>(a->row_mask), static_cast<const T*>(a->residual),
-                            static_cast<const T*>(a->out_mask), static_cast<T*>(a->out), rows, 1, (int)c, 0, st);
+                            static_cast<const T*>(a->out_mask), static_cast<T*>(a->out), rows, 1, (int)c, 0, st,
+                            splits, rows * c);
     }
   });
 }

@@ -373,11 +373,12 @@ __global__ __launch_bounds__(256) void to_position_major8_kernel(const T* __rest
 }
 
 // out[b][orig(v)][c] = (T(y[b][v][c] * m) + residual[b][orig(v)][c]) * (g != 0),
-// with m the row mask and g the output mask at the output position (1 without)
+// with m the row mask and g the output mask at the output position (1 without);
+// y the sum of `splits` partial products ss elements apart
 template <typename T>
 __global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
                                    const T* __restrict__ residual, const T* __restrict__ out_mask,
-                                   T* __restrict__ out, int64_t rows, int64_t n, int c, int t) {
+                                   T* __restrict__ out, int64_t rows, int64_t n, int c, int t, int splits, int64_t ss) {
   const int64_t total = rows * c;
   const int64_t nn = n * n;
   for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total;
@@ -387,6 +388,7 @@ __global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict_
     const int64_t bb = row / nn;
     const int64_t o = bb * nn + orig_pos(row - bb * nn, n, t);
     float v = to_f32(y[idx]);
+    for (int s = 1; s < splits; ++s) v += to_f32(y[s * ss + idx]);
     if (row_mask) v *= to_f32(row_mask[o]);
     v = round_to<T>(v);
     if (residual) v += to_f32(residual[o * c + ch]);
@@ -399,7 +401,8 @@ __global__ void scatter_add_kernel(const T* __restrict__ y, const T* __restrict_
 template <typename T>
 __global__ void scatter_add8_kernel(const T* __restrict__ y, const T* __restrict__ row_mask,
                                     const T* __restrict__ residual, const T* __restrict__ out_mask,
-                                    T* __restrict__ out, int64_t rows, int64_t n, int c, int t) {
+                                    T* __restrict__ out, int64_t rows, int64_t n, int c, int t, int splits,
+                                    int64_t ss) {
   const int c8 = c / 8;
   const int64_t total = rows * c8;
   const int64_t nn = n * n;
@@ -411,6 +414,12 @@ __global__ void scatter_add8_kernel(const T* __restrict__ y, const T* __restrict
     const int64_t o = bb * nn + orig_pos(row - bb * nn, n, t);
     float v[8];
     to_f32x8(load8(y + row * c + ch), v);
+    for (int s = 1; s < splits; ++s) {
+      float w[8];
+      to_f32x8(load8(y + s * ss + row * c + ch), w);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += w[e];
+    }
     const float m = row_mask ? to_f32(row_mask[o]) : 1.f;
     const float g = out_mask && to_f32(out_mask[o]) == 0.f ? 0.f : 1.f;
     float r[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -494,13 +503,13 @@ void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, i
 }
 template <typename T>
 void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
-                        int64_t n, int c, int t, hipStream_t st) {
-  if (c % 8 == 0 && al16(y) && al16(out) && (!residual || al16(residual)))
+                        int64_t n, int c, int t, hipStream_t st, int splits, int64_t split_stride) {
+  if (c % 8 == 0 && split_stride % 8 == 0 && al16(y) && al16(out) && (!residual || al16(residual)))
     hipLaunchKernelGGL(scatter_add8_kernel<T>, stride_grid(rows * c / 8), dim3(256), 0, st, y, row_mask, residual,
-                       out_mask, out, rows, n, c, t);
+                       out_mask, out, rows, n, c, t, splits, split_stride);
   else
     hipLaunchKernelGGL(scatter_add_kernel<T>, stride_grid(rows * c), dim3(256), 0, st, y, row_mask, residual, out_mask,
-                       out, rows, n, c, t);
+                       out, rows, n, c, t, splits, split_stride);
 }
 
 #define FJX_INST(T)                                                                                                \
@@ -515,7 +524,7 @@ void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const 
   template void launch_grid_mask_bias<T>(const T*, float*, int64_t, int64_t, int64_t, float, int, hipStream_t);     \
   template void launch_gate_rows<T>(T*, const T*, int64_t, int64_t, int64_t, int, hipStream_t);                      \
   template void launch_scatter_add<T>(const T*, const T*, const T*, const T*, T*, int64_t, int64_t, int, int,     \
-                                      hipStream_t);
+                                      hipStream_t, int, int64_t);
 FJX_INST(float)
 FJX_INST(bf16)
 #undef FJX_INST

@@ -263,9 +263,11 @@ void launch_grid_mask_bias(const T* mask, float* mb, int64_t batch, int64_t n, i
 template <typename T>
 void launch_gate_rows(T* o, const T* g, int64_t ldg, int64_t c0, int64_t rows, int width, hipStream_t st);
 // out[orig(v)] = (T(y[v] * row_mask) + residual[orig(v)]) * (out_mask != 0),
-// for a product the DMA GEMM does not take (its epilogue does this itself)
+// for a product the DMA GEMM does not take (its epilogue does this itself);
+// y may be `splits` partial products (split K), `split_stride` elements
+// apart, summed here
 template <typename T>
 void launch_scatter_add(const T* y, const T* row_mask, const T* residual, const T* out_mask, T* out, int64_t rows,
-                        int64_t n, int c, int t, hipStream_t st);
+                        int64_t n, int c, int t, hipStream_t st, int splits = 1, int64_t split_stride = 0);
 
 }  // namespace fjx
