@@ -313,8 +313,9 @@ __global__ __launch_bounds__(512) void triattn_prologue_kernel(TriAttnProloguePa
   }
 }
 
-// Epilogue tiles are 64 positions wide (256 threads, 52 KB of LDS in bf16),
-// so three workgroups share a CU and their phases interleave.
+// Epilogue tiles are 64 positions wide (256 threads, 38-57 KB of LDS in
+// bf16), so two workgroups share a CU (their 230-256 VGPRs allow no more)
+// and their phases interleave.
 constexpr int kTE = 64;
 
 // ---------------------------------------------------------------------------
