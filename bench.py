@@ -313,13 +313,14 @@ def other_configs(single_dtype) -> dict:
     headline (no per-kernel events): config 1 (tri-mul out+in, N=256, fp32,
     all-ones mask), config 2 (tri-attn start+end, N=384, bf16, 346 real
     tokens), config 4 (the 48-layer trunk at N=2048, all-ones mask, each
-    layer with its own weights) and config 5 (one unchunked layer at N=3072,
+    layer with its own weights, stacked) and config 5 (one unchunked layer at N=3072,
     3012 real tokens)."""
     import torch
 
-    from foldjax_amd import kernels
+    from foldjax_amd import boltz2, kernels
     from foldjax_amd import synthetic as syn
     from foldjax_amd.pairformer import PairformerLayerWeights, flops_block
+    from foldjax_amd.stacking import stacked_or_stack
 
     dev = torch.device("cuda:0")
     bf = torch.bfloat16
@@ -354,14 +355,14 @@ def other_configs(single_dtype) -> dict:
         s0 = t(syn.single_input(n, 384, seed=1, batch=1), single_dtype)
         tmask = t(syn.token_mask(n, n_real)[None], single_dtype)
         pmask = t(syn.pair_mask(n, n_real)[None], bf)
-        stack = [PairformerLayerWeights.random(bf, dev, seed=2 + i, single_dtype=single_dtype)
-                 for i in range(layers)]
+        # the layers stacked once and run through Boltz-2's module forward
+        # (donated s and z after the first layer), as a trunk's caller runs them
+        trunk = {"layers": stacked_or_stack([PairformerLayerWeights.random(bf, dev, seed=2 + i,
+                                                                           single_dtype=single_dtype)
+                                             for i in range(layers)])}
 
         def step():
-            s, z = s0, z0
-            for lay in stack:
-                s, z = lay.forward(s, z, tmask, pmask)
-            return s, z
+            return boltz2.pairformer_module_forward(trunk, s0, z0, tmask, pmask)
 
         ms = _timed(step, steps, 1, dev)
         s, z = step()
@@ -370,7 +371,7 @@ def other_configs(single_dtype) -> dict:
             raise RuntimeError(f"non-finite output in {key}")
         out[key] = round(ms, 3)
         out[key.replace("_ms", "_tflops")] = round(sum(flops_block(n).values()) * layers / (ms * 1e-3) / 1e12, 1)
-        del z0, s0, stack
+        del z0, s0, trunk, s, z
         torch.cuda.empty_cache()
     return out
 
@@ -413,14 +414,19 @@ def main() -> int:
 
     from foldjax_amd import kernels
 
+    # a trunk (--layers > 1) runs as users run it: the layers stacked once
+    # (one [L, ...] buffer per weight kind) through Boltz-2's module forward,
+    # whose first layer writes new s and z (the inputs stay as they are for
+    # the next step) and whose further layers update them in place
+    from foldjax_amd import boltz2
+    from foldjax_amd.stacking import stacked_or_stack
+
+    trunk = {"layers": stacked_or_stack([layer] + more)} if more else None
+
     def block_step():
-        # the first layer writes new s and z (the inputs stay as they are for
-        # the next step), every further one updates them in place, as the
-        # stacks do
-        s, z = layer.forward(s0, z0, tmask, pmask)
-        for lay in more:
-            s, z = lay.forward(s, z, tmask, pmask, donate=True)
-        return s, z
+        if trunk is None:
+            return layer.forward(s0, z0, tmask, pmask)
+        return boltz2.pairformer_module_forward(trunk, s0, z0, tmask, pmask)
 
     tri = layer.triangle
     if a.op in ("trimul", "triattn", "transition") and (a.c_z, a.c_h, a.heads) != (128, 128, 4):
