@@ -454,6 +454,15 @@ def main() -> int:
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize(dev)
+    if a.op != "block":
+        # a single-kernel op's few warm-up steps are a few ms of GPU work, too
+        # short for the GPU's clock to settle: the timed loop then carried a
+        # one-off ~40 ms ramp (0.64 -> 2.5 ms per step at 20 steps). The
+        # profiling ops keep stepping until 0.5 s of warm-up have passed.
+        t_w = time.perf_counter()
+        while time.perf_counter() - t_w < 0.5:
+            step()
+            torch.cuda.synchronize(dev)
 
     # the timed steps run without per-kernel events (their markers cost about
     # 0.1 ms per block); the same number of steps is then repeated with the
