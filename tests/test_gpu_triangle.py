@@ -130,6 +130,39 @@ def test_triattn_core_large_logits_bf16(mul):
     assert_parity(g[:, rows], want[:, rows], dtype, f"triattn_core mul={mul}")
 
 
+def test_triattn_core_some_workgroups_redone_bf16():
+    """Only some workgroups of the offset-free pass leave its safe range (q of
+    three rows scaled to scores of hundreds in log2 units): the fallback
+    kernel, launched with fewer workgroups than the pass (each reading the
+    flags of a run of its workgroups), must redo exactly those and leave the
+    others' outputs. 256 rows of N = 512: 1024 pass workgroups, more than the
+    GPU holds at once, so each fallback workgroup reads several flags. The
+    redone rows, rows sharing their workgroups and untouched rows against the
+    oracle."""
+    dtype = DTYPES["bf16"]
+    say("triattn_core partial fallback n=512 rows=256")
+    rng = np.random.default_rng(41)
+    b, i, h, n, d = 1, 256, 4, 512, 32
+    q, k, v = (rng.standard_normal((b, i, h, n, d)).astype(np.float32) for _ in range(3))
+    hot = [3, 130, 255]
+    q[:, hot] *= 40.0
+    tb = rng.standard_normal((b, 1, h, n, n)).astype(np.float32)
+    mask = (rng.random((b, i, n)) > 0.1).astype(np.float32)
+    mask[..., 0] = 1
+    mb = (1e9 * (mask - 1.0))[:, :, None, None, :].astype(np.float32)
+    scale = d ** -0.5
+    got = boltz2.hip_attention_core(device_tensor(q, dtype), device_tensor(k, dtype), device_tensor(v, dtype),
+                                    device_tensor(tb, dtype), torch.from_numpy(mb).cuda(), scale=scale)
+    torch.cuda.synchronize()
+    g = to_np(got)
+    assert np.all(np.isfinite(g))
+    rows = hot + [0, 2, 128, 131, 200, 252]  # redone, sharing a redone workgroup (rows 4r .. 4r+3), untouched
+    sel = np.array(rows)
+    want = O.attention_core(prep(q[:, sel], dtype), prep(k[:, sel], dtype), prep(v[:, sel], dtype), prep(tb, dtype),
+                            mb[:, sel].astype(np.float64), scale)
+    assert_parity(g[:, sel], want, dtype, "triattn_core partial fallback")
+
+
 def test_ports_agree_on_device():
     """Boltz-2, Protenix and OpenFold3 entry points run the same kernels on
     the same weights and agree to the last bit."""
