@@ -122,7 +122,11 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     T* dst = (half == 0 ? P.a_cm : P.b_cm) + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
     // row tiles in pairs with paired rows: lane group g holds positions
     // 32j + 8g .. +7 of its channel, one 16-byte store per channel row
-#pragma unroll 1
+    // two row-tile pairs per loop body give the scheduler the next pair's
+    // MFMAs to issue under this pair's sigmoids (the 2-block form keeps one:
+    // unrolled it needs more than the 128 VGPRs of two workgroups per CU)
+    constexpr int kJUnroll = NB == 4 ? 2 : 1;
+#pragma unroll kJUnroll
     for (int j = 0; j < kTP / 32; ++j) {
       f32x4 ap[2][2], ag[2][2];
 #pragma unroll
