@@ -596,7 +596,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     __syncthreads();
     if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
-#pragma unroll 2
+#pragma unroll
     for (int rt = 0; rt < (active ? kTE / 16 : 0); ++rt) {
       f32x4 acc[2];
       tile_mma<T, true>(xo, rt, wo, acc);
