@@ -5,9 +5,10 @@
 // permuted key order that lets the probabilities feed O^T = V^T P^T directly,
 // softmax sums on MFMA), for the offset-free pass only: p = exp2(s) straight
 // from the log2-unit score. A workgroup whose sums or outputs leave the safe
-// range is flagged for the offset kernel of fjx_flash.hip
-// (flash_tri8_kernel_bf16), which recomputes it; this kernel runs exactly that
-// kernel's grid (4 rows x 128 queries of one head per workgroup).
+// range is flagged for the offset kernel of fjx_flash.hip, which recomputes
+// it (flash_tri8_redo_kernel_bf16 walks the flags); the flags are indexed in
+// that kernel's grid, which this kernel runs exactly (4 rows x 128 queries of
+// one head per workgroup).
 //
 // Layout: 4 waves per workgroup, each owning one row of the group and its
 // 128 queries (NQT = 8 tiles of 16); two workgroups per CU, so two waves per
