@@ -58,11 +58,16 @@ namespace {
 // past cw are held at zero (zero LayerNorm affine, zero weight columns). NB:
 // the 32-channel blocks of x worked on (cw / 32 when it is known at compile
 // time, else all 4, the ones past cw being zero).
+// Pipeline: two LDS tiles. Halfway through a tile's MFMAs and sigmoids the
+// workgroup LayerNorms the next tile into the other buffer (its rows were
+// fetched a tile earlier) and fetches the one after: the two waves of a SIMD
+// belong to this one workgroup and would otherwise run the VALU-only
+// LayerNorm and the MFMA phase in lockstep, one after the other.
 // ---------------------------------------------------------------------------
 template <typename T, bool kNarrow, int NB = 4>
 __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulPrologueParams<T> P, int64_t ntiles) {
-  __shared__ __attribute__((aligned(16))) T xs[kTP][kLd];
-  __shared__ __attribute__((aligned(16))) float mrow[kTP];
+  __shared__ __attribute__((aligned(16))) T xs[2][kTP][kLd];
+  __shared__ __attribute__((aligned(16))) float mrow[2][kTP];
   __shared__ __attribute__((aligned(16))) LnAffine ln;
 
   const int64_t n = P.n;
@@ -111,29 +116,27 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
   int64_t tile = blockIdx.x;
   if (tile < ntiles) fetch(tile);
   __syncthreads();  // LayerNorm affine staged
-  for (; tile < ntiles; tile += gridDim.x) {
+  auto ln_tile = [&](int buf) {
+    ln_quad<T, T, NB>(xr, ln, P.eps, &xs[buf][p][0], cw);
+    if ((t & 3) == 0) mrow[buf][p] = mvalid ? (P.mask ? to_f32(mraw) : 1.0f) : 0.f;
+  };
+  if (tile < ntiles) {
+    ln_tile(0);
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
+  }
+  __syncthreads();
+  for (int cur = 0; tile < ntiles; tile += gridDim.x, cur ^= 1) {
     const TileRS tl = tile_at(tile, ntx, n);
     const int nvalid = (int)min<int64_t>(kTP, n - tl.s0);
-    ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
-    if ((t & 3) == 0) mrow[p] = mvalid ? (P.mask ? to_f32(mraw) : 1.0f) : 0.f;
-    __syncthreads();
-    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
-
     T* dst = (half == 0 ? P.a_cm : P.b_cm) + (int64_t)tl.b * kC * nn + (int64_t)tl.r * n + tl.s0;
-    // row tiles in pairs with paired rows: lane group g holds positions
-    // 32j + 8g .. +7 of its channel, one 16-byte store per channel row
-    // two row-tile pairs per loop body give the scheduler the next pair's
-    // MFMAs to issue under this pair's sigmoids (the 2-block form keeps one:
-    // unrolled it needs more than the 128 VGPRs of two workgroups per CU)
-    constexpr int kJUnroll = NB == 4 ? 2 : 1;
-#pragma unroll kJUnroll
-    for (int j = 0; j < kTP / 32; ++j) {
+    auto pair = [&](int j) {
       f32x4 ap[2][2], ag[2][2];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) tile_mma2_row<T, false, NB>(xs, paired_row(j, h, lane & 15), wp, wg, ap[h], ag[h]);
+      for (int h = 0; h < 2; ++h)
+        tile_mma2_row<T, false, NB>(xs[cur], paired_row(j, h, lane & 15), wp, wg, ap[h], ag[h]);
       const int p0 = 32 * j + 8 * (lane >> 4);
-      const f32x4 m0 = *reinterpret_cast<const f32x4*>(&mrow[p0]);
-      const f32x4 m1 = *reinterpret_cast<const f32x4*>(&mrow[p0 + 4]);
+      const f32x4 m0 = *reinterpret_cast<const f32x4*>(&mrow[cur][p0]);
+      const f32x4 m1 = *reinterpret_cast<const f32x4*>(&mrow[cur][p0 + 4]);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
         float v[8];
@@ -144,8 +147,16 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
         }
         store8_masked<T>(dst + (int64_t)(col0 + 16 * ct + (lane & 15)) * nn + p0, v, nvalid - p0, vec8, vec4);
       }
+    };
+    pair(0);
+    pair(1);
+    if (tile + gridDim.x < ntiles) {
+      ln_tile(cur ^ 1);  // the next tile's LayerNorm, under this tile's MFMAs
+      if (tile + 2 * gridDim.x < ntiles) fetch(tile + 2 * gridDim.x);
     }
-    __syncthreads();  // xs and mrow are free for the next tile
+    pair(2);
+    pair(3);
+    __syncthreads();  // the next tile's rows are in LDS; this tile's buffer is free
   }
 }
 
