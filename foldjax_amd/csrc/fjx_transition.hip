@@ -72,12 +72,17 @@ __device__ __forceinline__ void pair_bias_epilogue(const TransitionParams<T>& P,
 
 // The fp32 pair-bias weight split into bf16 high and low parts (16 heads x
 // 128) lives in the padding columns of the two tiles, which no tile access
-// touches: the high part in xs, the low part in hs, element (h, k) at row
-// 8h + k/16, column 128 + k%16. Without it in a buffer of its own the
-// kernel's LDS stays within two workgroups per CU.
+// touches: the high part in xs, the low part in hs. Without it in a buffer
+// of its own the kernel's LDS stays within two workgroups per CU. The 16
+// 8-element chunks c = k / 8 of head h sit in row 16 (c / 2) + h, padding
+// half (c % 2) ^ (h / 8): with 288-byte rows the 16-byte bank group of that
+// half is 2 h + ((c % 2) ^ (h / 8)) mod 16, so the 16 heads a fragment read
+// gathers (one per lane row) hit 16 distinct groups (rows 8h + k/16 would
+// put all 16 on one group).
 static_assert(tile::kLd - tile::kC == 16 && 16 * tile::kC == 16 * tile::kTP, "the split weight fills the padding");
 __device__ __forceinline__ bf16* wz_at(bf16 (*tl)[tile::kLd], int h, int k) {
-  return &tl[8 * h + (k >> 4)][tile::kC + (k & 15)];
+  const int c = k >> 3;
+  return &tl[16 * (c >> 1) + h][tile::kC + 8 * ((c & 1) ^ (h >> 3)) + (k & 7)];
 }
 
 // The same projection in fp32 for a bf16 transition (the attention runs in
