@@ -129,6 +129,15 @@ __device__ __forceinline__ int64_t grid_row(int64_t r, int64_t n, int t) {
 // wave-wide xor shuffle of a float (64 lanes)
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// v + v[lane ^ 1], then + [lane ^ 2]: the sum over each quad of lanes, the
+// same additions in the same order as two shfl_xor steps, on DPP quad
+// permutes (VALU operand modifiers) instead of ds_bpermute round trips
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  return v;
+}
+
 // LayerNorm of one row of c <= 512 channels by one wave, lane l holding
 // channels 8 l .. 8 l + 7
 template <typename T>

@@ -6,6 +6,7 @@
 
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 
 #include "fjx_common.hpp"
@@ -88,28 +89,62 @@ __device__ __forceinline__ void store_row_part(const RowPart<T>& r, T* __restric
 // LayerNorm of 128 channels held by 4 consecutive threads (the chunks of
 // load_row_part); put(c, o) receives the 8 outputs of channels c .. c+7.
 // cw < 128: the statistics are those of the first cw channels (the chunks
-// past cw hold zeros and are left out of the variance)
-template <typename T, typename Put, int NB = 4>
+// past cw hold zeros and are left out of the variance). kDot: bf16 rows
+// take their statistics on v_dot2_f32_bf16 (below) and the quad sums on
+// DPP; otherwise, and for fp32 rows, two passes over the unpacked values
+template <typename T, typename Put, int NB = 4, bool kDot = true>
 __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine& l, float eps, Put put, int cw = kC) {
   float v[8 * NB];
 #pragma unroll
   for (int q = 0; q < NB; ++q) to_f32x8(r.f[q], v + 8 * q);
-  float s = 0.f;
-#pragma unroll
-  for (int e = 0; e < 8 * NB; ++e) s += v[e];
-  s += shfl_xor(s, 1);
-  s += shfl_xor(s, 2);
   const float inv_c = cw == kC ? 1.0f / kC : 1.0f / (float)cw;
-  const float mean = s * inv_c;
-  float q2 = 0.f;
+  float mean, var;
+  if constexpr (kDot && std::is_same<T, bf16>::value) {
+    // bf16 rows: the sum and the sum of squares straight from the packed
+    // pairs on v_dot2_f32_bf16 (a bf16 product is exact in fp32), one
+    // instruction per two channels instead of an unpack, an add and a
+    // square per channel; var = E[x^2] - mean^2 in fp32 (chunks past cw
+    // hold zeros and add nothing to either sum)
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one = {static_cast<bf16>(1.0f), static_cast<bf16>(1.0f)};
+    float s[2] = {0.f, 0.f}, q2[2] = {0.f, 0.f};
 #pragma unroll
-  for (int e = 0; e < 8 * NB; ++e) {
-    const float d = v[e] - mean;
-    if (cw == kC || 32 * (e / 8) < cw) q2 += d * d;
+    for (int q = 0; q < NB; ++q) {
+      const u32x4 u = __builtin_bit_cast(u32x4, r.f[q]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // through a scalar: a bit_cast of the vector element itself compiles
+        // to a read of element 0 whatever e is
+        const uint32_t w = u[e];
+        const bf16x2 pr = __builtin_bit_cast(bf16x2, w);
+        s[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, one, s[e & 1], false);
+        q2[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(pr, pr, q2[e & 1], false);
+      }
+    }
+    const float st = quad_sum(s[0] + s[1]), qt = quad_sum(q2[0] + q2[1]);
+    mean = st * inv_c;
+    var = fmaxf(fmaf(-mean, mean, qt * inv_c), 0.f);
+  } else {
+    // the same sums whichever way the quad's lanes are combined (DPP or
+    // ds_bpermute); the tri-mul prologue measured faster with the latter
+    auto qsum = [](float x) {
+      if constexpr (kDot) return quad_sum(x);
+      x += shfl_xor(x, 1);
+      return x + shfl_xor(x, 2);
+    };
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8 * NB; ++e) s += v[e];
+    mean = qsum(s) * inv_c;
+    float q2 = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8 * NB; ++e) {
+      const float d = v[e] - mean;
+      if (cw == kC || 32 * (e / 8) < cw) q2 += d * d;
+    }
+    var = qsum(q2) * inv_c;
   }
-  q2 += shfl_xor(q2, 1);
-  q2 += shfl_xor(q2, 2);
-  const float rstd = __builtin_amdgcn_rsqf(q2 * inv_c + eps);
+  const float rstd = __builtin_amdgcn_rsqf(var + eps);
   const float shift = -mean * rstd;
 #pragma unroll
   for (int q = 0; q < NB; ++q) {
@@ -132,11 +167,11 @@ __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine&
 }
 
 // ... written to the same channels of dst_row as TO
-template <typename T, typename TO, int NB = 4>
+template <typename T, typename TO, int NB = 4, bool kDot = true>
 __device__ __forceinline__ void ln_quad(const RowPart<T>& r, const LnAffine& l, float eps, TO* __restrict__ dst_row,
                                         int cw = kC) {
   auto put = [&](int c, const float* o) { store8(dst_row + c, pack8<TO>(o)); };
-  ln_quad_put<T, decltype(put), NB>(r, l, eps, put, cw);
+  ln_quad_put<T, decltype(put), NB, kDot>(r, l, eps, put, cw);
 }
 
 // One wave's 32 output channels col0..col0+31 of a [128][128] weight as MFMA
