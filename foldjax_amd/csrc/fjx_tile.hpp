@@ -124,6 +124,18 @@ __device__ __forceinline__ void ln_quad_put(const RowPart<T>& r, const LnAffine&
     const float st = quad_sum(s[0] + s[1]), qt = quad_sum(q2[0] + q2[1]);
     mean = st * inv_c;
     var = fmaxf(fmaf(-mean, mean, qt * inv_c), 0.f);
+    // E[x^2] - mean^2 cancels when the mean dwarfs the spread; past a
+    // ratio of 64 (6 bits of the fp32 sums) the row takes the two-pass
+    // variance instead (quad-uniform: the 4 lanes hold the same sums)
+    if (mean * mean > 64.0f * var) {
+      float q2b = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8 * NB; ++e) {
+        const float d = v[e] - mean;
+        if (cw == kC || 32 * (e / 8) < cw) q2b += d * d;
+      }
+      var = quad_sum(q2b) * inv_c;
+    }
   } else {
     // the same sums whichever way the quad's lanes are combined (DPP or
     // ds_bpermute); the tri-mul prologue measured faster with the latter
