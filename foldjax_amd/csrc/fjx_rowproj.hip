@@ -449,6 +449,9 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 #pragma unroll
       for (int e = 0; e < 8; ++e) xp[p0 + e][ch] = ot[it][e];
     }
+    // the tile's x and o are in LDS: the next tile's loads go out now, ahead
+    // of LN_out and its two barriers
+    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
     __syncthreads();
     {
       // LN_out in place: each thread rewrites exactly the 32 channels it reads
@@ -457,7 +460,6 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
       ln_quad<T>(rp, ln_out, P.eps, &xp[p][0]);
     }
     __syncthreads();
-    if (tile + gridDim.x < ntiles) fetch(tile + gridDim.x);
 
 #pragma unroll 2
     for (int rt = 0; rt < (active ? kTE / 16 : 0); ++rt) {
