@@ -74,3 +74,20 @@ def mask_case(kind: str, n: int, seed: int = 3) -> np.ndarray:
         m[min(1, n - 1), :] = 0.0
         return m
     raise ValueError(kind)
+
+
+def spike_rows(rng: np.random.Generator, rows: int, c: int = 128) -> np.ndarray:
+    """Every other row bf16-exact with its mean dwarfing its spread: a
+    constant value (8-bit mantissa, 2^-4 to 2^15, either sign) with one or two
+    entries one bf16 step away, mean^2 / variance up to about 10^6; ordinary
+    rows in between."""
+    x = rng.standard_normal((rows, c)).astype(np.float32)
+    for r in range(0, rows, 2):
+        base = float(syn.bf16_round(np.array(
+            [2.0 ** rng.integers(-4, 15) * (1 + rng.integers(1, 128) / 128) * (1 if rng.random() < 0.5 else -1)],
+            dtype=np.float32))[0])
+        step = abs(base) * 2.0 ** -7
+        x[r] = base
+        for k in rng.choice(c, size=1 + r % 2, replace=False):
+            x[r, k] = syn.bf16_round(np.array([base + step * (1 if rng.random() < 0.5 else -1)], dtype=np.float32))[0]
+    return x

@@ -13,7 +13,7 @@ from foldjax_amd import params as P
 from foldjax_amd import synthetic as syn
 from foldjax_amd.pairformer import PairformerLayerWeights
 from oracle import triangle as O
-from tests.gpu_util import assert_parity, device_tensor, prep, prep_tree, say, to_np
+from tests.gpu_util import assert_parity, device_tensor, prep, prep_tree, say, spike_rows, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -35,23 +35,6 @@ def test_transition_parity(dt, c, rows):
     assert_parity(to_np(got), want, dtype, f"transition c={c}")
 
 
-def _spike_rows(rng, rows):
-    """Every other row bf16-exact with its mean dwarfing its spread: a
-    constant value (8-bit mantissa, 2^-4 to 2^15, either sign) with one or two
-    entries one bf16 step away, mean^2 / variance up to about 10^6; ordinary
-    rows in between."""
-    x = rng.standard_normal((rows, 128)).astype(np.float32)
-    for r in range(0, rows, 2):
-        base = float(syn.bf16_round(np.array(
-            [2.0 ** rng.integers(-4, 15) * (1 + rng.integers(1, 128) / 128) * (1 if rng.random() < 0.5 else -1)],
-            dtype=np.float32))[0])
-        step = abs(base) * 2.0 ** -7
-        x[r] = base
-        for c in rng.choice(128, size=1 + r % 2, replace=False):
-            x[r, c] = syn.bf16_round(np.array([base + step * (1 if rng.random() < 0.5 else -1)], dtype=np.float32))[0]
-    return x
-
-
 def test_transition_spike_rows_bf16():
     """Rows whose mean dwarfs their spread, where the LayerNorm's one-pass
     statistics E[x^2] - mean^2 cancel most (the bf16 LayerNorm takes them on
@@ -60,7 +43,7 @@ def test_transition_spike_rows_bf16():
     dtype = torch.bfloat16
     say("transition spike rows bf16")
     rng = np.random.default_rng(11)
-    x = _spike_rows(rng, 96)
+    x = spike_rows(rng, 96)
     w = syn.transition_weights(128, seed=11)
     got = protenix.transition(device_tensor(x, dtype), _protenix_transition(w))
     torch.cuda.synchronize()

@@ -16,7 +16,7 @@ from foldjax_amd import boltz2, kernels, openfold3, protenix
 from foldjax_amd import params as P
 from foldjax_amd import synthetic as syn
 from oracle import triangle as O
-from tests.gpu_util import assert_parity, device_tensor, mask_case, prep, prep_tree, say, to_np
+from tests.gpu_util import assert_parity, device_tensor, mask_case, prep, prep_tree, say, spike_rows, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -45,6 +45,37 @@ def test_trimul_parity(dt, direction, n, mask_kind):
     got, want, dtype = _trimul_case(n, dt, direction, mask_kind)
     assert got.shape == want.shape
     assert_parity(got, want, dtype, f"trimul {direction} n={n}")
+
+
+@pytest.mark.parametrize("op,arg", [("trimul", "outgoing"), ("trimul", "incoming"), ("triattn", True), ("triattn", False)])
+def test_spike_rows_bf16(op, arg):
+    """Pair tensors whose every other position is a row with its mean
+    dwarfing its spread (the bf16 LayerNorms take one-pass statistics and
+    switch to the two-pass variance for such rows): tri-mul both directions,
+    tri-attn both nodes, at the bf16 bar."""
+    dtype = torch.bfloat16
+    n = 48
+    say(f"spike rows {op} {arg} n={n} bf16")
+    z = spike_rows(np.random.default_rng(5), n * n).reshape(n, n, 128)
+    m = mask_case("random", n)
+    if op == "trimul":
+        w = syn.trimul_weights(128, 128, seed=6)
+        got = protenix.triangle_multiplication(device_tensor(z, dtype), device_tensor(m, dtype),
+                                               P.trimul_to_protenix(w), arg)
+        torch.cuda.synchronize()
+        want = O.protenix_triangle_multiplication(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), arg)
+    else:
+        w = syn.triattn_weights(128, 4, 32, seed=6)
+        got = protenix.triangle_attention(device_tensor(z, dtype), device_tensor(m, dtype),
+                                          P.triattn_to_protenix(w), num_heads=4, starting=arg)
+        torch.cuda.synchronize()
+        want = O.protenix_triangle_attention(prep(z, dtype), prep(m, dtype), prep_tree(w, dtype), num_heads=4,
+                                             starting=arg)
+    g = to_np(got)
+    if op == "triattn":  # fully masked rows of the attention are finite but arbitrary (compared elsewhere)
+        rows = _valid_rows(m, arg)
+        g, want = (g[rows], want[rows]) if arg else (g[:, rows], want[:, rows])
+    assert_parity(g, want, dtype, f"spike rows {op} {arg}")
 
 
 def _valid_rows(m: np.ndarray, starting: bool) -> np.ndarray:
