@@ -47,6 +47,27 @@ __device__ __forceinline__ void stage_ln_w(const T* __restrict__ ln_w, const T* 
   if (t < kC) l.w[t] = t < cw ? to_f32(ln_w[t]) : 0.f;
   else if (t < 2 * kC) l.b[t - kC] = t - kC < cw ? to_f32(ln_b[t - kC]) : 0.f;
 }
+// The same staging in two halves, for a kernel that stages an affine per
+// tile: the fetch is one unconditional load per thread (threads 0..127 gamma,
+// 128..255 beta, the others a clamped duplicate; channels at or past cw read
+// the last valid one), issued before the tile's row loads, and the put writes
+// it to LDS after them. A branch per thread, as in stage_ln, puts a wait for
+// every load issued so far (the row loads included) in front of each LDS
+// write.
+template <typename T>
+__device__ __forceinline__ T ln_fetch(const T* __restrict__ ln_w, const T* __restrict__ ln_b, int cw = kC) {
+  const int ti = min((int)threadIdx.x, 2 * kC - 1);
+  const int c = min(ti < kC ? ti : ti - kC, cw - 1);
+  return *((ti < kC ? ln_w : ln_b) + c);
+}
+template <typename T>
+__device__ __forceinline__ void ln_put(LnAffine& l, T v, int cw = kC) {
+  const int t = threadIdx.x;
+  if (t < 2 * kC) {
+    const int c = t < kC ? t : t - kC;
+    (t < kC ? l.w : l.b)[c] = c < cw ? to_f32(v) : 0.f;
+  }
+}
 
 // The 32 channels [32*part, +32) of one pair-tensor row (part = threadIdx.x % 4),
 // raw, or zeros when src is null (a position outside the grid)

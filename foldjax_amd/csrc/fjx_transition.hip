@@ -160,24 +160,25 @@ __device__ __forceinline__ void pair_bias_epilogue_f32(const TransitionParams<bf
 // bf16 high and low parts (hi = bf16(w), lo = bf16(w - hi)) in LDS, rows past
 // pb_heads zero (wz_at: the padding columns of xs and hs): the epilogue then
 // reads its fragments from LDS instead of waiting, at the end of the tile,
-// for global loads and the split
-__device__ __forceinline__ void stage_wz_split(const TransitionParams<bf16>& P, bf16 (*xs)[tile::kLd],
-                                               bf16 (*hs)[tile::kLd]) {
-  using namespace tile;
-  const int t = threadIdx.x;  // 512 threads x 4 weights = 16 x 128
+// for global loads and the split. In two halves like ln_fetch / ln_put: one
+// unconditional load per thread (512 threads x 4 weights = 16 x 128; heads
+// past pb_heads read the last one), then the split and the LDS writes.
+__device__ __forceinline__ f32x4 wz_fetch(const TransitionParams<bf16>& P) {
+  const int t = threadIdx.x;
+  const int h = min(t >> 5, P.pb_heads - 1);
+  return *reinterpret_cast<const f32x4*>(P.pbf_w + (int64_t)h * tile::kC + 4 * (t & 31));
+}
+__device__ __forceinline__ void wz_put(const TransitionParams<bf16>& P, f32x4 w, bf16 (*xs)[tile::kLd],
+                                       bf16 (*hs)[tile::kLd]) {
+  const int t = threadIdx.x;
   const int h = t >> 5;
   const int k0 = 4 * (t & 31);
   float hi[4], lo[4];
-  if (h < P.pb_heads) {
-    const f32x4 w = *reinterpret_cast<const f32x4*>(P.pbf_w + (int64_t)h * kC + k0);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      hi[e] = round_to<bf16>(w[e]);
-      lo[e] = w[e] - hi[e];
-    }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) hi[e] = lo[e] = 0.f;
+  for (int e = 0; e < 4; ++e) {
+    const float v = h < P.pb_heads ? w[e] : 0.f;
+    hi[e] = round_to<bf16>(v);
+    lo[e] = v - hi[e];
   }
   store4f(wz_at(xs, h, k0), hi);
   store4f(wz_at(hs, h, k0), lo);
@@ -218,18 +219,26 @@ __device__ __forceinline__ void transition128_body(const TransitionParams<T>& P)
   const int nch = kNarrow ? cw / 32 : 4;  // 128-wide hidden chunks (hidden = 4 cw)
 
   {
-    RowPart<T> xr;
-    if constexpr (kNarrow) {
-      load_row_part_w<T, NB>(p < nvalid ? P.x + (m0 + p) * cw : nullptr, xr, cw);
-      stage_ln_w<T>(P.ln_w, P.ln_b, ln, cw);
-    } else {
-      load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
-      stage_ln<T>(P.ln_w, P.ln_b, ln);
-    }
-    if (!kNarrow && P.pb_out) stage_ln<T>(P.pb_ln_w, P.pb_ln_b, pb_ln);
+    // every workgroup stages its affines (one tile each): their loads go out
+    // before the tile's rows, so that the LDS writes wait for them alone
+    // (ln_fetch)
+    const T lnv = ln_fetch<T>(P.ln_w, P.ln_b, cw);
+    const bool pb = !kNarrow && !kPbF32 && P.pb_out;
+    const T pbv = pb ? ln_fetch<T>(P.pb_ln_w, P.pb_ln_b) : lnv;
+    float pbfv = 0.f;
+    f32x4 wz = f32x4{0.f, 0.f, 0.f, 0.f};
     if constexpr (kPbF32) {
-      stage_ln<float>(P.pbf_ln_w, P.pbf_ln_b, pb_ln);
-      stage_wz_split(P, xs, hs);
+      pbfv = ln_fetch<float>(P.pbf_ln_w, P.pbf_ln_b);
+      wz = wz_fetch(P);
+    }
+    RowPart<T> xr;
+    if constexpr (kNarrow) load_row_part_w<T, NB>(p < nvalid ? P.x + (m0 + p) * cw : nullptr, xr, cw);
+    else load_row_part<T>(p < nvalid ? P.x + (m0 + p) * kC : nullptr, xr);
+    ln_put<T>(ln, lnv, cw);
+    if (pb) ln_put<T>(pb_ln, pbv);
+    if constexpr (kPbF32) {
+      ln_put<float>(pb_ln, pbfv);
+      wz_put(P, wz, xs, hs);
     }
     __syncthreads();
     ln_quad<T, T, NB>(xr, ln, P.eps, &xs[p][0], cw);
