@@ -56,9 +56,11 @@ def _args():
                    help="the single track's dtype: fp32 as the reference runs it over the bf16 pair track "
                         "(B2K/pairformer.py:182-199), or bf16")
     p.add_argument("--op", default="block",
-                   choices=["block", "trimul", "triattn", "transition", "transition_pb", "copy", "mixprobe"],
+                   choices=["block", "trimul", "triattn", "transition", "transition_pb", "copy", "mixprobe",
+                            "hbmprobe"],
                    help="profiling aid: run only one sublayer kind per step instead of the whole block; mixprobe: "
-                        "the issue rate of the flash attention's per-tile instruction mix alone")
+                        "the issue rate of the flash attention's per-tile instruction mix alone; hbmprobe: the rate "
+                        "of a plain HBM streaming kernel over the pair tensor's size")
     p.add_argument("--c-z", type=int, default=128,
                    help="with --op trimul|triattn|transition: the pair width (other than 128 runs the general-width "
                         "paths, e.g. 64 for the template stack, 384 for OpenDDE's structural pair track)")
@@ -295,6 +297,30 @@ def mix_probe(n: int) -> dict:
     return out
 
 
+HBM_MODES = {0: "copy", 1: "copy, nontemporal loads and stores", 2: "read only", 3: "write only"}
+
+
+def hbm_probe(n: int) -> dict:
+    """``fjx_probe_hbm_stream`` over two buffers of the pair tensor's size at
+    n (n * n * 128 bf16 values): each mode at 1, 2, 4 and 8 workgroups per
+    CU, GB/s of bytes moved (a copy moves twice the buffer)."""
+    import torch
+
+    from foldjax_amd import _lib
+
+    torch.zeros(1, device="cuda")  # the device context
+    nbytes = n * n * 128 * 2
+    out = {"op": "hbmprobe", "n": n, "bytes": nbytes, "modes": {}}
+    for mode, what in HBM_MODES.items():
+        row = {"mode": what}
+        moved = nbytes * (2 if mode in (0, 1) else 1)
+        for w in (1, 2, 4, 8):
+            ms = min(_lib.probe_hbm_stream(mode, w, nbytes) for _ in range(3))
+            row[f"wgs{w}"] = {"ms": round(ms, 4), "gbs": round(moved / (ms * 1e-3) / 1e9, 1)}
+        out["modes"][str(mode)] = row
+    return out
+
+
 def _timed(fn, steps: int, warmup: int, dev) -> float:
     import torch
 
@@ -397,6 +423,9 @@ def main() -> int:
 
     if a.op == "mixprobe":
         print(json.dumps(mix_probe(a.n)))
+        return 0
+    if a.op == "hbmprobe":
+        print(json.dumps(hbm_probe(a.n)))
         return 0
 
     dev = torch.device("cuda:0")

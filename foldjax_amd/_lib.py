@@ -126,6 +126,7 @@ SYMBOLS = {
     "fjx_prof_read": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_i64)]),
     "fjx_probe_issue_mix": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_float),
                                            _vp]),
+    "fjx_probe_hbm_stream": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _i64, ctypes.POINTER(ctypes.c_float), _vp]),
 }
 
 _lock = threading.Lock()
@@ -196,4 +197,12 @@ def probe_issue_mix(mix: int, waves_per_simd: int, iters: int, stream: int = 0) 
     instruction mix alone; see the header)."""
     ms = ctypes.c_float()
     check(load().fjx_probe_issue_mix(mix, waves_per_simd, iters, ctypes.byref(ms), stream))
+    return ms.value
+
+
+def probe_hbm_stream(mode: int, wgs_per_cu: int, nbytes: int, stream: int = 0) -> float:
+    """Kernel milliseconds of ``fjx_probe_hbm_stream`` (a plain HBM streaming
+    kernel; see the header)."""
+    ms = ctypes.c_float()
+    check(load().fjx_probe_hbm_stream(mode, wgs_per_cu, nbytes, ctypes.byref(ms), stream))
     return ms.value

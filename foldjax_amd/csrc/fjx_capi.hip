@@ -1237,6 +1237,18 @@ int fjx_probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipSt
   return FJX_OK;
 }
 
+int fjx_probe_hbm_stream(int mode, int wgs_per_cu, int64_t bytes, float* ms, hipStream_t st) {
+  g_err.clear();
+  if (mode < 0 || mode > 3 || wgs_per_cu < 1 || wgs_per_cu > 32 || bytes < 4096 || bytes % 4096 != 0 ||
+      bytes > ((int64_t)1 << 34) || !ms)
+    return fail(FJX_ERR_INVALID,
+                "fjx_probe_hbm_stream: mode 0..3, 1..32 workgroups per CU, bytes a multiple of 4096 in [4 KiB, "
+                "16 GiB], ms non-NULL");
+  if (fjx::probe_hbm_stream(mode, wgs_per_cu, bytes, ms, st) != 0)
+    return fail(FJX_ERR_HIP, "fjx_probe_hbm_stream: a HIP call failed");
+  return FJX_OK;
+}
+
 int fjx_prof_num_kernels(void) { return K_COUNT; }
 
 const char* fjx_prof_kernel_name(int id) { return (id >= 0 && id < K_COUNT) ? kKernelNames[id] : ""; }

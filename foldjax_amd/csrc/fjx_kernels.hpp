@@ -237,6 +237,7 @@ void launch_flash_single(const FlashParams<T>& p, int64_t batch, hipStream_t st)
 bool launch_flash_pipe(const FlashParams<bf16>& p, int64_t batch, hipStream_t st);
 // the flash tile's instruction mix alone (fjx_probe.hip): kernel ms, or -1 on a HIP error
 int probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream_t st);
+int probe_hbm_stream(int mode, int wgs_per_cu, int64_t bytes, float* ms, hipStream_t st);
 
 // general-width paths (fjx_generic.hip); positions v = r*n + s of the virtual
 // grid read the original grid at s*n + r when t = 1

@@ -13,6 +13,11 @@
 // Mixes: 0 = the kernel's (10 MFMA + 16 exp + 24 VALU), 1 = without the bias
 // widenings (10 MFMA + 16 exp + 8 VALU), 2 = the 10 MFMAs alone, 3 = the 16
 // exponentials alone, 4 = the 24 VALU alone.
+//
+// A second probe streams 16-byte accesses through HBM (copy, nontemporal
+// copy, read only, write only) at a chosen number of workgroups per CU: the
+// rate a plain streaming kernel reaches on this part, the practical ceiling
+// the HBM-bound row kernels are measured against beside the 8 TB/s figure.
 #include <hip/hip_runtime.h>
 
 #include "fjx_common.hpp"
@@ -108,6 +113,35 @@ __global__ __launch_bounds__(256) void issue_mix_kernel(float* sink, int iters) 
 #undef FJX_V
 #undef FJX_OPS
 
+// HBM streaming probe: 16-byte accesses over two device buffers, a
+// grid-stride loop of gridDim.x 256-thread workgroups, four accesses in
+// flight per lane. Mode 0 copies a -> b, mode 1 copies with nontemporal
+// loads and stores, mode 2 only reads a (folded into one value per lane
+// that is stored only if it matches a constant), mode 3 only writes b.
+template <int MODE>
+__global__ __launch_bounds__(256) void hbm_stream_kernel(const u32x4* __restrict__ a, u32x4* __restrict__ b,
+                                                         int64_t n, unsigned* sink) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  unsigned acc = 0;
+  for (; i + 3 * stride < n; i += 4 * stride) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if constexpr (MODE == 1) v[u] = __builtin_nontemporal_load(a + i + u * stride);
+      else if constexpr (MODE == 3) v[u] = u32x4{(unsigned)i, 1u, 2u, (unsigned)u};
+      else v[u] = a[i + u * stride];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if constexpr (MODE == 1) __builtin_nontemporal_store(v[u], b + i + u * stride);
+      else if constexpr (MODE == 2) acc ^= v[u][u];
+      else b[i + u * stride] = v[u];
+    }
+  }
+  if (MODE == 2 && acc == 0x9E3779B9u) sink[0] = acc;
+}
+
 }  // namespace
 
 // waves_per_simd waves on each SIMD of the device's CUs (256-thread
@@ -143,6 +177,48 @@ int probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream
   (void)hipStreamSynchronize(st);
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
+  return rc;
+}
+
+// mode (0-3, hbm_stream_kernel) over `bytes` (a multiple of 4 KiB) with
+// wgs_per_cu workgroups per CU: one warm-up launch, then one timed launch;
+// its time in ms (HIP events on `st`, synchronised). The two buffers are
+// allocated and freed on `st`.
+int probe_hbm_stream(int mode, int wgs_per_cu, int64_t bytes, float* ms, hipStream_t st) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess)
+    return -1;
+  u32x4 *a = nullptr, *b = nullptr;
+  unsigned* sink = nullptr;
+  if (hipMallocAsync(reinterpret_cast<void**>(&a), (size_t)bytes, st) != hipSuccess) return -1;
+  if (hipMallocAsync(reinterpret_cast<void**>(&b), (size_t)bytes, st) != hipSuccess) return -1;
+  if (hipMallocAsync(reinterpret_cast<void**>(&sink), 64, st) != hipSuccess) return -1;
+  if (hipMemsetAsync(a, 1, (size_t)bytes, st) != hipSuccess) return -1;
+  const int64_t n = bytes / 16;
+  const dim3 grid((unsigned)(cus * wgs_per_cu));
+  auto launch = [&]() {
+    switch (mode) {
+      case 0: hipLaunchKernelGGL(hbm_stream_kernel<0>, grid, dim3(256), 0, st, a, b, n, sink); break;
+      case 1: hipLaunchKernelGGL(hbm_stream_kernel<1>, grid, dim3(256), 0, st, a, b, n, sink); break;
+      case 2: hipLaunchKernelGGL(hbm_stream_kernel<2>, grid, dim3(256), 0, st, a, b, n, sink); break;
+      default: hipLaunchKernelGGL(hbm_stream_kernel<3>, grid, dim3(256), 0, st, a, b, n, sink); break;
+    }
+  };
+  hipEvent_t e0, e1;
+  if (hipEventCreate(&e0) != hipSuccess) return -1;
+  if (hipEventCreate(&e1) != hipSuccess) return -1;
+  launch();
+  (void)hipEventRecord(e0, st);
+  launch();
+  (void)hipEventRecord(e1, st);
+  int rc = hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(ms, e0, e1) == hipSuccess ? 0 : -1;
+  (void)hipFreeAsync(a, st);
+  (void)hipFreeAsync(b, st);
+  (void)hipFreeAsync(sink, st);
+  (void)hipStreamSynchronize(st);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
   return rc;
 }
 

@@ -373,6 +373,18 @@ int fjx_prof_read(int id, double* total_ms, int64_t* launches);
  */
 int fjx_probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream_t stream);
 
+/*
+ * Measurement aid, no counterpart in the reference: the rate of a plain HBM
+ * streaming kernel, the practical ceiling beside the 8 TB/s figure for the
+ * HBM-bound row kernels. Streams 16-byte accesses over two device buffers of
+ * `bytes` each (a multiple of 4096, at most 16 GiB; allocated and freed on
+ * `stream`): mode 0 copies, 1 copies with nontemporal loads and stores, 2
+ * only reads, 3 only writes; wgs_per_cu (1-32) 256-thread workgroups per CU.
+ * Returns the time of one launch after a warm-up launch in *ms (the call
+ * waits for it).
+ */
+int fjx_probe_hbm_stream(int mode, int wgs_per_cu, int64_t bytes, float* ms, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
