@@ -115,6 +115,12 @@ __device__ __forceinline__ float fast_sigmoid(float x) {
   // each); saturates cleanly to 0 (2^big = inf, rcp(inf) = 0) and to 1
   return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
+// the same sigmoid of x given y = -x log2 e, for a gate whose projection
+// weights were scaled by -log2 e in advance (scale_wslab): no multiply per
+// element
+__device__ __forceinline__ float sigmoid_nl2e(float y) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y));
+}
 
 // pair-grid row r = b n^2 + i n + j -> b n^2 + j n + i when t is set
 __device__ __forceinline__ int64_t grid_row(int64_t r, int64_t n, int t) {

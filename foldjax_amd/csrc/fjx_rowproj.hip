@@ -93,6 +93,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
     load_wslab<T>(P.w_g + (int64_t)half * kC * kC, col0, wg);
     stage_ln<T>(P.ln_w, P.ln_b, ln);
   }
+  scale_wslab<T>(wg, -kLog2e);  // gates from sigmoid_nl2e
 
   // the fetched position's mask value stays raw until it is used: a
   // conversion in the fetch would wait there for every load in flight,
@@ -144,8 +145,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_kernel(TriMulProloguePara
         float v[8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          v[q] = m0[q] * fast_sigmoid(ag[0][ct][q]) * ap[0][ct][q];
-          v[4 + q] = m1[q] * fast_sigmoid(ag[1][ct][q]) * ap[1][ct][q];
+          v[q] = m0[q] * sigmoid_nl2e(ag[0][ct][q]) * ap[0][ct][q];
+          v[4 + q] = m1[q] * sigmoid_nl2e(ag[1][ct][q]) * ap[1][ct][q];
         }
         store8_masked<T>(dst + (int64_t)(col0 + 16 * ct + (lane & 15)) * nn + p0, v, nvalid - p0, vec8, vec4);
       }
@@ -381,6 +382,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
     load_wslab_paired<T>(P.w_pout, col0, wp);
     stage_ln<T>(P.ln_in_w, P.ln_in_b, ln_in);
   }
+  scale_wslab<T>(wg, -kLog2e);  // gates from sigmoid_nl2e
   stage_ln<T>(P.ln_out_w, P.ln_out_b, ln_out);
 
   // per-tile inputs: the x row of position t/4 and 4 chunks of the
@@ -475,7 +477,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(TriMulEpiloguePara
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) y[4 * ct + q] = ap[ct][q] * round_to<T>(fast_sigmoid(ag[ct][q]));
+          for (int q = 0; q < 4; ++q) y[4 * ct + q] = ap[ct][q] * round_to<T>(sigmoid_nl2e(ag[ct][q]));
         if (P.residual) {
           float rv[8];
           if constexpr (res_x) to_f32x8(load8(&xraw[pp][c]), rv);
@@ -536,6 +538,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
     load_wslab_paired<T>(P.w_o, col0, wo);
     if (gated) stage_ln<T>(P.ln_w, P.ln_b, ln);
   }
+  if (gated) scale_wslab<T>(wg, -kLog2e);  // gates from sigmoid_nl2e
 
   auto orig_of = [&](const TileRS& tl, int pp) -> int64_t {
     const int64_t s = tl.s0 + pp;
@@ -602,7 +605,7 @@ __global__ __launch_bounds__(256) void triattn_epilogue_kernel(TriAttnEpiloguePa
         for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            ov[rt][4 * ct + q] = from_f32<T>(to_f32(ov[rt][4 * ct + q]) * fast_sigmoid(ag[ct][q]));
+            ov[rt][4 * ct + q] = from_f32<T>(to_f32(ov[rt][4 * ct + q]) * sigmoid_nl2e(ag[ct][q]));
       }
     }
     // gated (or raw) o -> xo; the four waves fill its 128 channels

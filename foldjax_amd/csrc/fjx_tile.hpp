@@ -222,6 +222,20 @@ __device__ __forceinline__ void load_wslab(const T* __restrict__ w, int col0, WS
       wf[ks][ct] = load8(w + (int64_t)(col0 + 16 * ct + (lane & 15)) * kC + 32 * ks + 8 * (lane >> 4));
 }
 
+// A slab times s, each weight rounded back to T: the persistent row kernels
+// hold their gate slabs as -log2(e) W once per launch, so that a gate is
+// sigmoid_nl2e of the accumulator (one multiply per element less; in bf16
+// each weight moves by at most half an ulp of the scaled value)
+template <typename T>
+__device__ __forceinline__ void scale_wslab(WSlab<T>& wf, float s) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wf[ks][ct][e] = from_f32<T>(to_f32(wf[ks][ct][e]) * s);
+}
+
 // The same slab with its output channels paired: row i of column tile ct is
 // channel col0 + 8 (i/4) + 4 ct + i%4, so in the transposed form lane group g
 // holds the 8 consecutive channels col0 + 8g .. +7 (acc[0] the first four,
