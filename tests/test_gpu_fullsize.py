@@ -58,11 +58,11 @@ class Lines:
         return self.rows[i]
 
 
-def device_normal(shape, seed: int) -> torch.Tensor:
-    """``N(0,1)`` drawn on the device (seeded), rounded to bf16."""
+def device_normal(shape, seed: int, dtype: torch.dtype = BF16) -> torch.Tensor:
+    """``N(0,1)`` drawn on the device (seeded), in ``dtype`` (bf16: rounded)."""
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
-    return torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(BF16)
+    return torch.randn(shape, generator=g, device="cuda", dtype=torch.float32).to(dtype)
 
 
 def positions(n: int, n_real: int, seed: int, extra: int = 8) -> list[tuple[int, int]]:
@@ -84,9 +84,18 @@ def positions(n: int, n_real: int, seed: int, extra: int = 8) -> list[tuple[int,
     return sorted(pairs)
 
 
-def check_rows(got: np.ndarray, want: np.ndarray, what: str, tol: float = BF16_REL) -> float:
+# the fp32-mode bar (north star): max-abs error against the float64 oracle
+FP32_ABS = 1e-4
+
+
+def check_rows(got: np.ndarray, want: np.ndarray, what: str, tol: float = BF16_REL, absolute: bool = False) -> float:
+    """Per-position relative error (bf16 mode) or, with ``absolute``, the
+    largest absolute error of any element (fp32 mode) within ``tol``."""
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
-    errs = np.linalg.norm(got - want, axis=-1) / np.maximum(np.linalg.norm(want, axis=-1), 1e-30)
+    if absolute:
+        errs = np.max(np.abs(got - want).reshape(len(got), -1), axis=-1)
+    else:
+        errs = np.linalg.norm(got - want, axis=-1) / np.maximum(np.linalg.norm(want, axis=-1), 1e-30)
     worst = int(np.argmax(errs))
     assert errs[worst] <= tol, f"{what}: position {worst} relative error {errs[worst]:.3e} > {tol}"
     return float(errs.max())
@@ -97,47 +106,60 @@ def gather(t: torch.Tensor, pos) -> np.ndarray:
     return t[idx[:, 0], idx[:, 1]].float().cpu().numpy().astype(np.float64)
 
 
+def bar(dtype: torch.dtype) -> dict:
+    """check_rows' bar for the pair track's dtype."""
+    return {"tol": FP32_ABS, "absolute": True} if dtype == torch.float32 else {}
+
+
 def check_trimul(z, mask_np, w, wq, direction, pos, what):
     """Update-only parity at ``pos``, then the fused-residual output that is
     carried forward. Returns that output."""
-    m = torch.from_numpy(mask_np).to("cuda", BF16)
+    m = torch.from_numpy(mask_np).to("cuda", z.dtype)
     upd = kernels.trimul(z, m, w, direction)
     out = kernels.trimul(z, m, w, direction, residual=z)
     zl = Lines(z)
     want = O.triangle_multiplication_at(zl, mask_np, wq, direction, pos)
-    check_rows(gather(upd, pos), want, f"{what} update")
-    check_rows(gather(out, pos), gather(z, pos) + want, f"{what} z+update")
+    check_rows(gather(upd, pos), want, f"{what} update", **bar(z.dtype))
+    check_rows(gather(out, pos), gather(z, pos) + want, f"{what} z+update", **bar(z.dtype))
     return out
 
 
 def check_triattn(z, mask_np, w, wq, starting, pos, what):
-    m = torch.from_numpy(mask_np).to("cuda", BF16)
+    if z.dtype == torch.float32:
+        # fp32 mode leaves out attention rows whose keys are all masked (the
+        # padded tail), as the small-size fp32 tests do: the reference adds
+        # -1e9 to every key there in fp32, which rounds the scores away (a
+        # uniform softmax), where the float64 oracle keeps them
+        pos = [(i, q) for i, q in pos if (mask_np[i] if starting else mask_np[:, i]).max() > 0]
+    m = torch.from_numpy(mask_np).to("cuda", z.dtype)
     upd = kernels.triattn(z, m, w, starting=starting)
     out = kernels.triattn(z, m, w, starting=starting, residual=z)
     zl = Lines(z)
     want = O.triangle_attention_at(zl, mask_np, wq, num_heads=4, starting=starting, positions=pos)
     opos = pos if starting else [(q, i) for i, q in pos]  # output index of grid entry (i, q)
-    check_rows(gather(upd, opos), want, f"{what} update")
-    check_rows(gather(out, opos), gather(z, opos) + want, f"{what} z+update")
+    check_rows(gather(upd, opos), want, f"{what} update", **bar(z.dtype))
+    check_rows(gather(out, opos), gather(z, opos) + want, f"{what} z+update", **bar(z.dtype))
     return out
 
 
 def run_layer_checked(n: int, n_real: int, seed: int, tag: str, z: torch.Tensor | None = None,
-                      s: torch.Tensor | None = None):
+                      s: torch.Tensor | None = None, dtype: torch.dtype = BF16):
     """One Boltz-2 Pairformer layer at size n on the product kernels (the
     weights of ``syn.pairformer_layer_weights(seed)``), sublayer by sublayer,
     each checked at sampled positions; from the given ``[n, n, 128]`` z and
-    ``[n, 384]`` s, or from seeded random ones. Returns the layer's s and z."""
+    ``[n, 384]`` s, or from seeded random ones. ``dtype``: both tracks' (bf16:
+    the relative bar, fp32: max-abs 1e-4). Returns the layer's s and z."""
     w = syn.pairformer_layer_weights(seed=seed)
-    wq = prep_tree(w, BF16)
-    layer = PairformerLayerWeights.from_fields(w, BF16, "cuda")
+    wq = prep_tree(w, dtype)
+    layer = PairformerLayerWeights.from_fields(w, dtype, "cuda")
+    b = bar(dtype)
     tri = layer.triangle
     pm = syn.pair_mask(n, n_real)
     tm = syn.token_mask(n, n_real)
     if z is None:
-        z = device_normal((n, n, 128), seed=seed + 100)
+        z = device_normal((n, n, 128), seed=seed + 100, dtype=dtype)
     if s is None:
-        s = torch.from_numpy(syn.single_input(n, 384, seed=1)).to("cuda", BF16)
+        s = torch.from_numpy(syn.single_input(n, 384, seed=1)).to("cuda", dtype)
     pos = positions(n, n_real, seed)
     say(f"{tag}: n={n} n_real={n_real} tri-mul outgoing")
     z = check_trimul(z, pm, tri.tri_mul_out, wq["tri_mul_out"], "outgoing", pos, f"{tag} tri-mul out")
@@ -153,16 +175,16 @@ def run_layer_checked(n: int, n_real: int, seed: int, tag: str, z: torch.Tensor 
     z, pb = kernels.transition(z_in, layer.transition_z, residual=z_in, pair_bias_for=layer.attention)
     rows_in = gather(z_in, pos)
     want = rows_in + O.transition(rows_in, wq["transition_z"])
-    check_rows(gather(z, pos), want, f"{tag} pair transition")
+    check_rows(gather(z, pos), want, f"{tag} pair transition", **b)
     att = wq["attention"]
     want_pb = O.pair_bias_at(att, Lines(z), pos)  # [P, H], from the GPU's transition output
     idx = torch.tensor(pos, device="cuda", dtype=torch.long)
     got_pb = (pb[0][:, idx[:, 0], idx[:, 1]].float().cpu().numpy().astype(np.float64).T) / LOG2E
-    check_rows(got_pb, want_pb, f"{tag} prepared pair bias")
+    check_rows(got_pb, want_pb, f"{tag} prepared pair bias", **b)
 
     say(f"{tag}: single attention with pair bias")
     s_in = s
-    s = kernels.single_attention(s_in, None, torch.from_numpy(tm).to("cuda", BF16), layer.attention,
+    s = kernels.single_attention(s_in, None, torch.from_numpy(tm).to("cuda", dtype), layer.attention,
                                  residual=s_in, pair_bias=pb)
     s_np = s_in.float().cpu().numpy().astype(np.float64)
     s_ln = O.layer_norm(s_np, att["pre_norm_s"]["weight"], att["pre_norm_s"]["bias"])
@@ -170,14 +192,14 @@ def run_layer_checked(n: int, n_real: int, seed: int, tag: str, z: torch.Tensor 
     want_s = s_np[queries] + O.boltz2_attention_pair_bias_at(att, s_ln, Lines(z), tm, queries)
     got_s = s.float().cpu().numpy().astype(np.float64)
     # padded queries see the same keys; their rows are part of the output too
-    check_rows(got_s[queries], want_s, f"{tag} single attention")
+    check_rows(got_s[queries], want_s, f"{tag} single attention", **b)
 
     say(f"{tag}: single transition")
     s_in = s
     s = kernels.transition(s_in, layer.transition_s, residual=s_in)
     s_np = s_in.float().cpu().numpy().astype(np.float64)
     check_rows(s.float().cpu().numpy().astype(np.float64), s_np + O.transition(s_np, wq["transition_s"]),
-               f"{tag} single transition")
+               f"{tag} single transition", **b)
     torch.cuda.synchronize()
     return s, z
 
@@ -265,6 +287,17 @@ def test_config3_block_fp32_single_track_n1024():
     fs, fz = layer.forward(s0, z0, tm, pm)
     torch.cuda.synchronize()
     assert torch.equal(fz, z1) and torch.equal(fs, s2), "layer.forward differs from the checked sublayer run"
+
+
+def test_fp32_block_sublayers_n512():
+    """fp32 mode at a multi-tile size: a whole layer with both tracks in
+    float32 at N=512 (490 real tokens: a padded tail), every sublayer and the
+    prepared pair bias checked at sampled positions to the north star's fp32
+    bar, max-abs 1e-4 against the float64 oracle. The fp32 paths run other
+    kernels than the bf16 ones at these sizes (the fp32 contraction over 2 x 2
+    tiles of 256, the fp32 flash kernels over several query tiles and key
+    blocks, the fp32 transition with its fp32 pair-bias epilogue)."""
+    run_layer_checked(512, 490, seed=11, tag="fp32 n512", dtype=torch.float32)
 
 
 def test_config4_layer_n2048():
