@@ -137,6 +137,7 @@ def check_triattn(z, mask_np, w, wq, starting, pos, what):
     zl = Lines(z)
     want = O.triangle_attention_at(zl, mask_np, wq, num_heads=4, starting=starting, positions=pos)
     opos = pos if starting else [(q, i) for i, q in pos]  # output index of grid entry (i, q)
+    assert bool(torch.isfinite(upd).all()), f"{what}: non-finite update (fully masked rows included)"
     check_rows(gather(upd, opos), want, f"{what} update", **bar(z.dtype))
     check_rows(gather(out, opos), gather(z, opos) + want, f"{what} z+update", **bar(z.dtype))
     return out
