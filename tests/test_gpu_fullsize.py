@@ -290,15 +290,17 @@ def test_config3_block_fp32_single_track_n1024():
     assert torch.equal(fz, z1) and torch.equal(fs, s2), "layer.forward differs from the checked sublayer run"
 
 
-def test_fp32_block_sublayers_n512():
-    """fp32 mode at a multi-tile size: a whole layer with both tracks in
-    float32 at N=512 (490 real tokens: a padded tail), every sublayer and the
-    prepared pair bias checked at sampled positions to the north star's fp32
-    bar, max-abs 1e-4 against the float64 oracle. The fp32 paths run other
-    kernels than the bf16 ones at these sizes (the fp32 contraction over 2 x 2
-    tiles of 256, the fp32 flash kernels over several query tiles and key
-    blocks, the fp32 transition with its fp32 pair-bias epilogue)."""
-    run_layer_checked(512, 490, seed=11, tag="fp32 n512", dtype=torch.float32)
+@pytest.mark.parametrize("n,n_real", [(512, 490), (1024, 973)])
+def test_fp32_block_sublayers(n, n_real):
+    """fp32 mode at multi-tile sizes: a whole layer with both tracks in
+    float32 at N=512 (490 real tokens) and at the headline N=1024 (973), every
+    sublayer and the prepared pair bias checked at sampled positions to the
+    north star's fp32 bar, max-abs 1e-4 against the float64 oracle. The fp32
+    paths run other kernels than the bf16 ones at these sizes (the fp32
+    contraction over 2 x 2 and 4 x 4 tiles of 256, the fp32 flash kernels
+    over several query tiles and key blocks, the fp32 transition with its
+    fp32 pair-bias epilogue)."""
+    run_layer_checked(n, n_real, seed=11, tag=f"fp32 n{n}", dtype=torch.float32)
 
 
 def test_config4_layer_n2048():
