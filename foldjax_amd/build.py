@@ -43,11 +43,17 @@ def _hipcc() -> str:
 # (the softmax reads the scores, and the offset kernel rescales the outputs,
 # every block) and never produce NaNs on purpose, so max() needs no NaN
 # canonicalisation; the row-projection kernels read their accumulators in
-# the epilogue arithmetic as well
+# the epilogue arithmetic as well. LLVM's machine scheduler runs its
+# ILP-oriented strategies on two files, each measured against the default
+# (rocprofv3 / in-process events, N=1024): the pipelined flash pass 2-3 %
+# faster with max-ilp, the row kernels' tri-mul epilogue 4 % and tri-attn
+# epilogue 1 % faster with iterative-ilp (the prologues unchanged); the other
+# files measured no better or slower with either.
 FILE_FLAGS = {
     "fjx_flash.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-    "fjx_rowproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-    "fjx_flash_pipe.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "fjx_rowproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "fjx_flash_pipe.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm",
+                           "-amdgpu-sched-strategy=max-ilp"],
 }
 
 
