@@ -47,9 +47,11 @@ def _hipcc() -> str:
 # ILP-oriented strategies on two files, each measured against the default
 # (rocprofv3 / in-process events, N=1024): the pipelined flash pass 2-3 %
 # faster with max-ilp, the row kernels' tri-mul epilogue 4 % and tri-attn
-# epilogue 1 % faster with iterative-ilp (the prologues unchanged); the other
-# files measured no better or slower with either.
+# epilogue 1 % faster with iterative-ilp (the prologues unchanged), the single
+# attention's flash kernel 27 % faster with iterative-ilp; the other files
+# measured no better or slower with either.
 FILE_FLAGS = {
+    "fjx_single_flash.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "fjx_flash.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "fjx_rowproj.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "fjx_flash_pipe.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-mfma-vgpr-form=1", "-mllvm",
