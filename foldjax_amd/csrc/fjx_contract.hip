@@ -38,11 +38,14 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t w, int64_t total) {
 }
 
 // BM x BM output tile per 256-thread workgroup (BM = 128, or 64 for small
-// problems that would otherwise leave most CUs idle), 2 x 2 waves of
-// (BM/2) x (BM/2).
+// problems that would otherwise leave most CUs idle, or 32 for small fp32
+// problems), 2 x 2 waves of (BM/2) x (BM/2). The 32-wide tile stages k-tiles
+// of 64 so that each of the 256 threads still fills one 8-element chunk per
+// operand; the k order of every accumulation is the same for all three tile
+// sizes, so they give bit-identical results.
 template <typename T, typename TO, int kBM>
 __global__ __launch_bounds__(256) void gemm_nt_kernel(GemmParams<T, TO> P) {
-  constexpr int BK = GemmCfg<T>::BK;
+  constexpr int BK = kBM == 32 ? 64 : GemmCfg<T>::BK;
   constexpr int LD = BK + 8;                  // padded LDS row (elements)
   constexpr int CHUNKS = kBM * BK / 8;        // 8-element chunks per operand tile
   constexpr int PER_T = CHUNKS / 256;         // chunks per thread per operand
@@ -546,9 +549,16 @@ void launch_gemm(const GemmParams<T, TO>& p, hipStream_t st) {
     if (launch_gemm_dma(p, st)) return;
   }
   auto tiles = [&](int64_t bm) { return p.batches * ((p.m + bm - 1) / bm) * ((p.n + bm - 1) / bm); };
-  // 128-wide tiles unless they would leave most of the 256 CUs idle
+  // 128-wide tiles unless they would leave most of the 256 CUs idle. fp32
+  // problems of fewer than four 64-wide tiles per CU (the single track's
+  // projections: 384 tiles at 1024 tokens, so half the SIMDs would run two
+  // waves and half one) take 32-wide tiles, which spread them evenly at
+  // several waves per SIMD; fp32 MFMAs are slow enough that the smaller
+  // tile's extra LDS reads stay far below the LDS rate.
   if (tiles(128) >= 512)
     hipLaunchKernelGGL((gemm_nt_kernel<T, TO, 128>), dim3((unsigned)tiles(128)), dim3(256), 0, st, p);
+  else if (std::is_same<T, float>::value && tiles(64) < 1024)
+    hipLaunchKernelGGL((gemm_nt_kernel<T, TO, 32>), dim3((unsigned)tiles(32)), dim3(256), 0, st, p);
   else
     hipLaunchKernelGGL((gemm_nt_kernel<T, TO, 64>), dim3((unsigned)tiles(64)), dim3(256), 0, st, p);
 }
