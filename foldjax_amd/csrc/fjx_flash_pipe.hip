@@ -161,10 +161,16 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
           16, dma_off[j & 1], (uint32_t)(blk * kPKB * 2 + (j >> 1) * 16 * np * 2), 0, 0);
   };
 
-  // Q of the wave's tiles, in registers for the whole row
+  // Q of the wave's tiles, in registers for the whole row; loaded through a
+  // buffer descriptor at the workgroup's first query with 32-bit lane
+  // offsets, so that no 64-bit query index is formed here and kept (spilled
+  // to scratch, whose stores and reloads reached HBM) until the output
+  // stores after the key loop
+  const __amdgpu_buffer_rsrc_t rq = buf_rsrc(Q + q0 * kPD, (uint32_t)(kPQwg * kPD * 2));
   bf16x8 qreg[NQT];
 #pragma unroll
-  for (int qt = 0; qt < NQT; ++qt) qreg[qt] = load8(Q + (q0 + qw + 16 * qt + li) * kPD + 8 * lg);
+  for (int qt = 0; qt < NQT; ++qt)
+    qreg[qt] = buf_load8(rq, (uint32_t)((qw + 16 * qt + li) * kPD * 2 + 16 * lg), 0);
 
   bf16x8 kf[2][4];     // K of two blocks
   bf16x8 vf[2][2][2];  // V^T of two blocks: [set][dt][32-key chunk]
@@ -400,7 +406,7 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   // it dims 8g .. 8g+7 instead, so each query's 64 bytes leave as four
   // 16-byte stores of one instruction: whole cache lines, not 8-byte pieces
   // written by two instructions.
-  bf16* OUT = P.out + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head;
+  bf16* OUT = P.out + b * P.o_stride_b + i * P.o_stride_row + h * P.o_stride_head + q0 * P.o_stride_q;
   auto pack2 = [](float x, float y) {
     return (uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(x)) |
            ((uint32_t)__builtin_bit_cast(uint16_t, static_cast<bf16>(y)) << 16);
@@ -409,7 +415,7 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
   for (int qt = 0; qt < NQT; ++qt) {
     const float ls = __shfl(lsum[qt >> 2][0], 16 * (qt & 3) + li, 64);
     const float inv = 1.0f / ls;
-    const int64_t q = q0 + qw + 16 * qt + li;
+    const int ql = qw + 16 * qt + li;  // query q0 + ql
     uint32_t a[2], c[2];  // a: dims 4g .., c: dims 16 + 4g ..
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
@@ -425,7 +431,7 @@ void flash_pipe_kernel_bf16(FlashParams<bf16> P) {
       a[e] = s16[0];  // dims 8g .. 8g+3
       c[e] = s16[1];  // dims 8g+4 .. 8g+7
     }
-    if (q < n) *reinterpret_cast<u32x4*>(OUT + q * P.o_stride_q + 8 * lg) = u32x4{a[0], a[1], c[0], c[1]};
+    if (q0 + ql < n) *reinterpret_cast<u32x4*>(OUT + ql * P.o_stride_q + 8 * lg) = u32x4{a[0], a[1], c[0], c[1]};
   }
 }
 
