@@ -270,7 +270,9 @@ def hbm_bytes_per_launch(n: int, single_dtype) -> dict:
 
 
 MIXES = {0: "flash tile: 10 MFMA + 16 exp + 24 VALU", 1: "without the bias widenings: 10 MFMA + 16 exp + 8 VALU",
-         2: "10 MFMA alone", 3: "16 exp alone", 4: "24 VALU alone"}
+         2: "10 MFMA alone", 3: "16 exp alone", 4: "24 VALU alone",
+         5: "the flash tile on 32x32x16 MFMAs: 4 x 32x32x16 + 2 x 16x16x32 + 16 exp + 24 VALU",
+         6: "4 x 32x32x16 + 2 x 16x16x32 MFMA alone"}
 
 
 def mix_probe(n: int) -> dict:

@@ -1230,8 +1230,8 @@ int fjx_prof_collect(void) {
 
 int fjx_probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream_t st) {
   g_err.clear();
-  if (mix < 0 || mix > 4 || waves_per_simd < 1 || waves_per_simd > 4 || iters < 1 || !ms)
-    return fail(FJX_ERR_INVALID, "fjx_probe_issue_mix: mix 0..4, 1..4 waves per SIMD, iters >= 1, ms non-NULL");
+  if (mix < 0 || mix > 6 || waves_per_simd < 1 || waves_per_simd > 4 || iters < 1 || !ms)
+    return fail(FJX_ERR_INVALID, "fjx_probe_issue_mix: mix 0..6, 1..4 waves per SIMD, iters >= 1, ms non-NULL");
   if (fjx::probe_issue_mix(mix, waves_per_simd, iters, ms, st) != 0)
     return fail(FJX_ERR_HIP, "fjx_probe_issue_mix: a HIP call failed");
   return FJX_OK;

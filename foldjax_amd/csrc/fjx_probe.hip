@@ -12,7 +12,11 @@
 //
 // Mixes: 0 = the kernel's (10 MFMA + 16 exp + 24 VALU), 1 = without the bias
 // widenings (10 MFMA + 16 exp + 8 VALU), 2 = the 10 MFMAs alone, 3 = the 16
-// exponentials alone, 4 = the 24 VALU alone.
+// exponentials alone, 4 = the 24 VALU alone; 5 = the same tile's scores and
+// products on v_mfma_f32_32x32x16_bf16 (4 of them carry the matrix-pipe work
+// of the 8 16x16x32 ones; the 2 row-sum MFMAs stay 16x16x32) with the same
+// 16 exp + 24 VALU, 6 = those 6 MFMAs alone: whether the issue floor depends
+// on the number of MFMA instructions or only on their matrix-pipe cycles.
 //
 // A second probe streams 16-byte accesses through HBM (copy, nontemporal
 // copy, read only, write only) at a chosen number of workgroups per CU: the
@@ -25,6 +29,8 @@
 
 namespace fjx {
 namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));  // a 32x32 MFMA accumulator
 
 #define FJX_M(i) "v_mfma_f32_16x16x32_bf16 %" #i ", %34, %35, %" #i "\n"
 #define FJX_E(j) "v_exp_f32 %" #j ", %36\n"
@@ -113,6 +119,75 @@ __global__ __launch_bounds__(256) void issue_mix_kernel(float* sink, int iters) 
 #undef FJX_V
 #undef FJX_OPS
 
+// mixes 5 and 6: %0, %1 the 16x16x32 accumulators, %2..%5 the 32x32x16 ones
+// (f32x16), %6..%21 exponential results, %22..%29 VALU chains, %30 / %31 the
+// MFMA fragments, %32 the exponentials' argument
+#define FJX_M16(i) "v_mfma_f32_16x16x32_bf16 %" #i ", %30, %31, %" #i "\n"
+#define FJX_M32(i) "v_mfma_f32_32x32x16_bf16 %" #i ", %30, %31, %" #i "\n"
+#define FJX_E(j) "v_exp_f32 %" #j ", %32\n"
+#define FJX_V(j) "v_fma_f32 %" #j ", %" #j ", 0.5, 1.0\n"
+#define FJX_OPS32                                                                                         \
+  "+v"(c[0]), "+v"(c[1]), "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]), "+v"(e[0]), "+v"(e[1]),         \
+      "+v"(e[2]), "+v"(e[3]), "+v"(e[4]), "+v"(e[5]), "+v"(e[6]), "+v"(e[7]), "+v"(e[8]), "+v"(e[9]),     \
+      "+v"(e[10]), "+v"(e[11]), "+v"(e[12]), "+v"(e[13]), "+v"(e[14]), "+v"(e[15]), "+v"(x[0]), "+v"(x[1]), \
+      "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7])                              \
+  : "v"(fa), "v"(fb), "v"(xe)
+
+template <int MIX>
+__global__ __launch_bounds__(256) void issue_mix32_kernel(float* sink, int iters) {
+  f32x4 c[2];
+  f32x16 d[4];
+  float e[16], x[8];
+  bf16x8 fa, fb;
+  const float t = 1e-3f * (float)threadIdx.x;
+  const float xe = -0.75f - t;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) c[i] = f32x4{t, t, t, t};
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int k = 0; k < 16; ++k) d[i][k] = t;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) e[j] = -0.01f * (float)j;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = t + (float)j;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    fa[k] = static_cast<bf16>(0.001f * (float)k);
+    fb[k] = static_cast<bf16>(t);
+  }
+  for (int it = 0; it < iters; ++it) {
+    if constexpr (MIX == 5) {
+      // each 32x32x16 MFMA (32 cycles) followed by the VALU work two 16x16x32
+      // ones (16 cycles each) carry in mix 0
+      asm volatile(FJX_M32(2) FJX_E(6) FJX_E(7) FJX_V(22) FJX_V(23) FJX_V(24) FJX_E(8) FJX_E(9) FJX_V(25) FJX_V(26) FJX_V(27)
+                   FJX_M32(3) FJX_E(10) FJX_E(11) FJX_V(28) FJX_V(29) FJX_E(12) FJX_E(13) FJX_V(22) FJX_V(23) FJX_V(24)
+                   FJX_M16(0) FJX_E(14) FJX_E(15) FJX_V(25) FJX_V(26)
+                   FJX_M32(4) FJX_E(16) FJX_E(17) FJX_V(27) FJX_V(28) FJX_V(29) FJX_E(18) FJX_E(19) FJX_V(22) FJX_V(23)
+                   FJX_M32(5) FJX_E(20) FJX_E(21) FJX_V(24) FJX_V(25) FJX_V(26)
+                   FJX_M16(1) FJX_V(27) FJX_V(28) FJX_V(29)
+                   : FJX_OPS32);
+    } else {
+      asm volatile(FJX_M32(2) FJX_M32(3) FJX_M16(0) FJX_M32(4) FJX_M32(5) FJX_M16(1) : FJX_OPS32);
+    }
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) s += c[i][0] + c[i][3];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s += d[i][0] + d[i][15];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s += e[j];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s += x[j];
+  sink[(int64_t)blockIdx.x * 256 + threadIdx.x] = s;
+}
+#undef FJX_M16
+#undef FJX_M32
+#undef FJX_E
+#undef FJX_V
+#undef FJX_OPS32
+
 // HBM streaming probe: 16-byte accesses over two device buffers, a
 // grid-stride loop of gridDim.x 256-thread workgroups, four accesses in
 // flight per lane. Mode 0 copies a -> b, mode 1 copies with nontemporal
@@ -165,7 +240,9 @@ int probe_issue_mix(int mix, int waves_per_simd, int iters, float* ms, hipStream
       case 1: hipLaunchKernelGGL(issue_mix_kernel<1>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
       case 2: hipLaunchKernelGGL(issue_mix_kernel<2>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
       case 3: hipLaunchKernelGGL(issue_mix_kernel<3>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
-      default: hipLaunchKernelGGL(issue_mix_kernel<4>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      case 4: hipLaunchKernelGGL(issue_mix_kernel<4>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      case 5: hipLaunchKernelGGL(issue_mix32_kernel<5>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
+      default: hipLaunchKernelGGL(issue_mix32_kernel<6>, dim3(blocks), dim3(256), 0, st, sink, iters); break;
     }
   };
   launch();  // warm-up: the clock settles under load

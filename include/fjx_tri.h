@@ -366,7 +366,9 @@ int fjx_prof_read(int id, double* total_ms, int64_t* launches);
  * issues the mix (0: 10 v_mfma_f32_16x16x32_bf16 + 16 v_exp_f32 + 24 other
  * VALU, the pipelined flash pass's instructions per 16 x 64 tile and wave;
  * 1: the same without the 16 bias widenings; 2: the MFMAs alone; 3: the
- * exponentials alone; 4: the 24 VALU alone) `iters` times in every wave,
+ * exponentials alone; 4: the 24 VALU alone; 5: mix 0 with its 8 score and
+ * product MFMAs as 4 v_mfma_f32_32x32x16_bf16 (the same matrix-pipe cycles
+ * in half the instructions); 6: those 6 MFMAs alone) `iters` times in every wave,
  * waves_per_simd (1-4) waves on each SIMD of the device, no memory traffic,
  * and returns its time in *ms (HIP events on `stream`; the call waits for
  * them). One SIMD issues one tile's mix in ms / (iters * waves_per_simd).

@@ -16,12 +16,13 @@ pytestmark = pytest.mark.gpu
 
 def test_issue_mix_probe_times():
     say("issue mix probe")
-    t = {mix: _lib.probe_issue_mix(mix, 2, 400) for mix in range(5)}
+    t = {mix: _lib.probe_issue_mix(mix, 2, 400) for mix in range(7)}
     assert all(v > 0 for v in t.values()), t
     assert _lib.probe_issue_mix(2, 2, 1600) > 2.0 * t[2]
     assert t[0] >= 0.9 * max(t[2], t[3]), t  # the full mix contains the MFMAs and the exponentials
+    assert t[5] >= 0.9 * max(t[6], t[3]), t  # so does its 32x32x16 form
     with pytest.raises(ValueError):
-        _lib.probe_issue_mix(5, 2, 10)
+        _lib.probe_issue_mix(7, 2, 10)
 
 
 def test_hbm_stream_probe_rates():
