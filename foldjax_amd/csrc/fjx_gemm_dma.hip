@@ -114,13 +114,18 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmParams<bf16, bf16> P)
   // stage st <- k-tile kt of tile tl (st a compile-time constant at every call)
   auto issue = [&](const Tile& tl, int64_t kt, int st) {
     const int64_t k0 = kt * kGDK;
-    // the k offset and the uniform row offset go in the scalar offset; a
-    // lane whose chunk lies past K reads from past the resource's end
-    const bool in0 = k0 + kc[0] < K, in1 = k0 + kc[1] < K;
-    // opaque here, so the sums below are formed per call rather than hoisted
-    // into loop-invariant registers (which would spill)
+    // opaque here, so the sums and compares below are formed per call rather
+    // than hoisted into loop-invariant registers, which spilled: the reload of
+    // a spilled 64-bit k offset waited (vmcnt counts in issue order) for the
+    // next stage's DMA issued just before it, in every k-step
 #pragma unroll
-    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(aoff[j]), "+v"(boff[j]));
+    for (int j = 0; j < 2; ++j) asm volatile("" : "+v"(aoff[j]), "+v"(boff[j]), "+v"(kc[j]));
+    // the k offset and the uniform row offset go in the scalar offset; a
+    // lane whose chunk lies past K reads from past the resource's end. The
+    // tail test in 32 bits against the uniform remaining depth (at least 1;
+    // clamped, a chunk offset is below 64)
+    const int krem = (int)min<int64_t>(K - k0, (int64_t)1 << 30);
+    const bool in0 = kc[0] < krem, in1 = kc[1] < krem;
 #pragma unroll
     for (int j = 0; j < kGNI; ++j) {
       const bool kin = (j & 1) ? in1 : in0;
